@@ -1,0 +1,193 @@
+#!/usr/bin/env python3
+"""FP32 GEMM throughput of the flash-train MI355X path (one GPU).
+
+A step is one execution of a cached Plan (ftrainPlanExecutePrimitive, primitive
+0) on the headline BASELINE workload, m = n = k = 8192, a, b ~ U(-1, 1) from a
+CPU torch.Generator seeded 2026, alpha 1, beta 0, no c; inputs are resident in
+HBM before timing.  Prints ONE JSON line (rank 0) with the metric, the
+roofline of the dominant kernel, the cached-Plan host overhead, and a CPU
+baseline.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import subprocess
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG_ROOT = os.path.join(REPO, "flash-train_amd")
+for _p in (PKG_ROOT, REPO):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+FP32_MATRIX_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix (AMD spec)
+HBM_PEAK_GBS = 8000.0
+METRIC = "FP32 GEMM TFLOP/s and % of MFMA FP32 peak at 8192³; µs/call on cached Plan"
+
+
+def log(*a) -> None:
+    print(*a, file=sys.stderr, flush=True)
+
+
+def plan_overhead() -> dict | None:
+    """Runs the C++ probe (separate process) on BASELINE config 5e (127, 97, 33)."""
+    exe = os.path.join(PKG_ROOT, "bench", "plan_overhead")
+    if not os.path.exists(exe):
+        return None
+    try:
+        out = subprocess.run([exe, "127", "97", "33", "10000"], capture_output=True, text=True, timeout=120)
+        return json.loads(out.stdout.strip().splitlines()[-1]) if out.returncode == 0 else {"error": out.stderr[-400:]}
+    except Exception as e:  # report, do not fail the bench
+        return {"error": str(e)}
+
+
+def traffic_from_profiles(kernel: str) -> float | None:
+    """HBM bytes per launch for `kernel`, from the committed rocprofv3 PMC summary (if any)."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel, {}).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(a, b, alpha: float, beta: float, budget_s: float) -> dict:
+    """The oracle's restatement of the reference kernel (fp32, in-order k sum), on a row sample."""
+    from oracle import oracle
+
+    import numpy as np
+
+    k = a.shape[1]
+    n = b.shape[1]
+    a_np, b_np = a.numpy(), b.numpy()
+    rows = 4
+    t0 = time.perf_counter()
+    oracle.gemm_ref(a_np[:rows], b_np, None, alpha, beta)
+    dt = max(time.perf_counter() - t0, 1e-6)
+    rows = int(min(a.shape[0], max(rows, rows * budget_s / dt)))
+    t0 = time.perf_counter()
+    oracle.gemm_ref(a_np[:rows], b_np, None, alpha, beta)
+    dt = time.perf_counter() - t0
+    tflops = 2.0 * rows * n * k / dt / 1e12
+    return {"value": round(tflops, 5), "unit": "TFLOP/s", "cores": oracle.threads(), "kind": "port",
+            "sample": f"{rows} of {a.shape[0]} rows of the workload ({rows}x{n}x{k}), {dt:.1f} s, "
+                      f"oracle/gemm_oracle.c ft_oracle_gemm_ref with OpenMP"}
+
+
+def torch_cpu_matmul(a, b, budget_s: float) -> dict:
+    import torch
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    rows = 256
+    t0 = time.perf_counter()
+    torch.matmul(a[:rows], b)
+    dt = max(time.perf_counter() - t0, 1e-6)
+    rows = int(min(a.shape[0], max(rows, rows * budget_s / dt)))
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        torch.matmul(a[:rows], b)
+        times.append(time.perf_counter() - t0)
+    dt = sorted(times)[1]
+    return {"value": round(2.0 * rows * b.shape[1] * a.shape[1] / dt / 1e12, 4), "unit": "TFLOP/s",
+            "cores": torch.get_num_threads(), "sample": f"{rows}x{b.shape[1]}x{a.shape[1]}, median of 3"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="square_8192")
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build runs the GEMM path on a single MI355X "
+              "(see DESIGN.md for how it would shard); use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import flash_train.capi as capi
+    from oracle import oracle
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    a_h, b_h, c_h, cfg = oracle.seeded_inputs(args.workload)
+    m, n, k = cfg["m"], cfg["n"], cfg["k"]
+    a, b = a_h.cuda(), b_h.cuda()
+    c = c_h.cuda() if c_h is not None else None
+    d = torch.empty(m, n, device="cuda")
+    stream = torch.cuda.Stream()
+    plan = capi.plan_for(a, b, c, d, cfg["alpha"], cfg["beta"])
+    name = plan.name(0)
+    log(f"workload {args.workload} ({m}x{n}x{k}); primitive 0 = {name}; plan = {plan.names()}")
+
+    h = stream.cuda_stream
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            plan.execute(0, h)
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record(stream)
+        for _ in range(args.steps):
+            plan.execute(0, h)
+        stop.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    ms = start.elapsed_time(stop) / args.steps
+
+    # Parity spot check of the benchmarked output (64 sampled rows, fp64).
+    import numpy as np
+
+    rows = np.sort(np.random.default_rng(1).choice(m, size=min(64, m), replace=False))
+    ref = oracle.sampled_rows_f64(a_h, b_h, c_h, cfg["alpha"], cfg["beta"], rows)
+    rep = oracle.tolerance_check(d[torch.as_tensor(rows).cuda()].cpu().numpy(), ref, k)
+
+    flops = 2.0 * m * n * k
+    tflops = flops / (ms * 1e-3) / 1e12
+    alg_bytes = 4.0 * (m * k + k * n + m * n * (2 if c is not None else 1))
+    overhead = plan_overhead()
+
+    result = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded CPU torch.Generator 2026, U(-1,1) for 8192^3)",
+        "config": {"workload": args.workload, "m": m, "n": n, "k": k, "alpha": cfg["alpha"], "beta": cfg["beta"],
+                   "c": c is not None, "primitive": name, "parallelism": "single GPU"},
+        "pct_of_fp32_matrix_peak": round(100.0 * tflops / FP32_MATRIX_PEAK_TFLOPS, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": FP32_MATRIX_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / FP32_MATRIX_PEAK_TFLOPS, 4),
+                     "traffic": traffic_from_profiles(name), "algorithmic_bytes": alg_bytes,
+                     "kernel_ms": round(ms, 4)},
+        "plan_overhead": overhead,
+        "parity": {"rows_checked": int(len(rows)), "max_abs_err": rep["max_abs_err"], "bound": rep["bound"],
+                   "ok": rep["ok"]},
+        "wall_s_timed": round(wall, 3),
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(a_h, b_h, cfg["alpha"], cfg["beta"], args.cpu_budget)
+        result["cpu_torch_matmul"] = torch_cpu_matmul(a_h, b_h, min(args.cpu_budget, 5.0))
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,143 @@
+#!/usr/bin/env python3
+"""Builds flash-train for MI355X in-tree with hipcc (gfx950).
+
+Outputs (all git-ignored, all shipped to the GPU box with the tree):
+  flash_train/libflash_train.so           the C-ABI library (exports the ftrain* API only)
+  flash_train/libflash_train_testing.so   same objects plus host-only test hooks
+  flash_train/torch/_flash_train_torch*.so the flash_train.torch.gemm binding
+  bench/plan_overhead                     C++ host-overhead probe used by bench.py
+
+Usage: python build.py [--jobs N] [--no-torch]
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures
+import os
+import subprocess
+import sys
+import sysconfig
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+BUILD = os.path.join(HERE, "_build")
+PKG = os.path.join(HERE, "flash_train")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+ARCH = "gfx950"
+
+COMMON = [
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-fvisibility-inlines-hidden",
+    "-Wall",
+    "-Wno-unused-function",
+    f"-I{os.path.join(HERE, 'csrc', 'include')}",
+    f"-I{os.path.join(REPO, 'include')}",
+]
+# Device code: gfx950 only, and no packed-FP32 instructions.
+DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+LIB_SOURCES = [
+    "csrc/runtime/error.cpp",
+    "csrc/runtime/values.cpp",
+    "csrc/runtime/pattern.cpp",
+    "csrc/runtime/cache.cpp",
+    "csrc/runtime/plan.cpp",
+    "csrc/runtime/handle.cpp",
+    "csrc/runtime/trace.cpp",
+    "csrc/gemm/catalog.cpp",
+    "csrc/gemm/problem.cpp",
+    "csrc/gemm/finder.cpp",
+    "csrc/gemm/primitives.cpp",
+    "csrc/gemm/kernels.hip",
+    "csrc/api/c_api.cpp",
+]
+TESTING_SOURCES = ["csrc/api/testing_api.cpp"]
+
+
+def run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(" ".join(cmd) + "\n" + proc.stdout)
+        raise SystemExit(f"build step failed: {cmd[-1]}")
+
+
+def obj_path(src: str) -> str:
+    return os.path.join(BUILD, src.replace("/", "_") + ".o")
+
+
+def compile_one(src: str) -> str:
+    out = obj_path(src)
+    cmd = [HIPCC, *COMMON]
+    if src.endswith(".hip"):
+        cmd += ["-x", "hip", *DEVICE]
+    cmd += ["-c", os.path.join(HERE, src), "-o", out]
+    run(cmd)
+    return out
+
+
+def link_shared(objs: list[str], out: str, soname: str) -> None:
+    # Export the ftrain* C entry points only; library-internal and C++
+    # standard-library template symbols stay local.
+    script = os.path.join(BUILD, "exports.map")
+    with open(script, "w") as f:
+        f.write("{ global: ftrain*; local: *; };\n")
+    run([HIPCC, f"-Wl,--version-script={script}", "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", out,
+         f"-Wl,-soname,{soname}", f"-L{ROCM}/lib", "-lroctx64", f"-Wl,-rpath,{ROCM}/lib", "-Wl,--no-undefined"])
+
+
+def torch_flags() -> tuple[list[str], list[str]]:
+    import torch.utils.cpp_extension as ce  # imported lazily: only the binding needs torch
+
+    inc = [f"-I{p}" for p in ce.include_paths()] + [f"-I{sysconfig.get_paths()['include']}"]
+    libdirs = ce.library_paths()
+    abi = "1" if __import__("torch")._C._GLIBCXX_USE_CXX11_ABI else "0"
+    cflags = inc + ["-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+                    "-DTORCH_API_INCLUDE_EXTENSION_H", "-DTORCH_EXTENSION_NAME=_flash_train_torch",
+                    "-Wno-unused-result", "-Wno-deprecated-declarations"]
+    ldflags = [f"-L{d}" for d in libdirs] + [f"-Wl,-rpath,{d}" for d in libdirs] + [
+        "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python"]
+    return cflags, ldflags
+
+
+def build_torch_binding() -> None:
+    cflags, ldflags = torch_flags()
+    src = os.path.join(PKG, "torch", "csrc", "flash_train_torch.cpp")
+    obj = os.path.join(BUILD, "flash_train_torch.o")
+    run([HIPCC, *COMMON, *cflags, "-c", src, "-o", obj])
+    suffix = sysconfig.get_config_var("EXT_SUFFIX")
+    out = os.path.join(PKG, "torch", "_flash_train_torch" + suffix)
+    run([HIPCC, "-shared", "-fPIC", obj, "-o", out, f"-L{PKG}", "-lflash_train", "-Wl,-rpath,$ORIGIN/..",
+         *ldflags, f"-L{ROCM}/lib"])
+
+
+def build_plan_overhead() -> None:
+    os.makedirs(os.path.join(HERE, "bench"), exist_ok=True)
+    src = os.path.join(HERE, "bench", "plan_overhead.cpp")
+    out = os.path.join(HERE, "bench", "plan_overhead")
+    run([HIPCC, "-O2", "-std=c++17", f"-I{os.path.join(REPO, 'include')}", src, "-o", out, f"-L{PKG}",
+         "-lflash_train", f"-Wl,-rpath,{PKG}", f"-Wl,-rpath,{ROCM}/lib"])
+
+
+def main(argv: list[str] | None = None) -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
+    ap.add_argument("--no-torch", action="store_true")
+    args = ap.parse_args(argv)
+    os.makedirs(BUILD, exist_ok=True)
+    with concurrent.futures.ThreadPoolExecutor(args.jobs) as pool:
+        lib_objs = list(pool.map(compile_one, LIB_SOURCES))
+        test_objs = list(pool.map(compile_one, TESTING_SOURCES))
+    link_shared(lib_objs, os.path.join(PKG, "libflash_train.so"), "libflash_train.so")
+    link_shared(lib_objs + test_objs, os.path.join(PKG, "libflash_train_testing.so"), "libflash_train_testing.so")
+    build_plan_overhead()
+    if not args.no_torch:
+        build_torch_binding()
+
+
+if __name__ == "__main__":
+    main()

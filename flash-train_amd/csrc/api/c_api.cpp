@@ -1,0 +1,335 @@
+// The exported C ABI: the 29 ftrain* entry points of the reference
+// (include/flash_train/common.h:162-589, include/flash_train/flash_train.h:46-48;
+// implementations src/api/{common,pattern,ops_args,plan,gemm}_api.cpp).
+//
+// Each entry point runs its body through `guarded`, which maps exceptions to
+// status codes (Exception -> its status, bad_alloc -> OUT_OF_MEMORY, any
+// other exception -> INTERNAL_ERROR) and records the status and message as
+// the thread's last result (reference src/include/flash_train/api.hpp:37-62).
+#include <exception>
+#include <new>
+#include <optional>
+#include <utility>
+
+#include <flash_train/flash_train.h>
+
+#include "ft/handles.hpp"
+#include "ft/trace.hpp"
+
+namespace ftrain {
+
+Result& lastResult() noexcept {
+    static thread_local Result r;
+    return r;
+}
+
+namespace {
+
+[[noreturn]] void invalid(const char* message) { throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "%s", message); }
+
+template <typename T>
+void requireNonNull(const T* p, const char* message) {
+    if (p == nullptr) invalid(message);
+}
+
+OpNode gemmNode(OperationKind kind, uint64_t a, uint64_t b, uint64_t c, uint64_t d, uint64_t alpha, uint64_t beta) {
+    return OpNode{kind, {a, b, c, alpha, beta}, {d}};
+}
+
+template <typename Id>
+FTrainStatus addOperand(FTrainPattern pattern, Id* out, OperandKind kind, const char* fn) {
+    return guarded([&] {
+        if (pattern == nullptr) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: pattern must not be null", fn);
+        if (out == nullptr) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: output must not be null", fn);
+        *out = Id{pattern->builder.addOperand(kind)};
+    });
+}
+
+template <typename Id>
+FTrainStatus addGemmLike(FTrainPattern pattern, Id* op, OperationKind kind, uint64_t a, uint64_t b, uint64_t c,
+                         uint64_t d, uint64_t alpha, uint64_t beta, const char* fn) {
+    return guarded([&] {
+        if (pattern == nullptr) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: pattern must not be null", fn);
+        if (op == nullptr) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: op output must not be null", fn);
+        *op = Id{pattern->builder.addOperation(gemmNode(kind, a, b, c, d, alpha, beta))};
+    });
+}
+
+FTrainStatus setOperation(FTrainArgs args, uint64_t op, OperationKind kind, FTrainNumericType compute_type,
+                          const char* fn) {
+    return guarded([&] {
+        if (args == nullptr) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: args handle must not be null", fn);
+        if (compute_type == FTRAIN_NUMERIC_TYPE_INVALID || compute_type >= FTRAIN_NUMERIC_TYPE_COUNT)
+            throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: compute_type %u is invalid", fn,
+                            unsigned(compute_type));
+        args->args.setOperation(op, OperationAttributes{kind, compute_type});
+    });
+}
+
+}  // namespace
+}  // namespace ftrain
+
+using namespace ftrain;
+
+extern "C" {
+
+FTrainStatus ftrainGetLastStatus(void) { return lastResult().getStatus(); }
+const char* ftrainGetLastMessage(void) { return lastResult().getMessage(); }
+
+// ---------------------------------------------------------------- Pattern
+
+FTrainStatus ftrainPatternCreate(FTrainPattern* pattern) {
+    return guarded([&] {
+        requireNonNull(pattern, "ftrainPatternCreate: pattern output must not be null");
+        *pattern = new FTrainPatternStruct();
+    });
+}
+
+FTrainStatus ftrainPatternDestroy(FTrainPattern pattern) {
+    return guarded([&] {
+        requireNonNull(pattern, "ftrainPatternDestroy: pattern must not be null");
+        delete pattern;
+    });
+}
+
+FTrainStatus ftrainPatternAddTensor(FTrainPattern pattern, FTrainTensorId* tensor) {
+    return addOperand(pattern, tensor, OperandKind::kTensor, "ftrainPatternAddTensor");
+}
+
+FTrainStatus ftrainPatternAddTensorList(FTrainPattern pattern, FTrainTensorListId* tensor_list) {
+    return addOperand(pattern, tensor_list, OperandKind::kTensorList, "ftrainPatternAddTensorList");
+}
+
+FTrainStatus ftrainPatternAddGroupedTensor(FTrainPattern pattern, FTrainGroupedTensorId* grouped_tensor) {
+    return addOperand(pattern, grouped_tensor, OperandKind::kGroupedTensor, "ftrainPatternAddGroupedTensor");
+}
+
+FTrainStatus ftrainPatternAddGemm(FTrainPattern pattern, FTrainGemmOpId* op, FTrainTensorId a, FTrainTensorId b,
+                                  FTrainTensorId c, FTrainTensorId d, FTrainTensorId alpha, FTrainTensorId beta) {
+    return addGemmLike(pattern, op, OperationKind::kGemm, a.opaque, b.opaque, c.opaque, d.opaque, alpha.opaque,
+                       beta.opaque, "ftrainPatternAddGemm");
+}
+
+FTrainStatus ftrainPatternAddGroupedABCDGemm(FTrainPattern pattern, FTrainGroupedABCDGemmOpId* op,
+                                             FTrainGroupedTensorId a, FTrainGroupedTensorId b, FTrainGroupedTensorId c,
+                                             FTrainGroupedTensorId d, FTrainTensorId alpha, FTrainTensorId beta) {
+    return addGemmLike(pattern, op, OperationKind::kGroupedABCDGemm, a.opaque, b.opaque, c.opaque, d.opaque,
+                       alpha.opaque, beta.opaque, "ftrainPatternAddGroupedABCDGemm");
+}
+
+FTrainStatus ftrainPatternAddGroupedBCDGemm(FTrainPattern pattern, FTrainGroupedBCDGemmOpId* op, FTrainTensorListId a,
+                                            FTrainGroupedTensorId b, FTrainGroupedTensorId c, FTrainGroupedTensorId d,
+                                            FTrainTensorId alpha, FTrainTensorId beta) {
+    return addGemmLike(pattern, op, OperationKind::kGroupedBCDGemm, a.opaque, b.opaque, c.opaque, d.opaque,
+                       alpha.opaque, beta.opaque, "ftrainPatternAddGroupedBCDGemm");
+}
+
+FTrainStatus ftrainPatternAddGroupedABGemm(FTrainPattern pattern, FTrainGroupedABGemmOpId* op, FTrainGroupedTensorId a,
+                                           FTrainGroupedTensorId b, FTrainTensorListId c, FTrainTensorListId d,
+                                           FTrainTensorId alpha, FTrainTensorId beta) {
+    return addGemmLike(pattern, op, OperationKind::kGroupedABGemm, a.opaque, b.opaque, c.opaque, d.opaque,
+                       alpha.opaque, beta.opaque, "ftrainPatternAddGroupedABGemm");
+}
+
+// ---------------------------------------------------------------- Ops
+
+FTrainStatus ftrainOpsCreate(FTrainOps* ops, FTrainPattern pattern) {
+    TraceRange trace("ftrainOpsCreate");
+    return guarded([&] {
+        requireNonNull(ops, "ftrainOpsCreate: ops output must not be null");
+        requireNonNull(pattern, "ftrainOpsCreate: pattern must not be null");
+        const Pattern user = pattern->builder.build();
+        const auto engine  = globalHandle().find(user.key());
+        if (!engine)
+            throw Exception(FTRAIN_STATUS_UNSUPPORTED,
+                            "ftrainOpsCreate: PatternBuilder does not match any registered OpsEngine");
+        *ops = new FTrainOpsStruct{Ops(user, engine->pattern())};
+    });
+}
+
+FTrainStatus ftrainOpsDestroy(FTrainOps ops) {
+    return guarded([&] {
+        requireNonNull(ops, "ftrainOpsDestroy: ops handle must not be null");
+        delete ops;
+    });
+}
+
+// ---------------------------------------------------------------- Args
+
+FTrainStatus ftrainArgsCreate(FTrainArgs* args, FTrainOps ops) {
+    TraceRange trace("ftrainArgsCreate");
+    return guarded([&] {
+        requireNonNull(args, "ftrainArgsCreate: args output must not be null");
+        requireNonNull(ops, "ftrainArgsCreate: ops handle must not be null");
+        *args = new FTrainArgsStruct{ops->ops.makeArgs()};
+    });
+}
+
+FTrainStatus ftrainArgsDestroy(FTrainArgs args) {
+    return guarded([&] {
+        requireNonNull(args, "ftrainArgsDestroy: args handle must not be null");
+        delete args;
+    });
+}
+
+FTrainStatus ftrainArgsSetTensor(FTrainArgs args, FTrainTensorId tensor, FTrainStorageView storage_view) {
+    return guarded([&] {
+        requireNonNull(args, "ftrainArgsSetTensor: args handle must not be null");
+        args->args.setOperand(tensor.opaque, OperandValue(Tensor{StorageView(storage_view)}));
+    });
+}
+
+FTrainStatus ftrainArgsSetTensorList(FTrainArgs args, FTrainTensorListId tensor_list,
+                                     const FTrainStorageView storage_views[], uint32_t num_storage_views) {
+    return guarded([&] {
+        requireNonNull(args, "ftrainArgsSetTensorList: args handle must not be null");
+        if (storage_views == nullptr && num_storage_views != 0)
+            throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT,
+                            "ftrainArgsSetTensorList: storage_views must not be null when num_storage_views is %u",
+                            num_storage_views);
+        TensorList list;
+        list.views.reserve(num_storage_views);
+        for (uint32_t i = 0; i < num_storage_views; ++i) list.views.emplace_back(storage_views[i]);
+        args->args.setOperand(tensor_list.opaque, OperandValue(std::move(list)));
+    });
+}
+
+FTrainStatus ftrainArgsSetGroupedTensor(FTrainArgs args, FTrainGroupedTensorId grouped_tensor, uint32_t num_groups,
+                                        FTrainStorageView data, const FTrainStorageView* offsets,
+                                        const FTrainStorageView dim_sizes[], const FTrainStorageView strides[]) {
+    return guarded([&] {
+        requireNonNull(args, "ftrainArgsSetGroupedTensor: args handle must not be null");
+        StorageView data_view(data);
+        std::optional<StorageView> offsets_view;
+        if (offsets != nullptr) offsets_view.emplace(*offsets);
+        std::vector<StorageView> sizes, steps;
+        if (dim_sizes != nullptr)
+            for (std::size_t d = 0; d < data.num_dims; ++d) sizes.emplace_back(dim_sizes[d]);
+        if (strides != nullptr)
+            for (std::size_t d = 0; d < data.num_dims; ++d) steps.emplace_back(strides[d]);
+        args->args.setOperand(grouped_tensor.opaque,
+                              OperandValue(GroupedTensor(num_groups, std::move(data_view), std::move(offsets_view),
+                                                         std::move(sizes), std::move(steps))));
+    });
+}
+
+FTrainStatus ftrainArgsSetGemm(FTrainArgs args, FTrainGemmOpId op, FTrainNumericType compute_type) {
+    return setOperation(args, op.opaque, OperationKind::kGemm, compute_type, "ftrainArgsSetGemm");
+}
+
+FTrainStatus ftrainArgsSetGroupedABCDGemm(FTrainArgs args, FTrainGroupedABCDGemmOpId op,
+                                          FTrainNumericType compute_type) {
+    return setOperation(args, op.opaque, OperationKind::kGroupedABCDGemm, compute_type,
+                        "ftrainArgsSetGroupedABCDGemm");
+}
+
+FTrainStatus ftrainArgsSetGroupedBCDGemm(FTrainArgs args, FTrainGroupedBCDGemmOpId op, FTrainNumericType compute_type) {
+    return setOperation(args, op.opaque, OperationKind::kGroupedBCDGemm, compute_type, "ftrainArgsSetGroupedBCDGemm");
+}
+
+FTrainStatus ftrainArgsSetGroupedABGemm(FTrainArgs args, FTrainGroupedABGemmOpId op, FTrainNumericType compute_type) {
+    return setOperation(args, op.opaque, OperationKind::kGroupedABGemm, compute_type, "ftrainArgsSetGroupedABGemm");
+}
+
+// ---------------------------------------------------------------- Plan
+
+FTrainStatus ftrainPlanCreate(FTrainPlan* plan, FTrainArgs args) {
+    TraceRange trace("ftrainPlanCreate");
+    return guarded([&] {
+        requireNonNull(plan, "ftrainPlanCreate: plan output must not be null");
+        requireNonNull(args, "ftrainPlanCreate: args handle must not be null");
+        const auto engine = globalHandle().find(args->args.key());
+        if (!engine) throw Exception(FTRAIN_STATUS_INTERNAL_ERROR, "OpsEngine registered for Args is unavailable");
+        *plan = new FTrainPlanStruct{engine->createPlan(args->args)};
+    });
+}
+
+FTrainStatus ftrainPlanDestroy(FTrainPlan plan) {
+    return guarded([&] {
+        requireNonNull(plan, "ftrainPlanDestroy: plan handle must not be null");
+        delete plan;
+    });
+}
+
+FTrainStatus ftrainPlanGetNumPrimitives(FTrainPlan plan, uint64_t* num_primitives) {
+    return guarded([&] {
+        requireNonNull(plan, "ftrainPlanGetNumPrimitives: plan handle must not be null");
+        requireNonNull(num_primitives, "ftrainPlanGetNumPrimitives: num_primitives output must not be null");
+        *num_primitives = plan->plan.size();
+    });
+}
+
+FTrainStatus ftrainPlanGetPrimitiveName(FTrainPlan plan, uint64_t primitive_index, const char** name) {
+    return guarded([&] {
+        requireNonNull(plan, "ftrainPlanGetPrimitiveName: plan handle must not be null");
+        requireNonNull(name, "ftrainPlanGetPrimitiveName: name output must not be null");
+        *name = plan->plan.primitiveName(primitive_index);
+    });
+}
+
+FTrainStatus ftrainPlanGetPrimitiveRequiredWorkspaceBytes(FTrainPlan plan, uint64_t primitive_index,
+                                                          uint64_t* workspace_bytes) {
+    return guarded([&] {
+        requireNonNull(plan, "ftrainPlanGetPrimitiveRequiredWorkspaceBytes: plan handle must not be null");
+        requireNonNull(workspace_bytes,
+                       "ftrainPlanGetPrimitiveRequiredWorkspaceBytes: workspace_bytes output must not be null");
+        *workspace_bytes = plan->plan.requiredWorkspaceBytes(primitive_index);
+    });
+}
+
+FTrainStatus ftrainPlanExecutePrimitive(FTrainPlan plan, uint64_t primitive_index, void* workspace,
+                                        uint64_t workspace_bytes, FTrainStream stream) {
+    TraceRange trace("ftrainPlanExecutePrimitive");
+    return guarded([&] {
+        requireNonNull(plan, "ftrainPlanExecutePrimitive: plan handle must not be null");
+        plan->plan.execute(primitive_index, workspace, workspace_bytes, stream);
+    });
+}
+
+// ---------------------------------------------------------------- convenience
+
+FTrainStatus ftrainGemm(FTrainStorageView a, FTrainStorageView b, FTrainStorageView c, FTrainStorageView d,
+                        FTrainStorageView alpha, FTrainStorageView beta, FTrainNumericType compute_type,
+                        void* workspace, uint64_t workspace_bytes, FTrainStream stream) {
+    TraceRange trace("ftrainGemm");
+    // One Ops for the Gemm Pattern per process, built through the staged API
+    // (reference src/api/gemm_api.cpp:28-49).
+    struct Entry {
+        FTrainOps ops = nullptr;
+        FTrainTensorId a{}, b{}, c{}, d{}, alpha{}, beta{};
+        FTrainGemmOpId gemm{};
+        FTrainStatus status = FTRAIN_STATUS_SUCCESS;
+    };
+    static const Entry entry = [] {
+        Entry e;
+        FTrainPattern p = nullptr;
+        FTrainStatus s  = ftrainPatternCreate(&p);
+        for (FTrainTensorId* id : {&e.a, &e.b, &e.c, &e.alpha, &e.beta, &e.d})
+            if (s == FTRAIN_STATUS_SUCCESS) s = ftrainPatternAddTensor(p, id);
+        if (s == FTRAIN_STATUS_SUCCESS) s = ftrainPatternAddGemm(p, &e.gemm, e.a, e.b, e.c, e.d, e.alpha, e.beta);
+        if (s == FTRAIN_STATUS_SUCCESS) s = ftrainOpsCreate(&e.ops, p);
+        if (p != nullptr) ftrainPatternDestroy(p);
+        e.status = s;
+        return e;
+    }();
+    if (entry.status != FTRAIN_STATUS_SUCCESS) return entry.status;
+
+    FTrainArgs args = nullptr;
+    FTrainPlan plan = nullptr;
+    FTrainStatus s  = ftrainArgsCreate(&args, entry.ops);
+    const std::pair<FTrainTensorId, const FTrainStorageView*> ports[] = {
+        {entry.a, &a}, {entry.b, &b}, {entry.c, &c}, {entry.d, &d}, {entry.alpha, &alpha}, {entry.beta, &beta}};
+    for (const auto& port : ports)
+        if (s == FTRAIN_STATUS_SUCCESS) s = ftrainArgsSetTensor(args, port.first, *port.second);
+    if (s == FTRAIN_STATUS_SUCCESS) s = ftrainArgsSetGemm(args, entry.gemm, compute_type);
+    if (s == FTRAIN_STATUS_SUCCESS) s = ftrainPlanCreate(&plan, args);
+    if (s == FTRAIN_STATUS_SUCCESS) s = ftrainPlanExecutePrimitive(plan, 0, workspace, workspace_bytes, stream);
+    // Keep the failing step's diagnostic across the clean-up calls.
+    const Result failure = s != FTRAIN_STATUS_SUCCESS ? lastResult() : Result{};
+    if (plan != nullptr) ftrainPlanDestroy(plan);
+    if (args != nullptr) ftrainArgsDestroy(args);
+    if (s != FTRAIN_STATUS_SUCCESS) lastResult() = failure;
+    return s;
+}
+
+}  // extern "C"

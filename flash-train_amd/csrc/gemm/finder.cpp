@@ -1,0 +1,126 @@
+// ShapeCost Finder: ranks the kernel catalog by a roofline cost model.
+//
+// The reference ships only a placeholder Finder that expresses no preference
+// (src/include/flash_train/family/gemm/finder.hpp:21-26); selection then falls
+// back to registration order.  This Finder estimates each variant's time on
+// the problem's shape and returns the variants best-first; the engine drops
+// the ones whose applicability check fails (alignment, size limits) and
+// caches the surviving order per problem key.
+//
+// Model, per variant (microseconds):
+//   compute: workgroups = tiles * splits are issued in rounds of
+//            (CUs * occupancy); a round lasts one workgroup's MFMA work at
+//            the variant's sustained fraction of 256 FP32 matrix FLOP/clk/CU
+//            at 2.4 GHz, scaled by how many workgroups share a CU.
+//   memory : algorithmic bytes (a, b, d, optional c; for split-k also the
+//            prologue pass and one atomic read-modify-write per split) at
+//            80% of 8 TB/s.
+//   time   = max(compute, memory) + launch latency (one more for split-k).
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <limits>
+#include <numeric>
+
+#include <hip/hip_runtime_api.h>
+
+#include "ft/gemm.hpp"
+
+namespace ftrain {
+namespace gemm {
+
+namespace {
+constexpr double kCuFlopPerMicro = 256.0 * 2.4e3;  // FP32 matrix FLOP per microsecond per CU
+constexpr double kHbmBytesPerMicro = 8.0e6 * 0.8;  // sustained HBM bytes per microsecond
+constexpr double kLaunchMicros = 4.0;
+constexpr uint64_t kMinSplitDepth = 256;  // reduction depth worth one split-k workgroup
+constexpr uint64_t kMinGemvDepth  = 64;
+
+uint64_t ceilDiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+}  // namespace
+
+int computeUnits(FTrainDeviceId device) {
+    static std::atomic<int> cached[64] = {};
+    const int slot = device >= 0 && device < 64 ? device : -1;
+    if (slot >= 0) {
+        const int v = cached[slot].load(std::memory_order_relaxed);
+        if (v > 0) return v;
+    }
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        n = 256;
+    }
+    if (slot >= 0) cached[slot].store(n, std::memory_order_relaxed);
+    return n;
+}
+
+uint32_t chooseSplits(Variant v, const GemmShape& s, int cus) {
+    const VariantInfo& vi = info(v);
+    if (!vi.split) return 1;
+    if (vi.gemv) {
+        const uint64_t col_groups = ceilDiv(std::max<uint64_t>(s.n, 1), kGemvCols);
+        const uint64_t want       = ceilDiv(uint64_t(cus) * vi.occupancy, col_groups);
+        const uint64_t most       = std::max<uint64_t>(1, s.k / kMinGemvDepth);
+        return static_cast<uint32_t>(std::clamp<uint64_t>(std::min(want, most), 1, 1024));
+    }
+    const uint64_t tiles = ceilDiv(s.m, vi.bm) * ceilDiv(s.n, vi.bn);
+    if (tiles == 0) return 0;
+    const uint64_t want = ceilDiv(uint64_t(cus) * vi.occupancy, tiles);
+    const uint64_t most = s.k / kMinSplitDepth;
+    const uint64_t splits = std::min<uint64_t>({want, most, 1024});
+    return splits >= 2 ? static_cast<uint32_t>(splits) : 0;
+}
+
+double estimateMicros(Variant v, const GemmShape& s, bool has_c, int cus) {
+    const VariantInfo& vi = info(v);
+    const double m = double(s.m), n = double(s.n), k = double(s.k);
+    double bytes = 4.0 * (m * k + k * n + m * n * (has_c ? 2.0 : 1.0));
+    double launch = kLaunchMicros;
+    uint32_t splits = 1;
+    if (vi.split) {
+        splits = chooseSplits(v, s, cus);
+        if (splits == 0) return std::numeric_limits<double>::infinity();
+        bytes += 4.0 * m * n * (has_c ? 2.0 : 1.0) + 8.0 * m * n * splits;
+        launch += kLaunchMicros;
+    }
+    if (vi.gemv) {
+        if (s.m > uint64_t(kGemvRows)) return std::numeric_limits<double>::infinity();
+        return bytes / kHbmBytesPerMicro + launch;
+    }
+    if (vi.simt) {
+        const double rate = cus * kCuFlopPerMicro * 0.5 * vi.efficiency;  // no packed FP32: half the vector rate
+        return std::max(2.0 * m * n * k / rate, bytes / kHbmBytesPerMicro) + launch;
+    }
+    const uint64_t chunk   = splits == 1 ? s.k : ceilDiv(ceilDiv(s.k, splits), vi.bk) * vi.bk;
+    const uint64_t used    = chunk == 0 ? 1 : ceilDiv(s.k, chunk);
+    const uint64_t tiles   = ceilDiv(s.m, vi.bm) * ceilDiv(s.n, vi.bn);
+    const uint64_t wgs     = tiles * used;
+    const uint64_t slots   = uint64_t(cus) * vi.occupancy;
+    const uint64_t rounds  = ceilDiv(wgs, slots);
+    const uint64_t sharing = std::min<uint64_t>(vi.occupancy, ceilDiv(wgs, cus));
+    const double depth     = double(std::max<uint64_t>(chunk, vi.bk));
+    const double per_round = 2.0 * vi.bm * vi.bn * depth * double(sharing) / (kCuFlopPerMicro * vi.efficiency);
+    return std::max(double(rounds) * per_round, bytes / kHbmBytesPerMicro) + launch;
+}
+
+}  // namespace gemm
+
+std::vector<std::string> ShapeCostFinder::candidates(const GemmProblem& problem, const Constraints& constraints) {
+    const GemmShape s = problem.shape();
+    const int cus     = gemm::computeUnits(constraints.device());
+    const bool has_c  = problem.c().memory() != nullptr;
+    std::vector<std::pair<double, int>> ranked;
+    for (int i = 0; i < static_cast<int>(gemm::Variant::kCount); ++i) {
+        const double t = gemm::estimateMicros(static_cast<gemm::Variant>(i), s, has_c, cus);
+        if (std::isfinite(t)) ranked.emplace_back(t, i);
+    }
+    std::stable_sort(ranked.begin(), ranked.end(),
+                     [](const auto& x, const auto& y) { return x.first < y.first; });
+    std::vector<std::string> names;
+    names.reserve(ranked.size());
+    for (const auto& r : ranked) names.emplace_back(gemm::info(static_cast<gemm::Variant>(r.second)).name);
+    return names;
+}
+
+}  // namespace ftrain

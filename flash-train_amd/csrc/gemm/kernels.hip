@@ -1,0 +1,457 @@
+// FP32 GEMM kernels for MI355X (gfx950 / CDNA4).
+//
+// Replaces the reference's single SIMT kernel
+// (src/primitive/hygon/gemm/fp32_gemm.hip:18-51) with:
+//   * MFMA tile kernels built on v_mfma_f32_32x32x2_f32 (a 32x32 fp32 output
+//     block per wave-instruction, k = 2 per instruction, 16 accumulator
+//     registers per lane), LDS double buffering, 128-bit global loads, an
+//     XCD-aware tile order, and a fused alpha/beta epilogue with optional
+//     c read; optionally split over k with atomic accumulation;
+//   * a streaming split-k kernel for skinny m (GEMV-like, HBM bound);
+//   * a general SIMT kernel with 64-bit indexing for shapes the others
+//     cannot take;
+//   * the elementwise prologue d = beta*c (or 0) used by the split-k paths.
+//
+// MFMA operand/result layout used below (v_mfma_f32_32x32x2_f32, one block):
+//   A operand: lane l holds A[row = l % 32][kk = l / 32]
+//   B operand: lane l holds B[kk = l / 32][col = l % 32]
+//   result   : lane l, register r holds D[row = 8*(r/4) + 4*(l/32) + r%4][col = l % 32]
+// The two reduction slots kk = 0, 1 may carry any two k indices as long as
+// A and B agree; here lane half h = l/32 walks k = h*BK/2 + s for step s,
+// which lets each lane fetch its A values for four steps with one 128-bit
+// LDS read from a row-major (k-contiguous) A tile.
+//
+// Column interleave: inside a wave tile made of TN 32-column MFMA blocks,
+// block bj / MFMA column j maps to tile column j*TN + bj.  A lane then owns TN
+// adjacent output columns per row, so B operands come from one TN-wide LDS
+// read and the epilogue stores and c loads are TN-wide vectors.
+#include <hip/hip_runtime.h>
+
+#include "ft/gemm_kernels.hpp"
+
+namespace ftrain::gemm {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+
+template <int N>
+struct VecOf;
+template <>
+struct VecOf<1> {
+    using type = float;
+};
+template <>
+struct VecOf<2> {
+    using type = floatx2;
+};
+template <>
+struct VecOf<4> {
+    using type = floatx4;
+};
+
+__device__ __forceinline__ float lane_of(float v, int) { return v; }
+__device__ __forceinline__ float lane_of(floatx2 v, int i) { return v[i]; }
+__device__ __forceinline__ float lane_of(floatx4 v, int i) { return v[i]; }
+
+// Maps a linear workgroup id to an output tile.  Workgroups are dispatched
+// round-robin over the 8 XCDs (each with its own L2), so consecutive ids
+// land on different XCDs; the first step regroups ids so that each XCD
+// receives a contiguous range of logical tiles.  The second step walks those
+// tiles in column sweeps over bands of 8 tile rows, so the tiles resident on
+// one XCD share A row-panels and B column-panels in its L2.
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int tiles = tiles_m * tiles_n;
+    const int per   = tiles >> 3;
+    int t           = bid;
+    if (bid < (per << 3)) t = (bid & 7) * per + (bid >> 3);
+    constexpr int kBand  = 8;
+    const int band_span  = kBand * tiles_n;
+    const int band       = t / band_span;
+    const int first_m    = band * kBand;
+    const int band_rows  = min(tiles_m - first_m, kBand);
+    const int within     = t - band * band_span;
+    tm                   = first_m + within % band_rows;
+    tn                   = within / band_rows;
+}
+
+// ----------------------------------------------------------------------------
+// MFMA tile kernel.
+//   BM x BN output tile per workgroup, BK reduction step per LDS stage,
+//   WM x WN waves, each wave owning a (BM/WM) x (BN/WN) sub-tile of 32x32
+//   MFMA blocks.  VEC: 128-bit global loads/stores (caller guarantees
+//   alignment and k % 4 == n % 4 == 0).  SPLIT: this workgroup reduces over
+//   [z*k_chunk, z*k_chunk + k_chunk) and atomically adds alpha*partial into d,
+//   which the prologue kernel initialised to beta*c (or 0).
+// ----------------------------------------------------------------------------
+template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool SPLIT>
+__global__ __launch_bounds__(WM* WN * 64) void mfma_gemm(GemmParams p) {
+    constexpr int NT  = WM * WN * 64;
+    constexpr int WTM = BM / WM;
+    constexpr int WTN = BN / WN;
+    constexpr int TM  = WTM / 32;
+    constexpr int TN  = WTN / 32;
+    constexpr int SA  = BK + 4;  // A tile row stride in LDS (floats); +4 spreads rows over banks
+    constexpr int SB  = BN + 4;  // B tile row stride in LDS (floats)
+    constexpr int HK  = BK / 2;  // k steps per stage
+    static_assert(TM >= 1 && TN >= 1 && (TN == 1 || TN == 2 || TN == 4), "wave tile");
+    static_assert(BK % 8 == 0, "BK");
+    using BVec = typename VecOf<TN>::type;
+
+    __shared__ __attribute__((aligned(16))) float As[2][BM * SA];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BK * SB];
+
+    const int tid  = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int li   = lane & 31;
+    const int h    = lane >> 5;
+    const int wrow = (wave / WN) * WTM;
+    const int wcol = (wave % WN) * WTN;
+
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * BM;
+    const int n0 = tn * BN;
+    const int M = p.m, N = p.n, K = p.k;
+    const int kbeg = SPLIT ? blockIdx.z * p.k_chunk : 0;
+    const int kend = SPLIT ? min(K, kbeg + p.k_chunk) : K;
+    const int nstages = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+
+    const float* __restrict__ A = p.a;
+    const float* __restrict__ B = p.b;
+
+    // Global -> register staging for one stage.
+    constexpr int A_LD = VEC ? BM * BK / 4 / NT : BM * BK / NT;
+    constexpr int B_LD = VEC ? BK * BN / 4 / NT : BK * BN / NT;
+    static_assert(A_LD >= 1 && B_LD >= 1, "tile too small for the workgroup");
+    floatx4 ra4[VEC ? A_LD : 1];
+    floatx4 rb4[VEC ? B_LD : 1];
+    float ra1[VEC ? 1 : A_LD];
+    float rb1[VEC ? 1 : B_LD];
+
+    auto load_stage = [&](int k0) {
+        if constexpr (VEC) {
+#pragma unroll
+            for (int j = 0; j < A_LD; ++j) {
+                const int idx = tid + j * NT;
+                const int row = idx / (BK / 4);
+                const int kq  = idx % (BK / 4);
+                const int gm = m0 + row, gk = k0 + 4 * kq;
+                ra4[j]        = floatx4{0.f, 0.f, 0.f, 0.f};
+                if (gm < M && gk < kend) ra4[j] = *reinterpret_cast<const floatx4*>(A + (size_t)gm * K + gk);
+            }
+#pragma unroll
+            for (int j = 0; j < B_LD; ++j) {
+                const int idx = tid + j * NT;
+                const int r   = idx / (BN / 4);
+                const int cq  = idx % (BN / 4);
+                const int gk = k0 + r, gn = n0 + 4 * cq;
+                rb4[j]        = floatx4{0.f, 0.f, 0.f, 0.f};
+                if (gk < kend && gn < N) rb4[j] = *reinterpret_cast<const floatx4*>(B + (size_t)gk * N + gn);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < A_LD; ++j) {
+                const int idx = tid + j * NT;
+                const int row = idx / BK;
+                const int kk  = idx % BK;
+                const int gm = m0 + row, gk = k0 + kk;
+                ra1[j]        = (gm < M && gk < kend) ? A[(size_t)gm * K + gk] : 0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < B_LD; ++j) {
+                const int idx = tid + j * NT;
+                const int r   = idx / BN;
+                const int cc  = idx % BN;
+                const int gk = k0 + r, gn = n0 + cc;
+                rb1[j]        = (gk < kend && gn < N) ? B[(size_t)gk * N + gn] : 0.f;
+            }
+        }
+    };
+
+    auto store_stage = [&](int buf) {
+        if constexpr (VEC) {
+#pragma unroll
+            for (int j = 0; j < A_LD; ++j) {
+                const int idx = tid + j * NT;
+                const int row = idx / (BK / 4);
+                const int kq  = idx % (BK / 4);
+                *reinterpret_cast<floatx4*>(&As[buf][row * SA + 4 * kq]) = ra4[j];
+            }
+#pragma unroll
+            for (int j = 0; j < B_LD; ++j) {
+                const int idx = tid + j * NT;
+                const int r   = idx / (BN / 4);
+                const int cq  = idx % (BN / 4);
+                *reinterpret_cast<floatx4*>(&Bs[buf][r * SB + 4 * cq]) = rb4[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < A_LD; ++j) {
+                const int idx                         = tid + j * NT;
+                As[buf][(idx / BK) * SA + idx % BK]   = ra1[j];
+            }
+#pragma unroll
+            for (int j = 0; j < B_LD; ++j) {
+                const int idx                         = tid + j * NT;
+                Bs[buf][(idx / BN) * SB + idx % BN]   = rb1[j];
+            }
+        }
+    };
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    if (nstages > 0) {
+        load_stage(kbeg);
+        store_stage(0);
+    }
+    __syncthreads();
+
+    for (int st = 0; st < nstages; ++st) {
+        const int cur = st & 1;
+        if (st + 1 < nstages) load_stage(kbeg + (st + 1) * BK);
+
+        // A values of this lane for all HK steps: rows wrow + bi*32 + li,
+        // k = h*HK + 0 .. HK-1.
+        floatx4 av[TM][HK / 4];
+#pragma unroll
+        for (int bi = 0; bi < TM; ++bi)
+#pragma unroll
+            for (int q = 0; q < HK / 4; ++q)
+                av[bi][q] = *reinterpret_cast<const floatx4*>(&As[cur][(wrow + bi * 32 + li) * SA + h * HK + 4 * q]);
+
+#pragma unroll
+        for (int s = 0; s < HK; ++s) {
+            const BVec bv = *reinterpret_cast<const BVec*>(&Bs[cur][(h * HK + s) * SB + wcol + li * TN]);
+#pragma unroll
+            for (int bi = 0; bi < TM; ++bi)
+#pragma unroll
+                for (int bj = 0; bj < TN; ++bj)
+                    acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[bi][s / 4][s % 4], lane_of(bv, bj),
+                                                                       acc[bi][bj], 0, 0, 0);
+        }
+
+        if (st + 1 < nstages) store_stage(cur ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue.
+    const float alpha = p.alpha;
+    const float beta  = p.beta;
+    const float* __restrict__ C = p.c;
+    float* __restrict__ D       = p.d;
+    const int col = n0 + wcol + li * TN;
+#pragma unroll
+    for (int bi = 0; bi < TM; ++bi) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + wrow + bi * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+            if (row >= M) continue;
+            const size_t base = (size_t)row * N + col;
+            if constexpr (SPLIT) {
+#pragma unroll
+                for (int bj = 0; bj < TN; ++bj)
+                    if (col + bj < N) unsafeAtomicAdd(D + base + bj, alpha * acc[bi][bj][r]);
+            } else if constexpr (VEC) {
+                if (col >= N) continue;
+                BVec out;
+                if constexpr (TN == 1) {
+                    out = alpha * acc[bi][0][r] + (C != nullptr ? beta * C[base] : 0.f);
+                } else {
+                    BVec cv;
+#pragma unroll
+                    for (int bj = 0; bj < TN; ++bj) cv[bj] = 0.f;
+                    if (C != nullptr) cv = *reinterpret_cast<const BVec*>(C + base);
+#pragma unroll
+                    for (int bj = 0; bj < TN; ++bj)
+                        out[bj] = alpha * acc[bi][bj][r] + (C != nullptr ? beta * cv[bj] : 0.f);
+                }
+                *reinterpret_cast<BVec*>(D + base) = out;
+            } else {
+#pragma unroll
+                for (int bj = 0; bj < TN; ++bj)
+                    if (col + bj < N)
+                        D[base + bj] = alpha * acc[bi][bj][r] + (C != nullptr ? beta * C[base + bj] : 0.f);
+            }
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
+// Skinny-m streaming kernel (m <= 8).  Each workgroup covers 256 columns and
+// one k range; its 4 waves interleave over the k rows of that range, each
+// lane streaming 4 adjacent columns of b.  The waves' partial sums meet in
+// LDS and alpha*sum is added atomically into d (initialised by the
+// prologue).  Bound by the one pass over b.
+// ----------------------------------------------------------------------------
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void gemv_splitk(GemmParams p) {
+    const int tid  = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int M = p.m, N = p.n, K = p.k;
+    const int col0 = blockIdx.x * kGemvCols + lane * 4;
+    const int kbeg = blockIdx.z * p.k_chunk;
+    const int kend = min(K, kbeg + p.k_chunk);
+    const float* __restrict__ A = p.a;
+    const float* __restrict__ B = p.b;
+
+    float acc[kGemvRows][4];
+#pragma unroll
+    for (int i = 0; i < kGemvRows; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[i][c] = 0.f;
+
+    auto step = [&](int k) {
+        floatx4 bv = floatx4{0.f, 0.f, 0.f, 0.f};
+        const float* brow = B + (size_t)k * N;
+        if constexpr (VEC) {
+            if (col0 < N) bv = *reinterpret_cast<const floatx4*>(brow + col0);
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (col0 + c < N) bv[c] = brow[col0 + c];
+        }
+#pragma unroll
+        for (int i = 0; i < kGemvRows; ++i) {
+            if (i < M) {
+                const float av = A[(size_t)i * K + k];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[i][c] += av * bv[c];
+            }
+        }
+    };
+
+    int k = kbeg + wave;
+    for (; k + 12 < kend; k += 16) {
+        step(k);
+        step(k + 4);
+        step(k + 8);
+        step(k + 12);
+    }
+    for (; k < kend; k += 4) step(k);
+
+    __shared__ float part[4][kGemvRows][kGemvCols + 4];
+#pragma unroll
+    for (int i = 0; i < kGemvRows; ++i)
+        if (i < M)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) part[wave][i][lane * 4 + c] = acc[i][c];
+    __syncthreads();
+
+    const int col = blockIdx.x * kGemvCols + tid;
+    if (col < N) {
+        for (int i = 0; i < M; ++i) {
+            const float s = part[0][i][tid] + part[1][i][tid] + part[2][i][tid] + part[3][i][tid];
+            unsafeAtomicAdd(p.d + (size_t)i * N + col, p.alpha * s);
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
+// d = c ? beta * c : 0 (grid-stride, 64-bit).  Initialises the accumulation
+// target of the split-k kernels; safe in place (c == d).
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void prologue(WideParams p) {
+    const uint64_t total  = p.m * p.n;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride)
+        p.d[i] = p.c != nullptr ? p.beta * p.c[i] : 0.f;
+}
+
+// ----------------------------------------------------------------------------
+// General SIMT kernel: 64x64 tiles, 4x4 outputs per thread, 64-bit indices,
+// grid-stride over tiles.  Any shape, 4-byte alignment.
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void simt_gemm(WideParams p) {
+    constexpr int T = 64, BK = 16;
+    __shared__ float As[BK][T + 4];
+    __shared__ float Bs[BK][T + 4];
+    const int tid = threadIdx.x;
+    const int tx = tid % 16, ty = tid / 16;
+    const uint64_t M = p.m, N = p.n, K = p.k;
+    const uint64_t tiles_n = (N + T - 1) / T;
+    const uint64_t tiles   = ((M + T - 1) / T) * tiles_n;
+    for (uint64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
+        const uint64_t m0 = (t / tiles_n) * T;
+        const uint64_t n0 = (t % tiles_n) * T;
+        float acc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+        for (uint64_t k0 = 0; k0 < K; k0 += BK) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int idx = tid + j * 256;
+                const int r = idx / BK, kk = idx % BK;
+                const uint64_t gm = m0 + r, gk = k0 + kk;
+                As[kk][r] = (gm < M && gk < K) ? p.a[gm * K + gk] : 0.f;
+                const int rb = idx / T, cb = idx % T;
+                const uint64_t bk = k0 + rb, bn = n0 + cb;
+                Bs[rb][cb] = (bk < K && bn < N) ? p.b[bk * N + bn] : 0.f;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int kk = 0; kk < BK; ++kk) {
+                float av[4], bv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) av[i] = As[kk][ty * 4 + i];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) bv[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * bv[j];
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint64_t row = m0 + ty * 4 + i;
+            if (row >= M) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint64_t c = n0 + tx * 4 + j;
+                if (c >= N) continue;
+                const uint64_t idx = row * N + c;
+                p.d[idx]           = p.alpha * acc[i][j] + (p.c != nullptr ? p.beta * p.c[idx] : 0.f);
+            }
+        }
+    }
+}
+
+
+}  // namespace
+
+const void* kernelFor(Variant v) {
+    switch (v) {
+        case Variant::kMfma256x256: return reinterpret_cast<const void*>(&mfma_gemm<256, 256, 16, 2, 2, true, false>);
+        case Variant::kMfma256x256S: return reinterpret_cast<const void*>(&mfma_gemm<256, 256, 16, 2, 2, true, true>);
+        case Variant::kMfma128x128: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, true, false>);
+        case Variant::kMfma128x128S: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, true, true>);
+        case Variant::kMfma64x256: return reinterpret_cast<const void*>(&mfma_gemm<64, 256, 16, 1, 4, true, false>);
+        case Variant::kMfma64x256S: return reinterpret_cast<const void*>(&mfma_gemm<64, 256, 16, 1, 4, true, true>);
+        case Variant::kMfma256x64: return reinterpret_cast<const void*>(&mfma_gemm<256, 64, 16, 4, 1, true, false>);
+        case Variant::kMfma256x64S: return reinterpret_cast<const void*>(&mfma_gemm<256, 64, 16, 4, 1, true, true>);
+        case Variant::kMfma128x128U: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, false, false>);
+        case Variant::kMfma128x128US: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, false, true>);
+        case Variant::kGemvS: return reinterpret_cast<const void*>(&gemv_splitk<true>);
+        case Variant::kGemvUS: return reinterpret_cast<const void*>(&gemv_splitk<false>);
+        case Variant::kSimt: return reinterpret_cast<const void*>(&simt_gemm);
+        default: return nullptr;
+    }
+}
+
+const void* prologueKernel() { return reinterpret_cast<const void*>(&prologue); }
+
+}  // namespace ftrain::gemm

@@ -1,0 +1,177 @@
+// GEMM Primitives: one Primitive per kernel variant of the catalog.
+//
+// The applicability checklist starts with the reference Fp32Gemm's rules
+// (src/primitive/hygon/gemm/fp32_gemm.cpp:27-62), with the same reason
+// strings, then adds each variant's own limits.  configure() turns the
+// problem into a ready launch (kernel, grid, packed parameters, host-side
+// alpha/beta values) so run() is one or two hipLaunchKernel calls.
+#include <limits>
+
+#include <hip/hip_runtime.h>
+
+#include "ft/gemm.hpp"
+
+namespace ftrain {
+namespace {
+
+using gemm::GemmParams;
+using gemm::Variant;
+using gemm::VariantInfo;
+using gemm::WideParams;
+
+uint64_t ceilDiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+bool floatAligned(const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % alignof(float) == 0; }
+bool vecAligned(const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+// Rules every variant shares (reference fp32_gemm.cpp:27-62).
+Result commonChecks(const GemmProblem& p) {
+    if (p.computeType() != FTRAIN_NUMERIC_TYPE_FP32) return Result(FTRAIN_STATUS_UNSUPPORTED, "compute type is not fp32");
+    for (int i = 0; i < 6; ++i)
+        if (p.port(i).numericType() != FTRAIN_NUMERIC_TYPE_FP32)
+            return Result(FTRAIN_STATUS_UNSUPPORTED, "an operand is not fp32");
+    for (int i = 0; i < 6; ++i)
+        if (p.port(i).indexType() != FTRAIN_INDEX_TYPE_CONTINUOUS)
+            return Result(FTRAIN_STATUS_UNSUPPORTED, "an operand is not continuously indexed");
+    for (int i = 0; i < 6; ++i)
+        if (!floatAligned(p.port(i).memory()))
+            return Result(FTRAIN_STATUS_UNSUPPORTED, "an operand address is not float-aligned");
+    if (p.emptyOutput()) return Result{};
+    const GemmShape s = p.shape();
+    if (p.d().memory() == nullptr || (s.k != 0 && (p.a().memory() == nullptr || p.b().memory() == nullptr)))
+        return Result(FTRAIN_STATUS_UNSUPPORTED, "a required operand address is null");
+    return Result{};
+}
+
+void check(hipError_t e, const char* what) {
+    if (e != hipSuccess)
+        throw Exception(FTRAIN_STATUS_INTERNAL_ERROR, "%s launch failed: %s", what, hipGetErrorString(e));
+}
+
+class GemmPrimitive final : public Primitive<GemmProblem> {
+  public:
+    explicit GemmPrimitive(Variant v) : v_(v), info_(&gemm::info(v)) {}
+
+    const char* name() const noexcept override { return info_->name; }
+    std::unique_ptr<PrimitiveBase> clone() const override { return std::make_unique<GemmPrimitive>(*this); }
+    uint64_t requiredWorkspaceBytes() const noexcept override { return 0; }
+
+    Result isApplicable(const GemmProblem& p, const Constraints& constraints) const override {
+        Result r = commonChecks(p);
+        if (!r.isSuccess() || p.emptyOutput()) return r;
+        const GemmShape s = p.shape();
+        if (!info_->simt) {
+            constexpr uint64_t kMax = std::numeric_limits<int32_t>::max();
+            if (s.m > kMax || s.n > kMax || s.k > kMax)
+                return Result(FTRAIN_STATUS_UNSUPPORTED, "a dimension exceeds the 32-bit kernel limit");
+            if (ceilDiv(s.m, info_->bm) * ceilDiv(s.n, info_->bn) > kMax)
+                return Result(FTRAIN_STATUS_UNSUPPORTED, "the tile count exceeds the grid limit");
+        }
+        if (info_->vec) {
+            if (s.n % 4 != 0 || s.k % 4 != 0)
+                return Result(FTRAIN_STATUS_UNSUPPORTED, "n or k is not a multiple of 4 (128-bit loads)");
+            for (int i = 0; i < 4; ++i)
+                if (!vecAligned(p.port(i).memory()))
+                    return Result(FTRAIN_STATUS_UNSUPPORTED, "a matrix address is not 16-byte aligned");
+        }
+        if (info_->gemv && s.m > uint64_t(gemm::kGemvRows))
+            return Result(FTRAIN_STATUS_UNSUPPORTED, "m exceeds the skinny-kernel row limit");
+        if (info_->split && !info_->gemv &&
+            gemm::chooseSplits(v_, s, gemm::computeUnits(constraints.device())) == 0)
+            return Result(FTRAIN_STATUS_UNSUPPORTED, "reduction depth too shallow to split");
+        return Result{};
+    }
+
+    void configure(const GemmProblem& p) override {
+        const GemmShape s = p.shape();
+        empty_            = p.emptyOutput();
+        const float alpha = *static_cast<const float*>(p.alpha().memory());
+        const float beta  = *static_cast<const float*>(p.beta().memory());
+        const auto* a     = static_cast<const float*>(p.a().memory());
+        const auto* b     = static_cast<const float*>(p.b().memory());
+        const auto* c     = static_cast<const float*>(p.c().memory());
+        auto* d           = static_cast<float*>(p.d().memory());
+        wide_             = WideParams{a, b, c, d, alpha, beta, s.m, s.n, s.k};
+        if (empty_) return;
+
+        kernel_ = gemm::kernelFor(v_);
+        block_  = dim3(info_->threads);
+        if (info_->simt) {
+            const uint64_t tiles = ceilDiv(s.m, 64) * ceilDiv(s.n, 64);
+            grid_                = dim3(static_cast<uint32_t>(std::min<uint64_t>(tiles, 1u << 20)));
+            args_[0]             = &wide_;
+            return;
+        }
+        const int cus        = gemm::computeUnits(getCurrentDeviceIdOr(0));
+        uint32_t splits      = info_->split ? gemm::chooseSplits(v_, s, cus) : 1;
+        uint64_t chunk       = s.k;
+        if (info_->split) {
+            const uint64_t step = info_->gemv ? 1 : uint64_t(info_->bk);
+            chunk               = ceilDiv(ceilDiv(s.k, splits), step) * step;
+            splits              = chunk == 0 ? 1 : static_cast<uint32_t>(ceilDiv(s.k, chunk));
+        }
+        params_ = GemmParams{a, b, c, d, alpha, beta, int32_t(s.m), int32_t(s.n), int32_t(s.k), int32_t(chunk), 0, 0};
+        if (info_->gemv) {
+            grid_ = dim3(static_cast<uint32_t>(ceilDiv(s.n, gemm::kGemvCols)), 1, splits);
+        } else {
+            params_.tiles_m = int32_t(ceilDiv(s.m, info_->bm));
+            params_.tiles_n = int32_t(ceilDiv(s.n, info_->bn));
+            grid_           = dim3(uint32_t(params_.tiles_m) * uint32_t(params_.tiles_n), 1, splits);
+        }
+        args_[0] = &params_;
+        if (info_->split) {
+            prologue_args_[0] = &wide_;
+            prologue_grid_    = dim3(static_cast<uint32_t>(std::min<uint64_t>(ceilDiv(s.m * s.n, 256), 16384)));
+        }
+    }
+
+  protected:
+    void run(const Resources& r) override {
+        if (empty_) return;
+        if (info_->split)
+            check(hipLaunchKernel(gemm::prologueKernel(), prologue_grid_, dim3(256), prologue_args_, 0, r.stream),
+                  "GEMM prologue");
+        check(hipLaunchKernel(kernel_, grid_, block_, args_, 0, r.stream), info_->name);
+    }
+
+  public:
+    // clone() copies; the launch argument arrays must then point at the
+    // copy's own parameter blocks.
+    GemmPrimitive(const GemmPrimitive& o)
+        : Primitive<GemmProblem>(o), v_(o.v_), info_(o.info_), empty_(o.empty_), kernel_(o.kernel_), grid_(o.grid_),
+          block_(o.block_), prologue_grid_(o.prologue_grid_), params_(o.params_), wide_(o.wide_) {
+        args_[0]          = info_->simt ? static_cast<void*>(&wide_) : static_cast<void*>(&params_);
+        prologue_args_[0] = &wide_;
+    }
+    GemmPrimitive& operator=(const GemmPrimitive&) = delete;
+
+  private:
+    static FTrainDeviceId getCurrentDeviceIdOr(FTrainDeviceId fallback) {
+        int dev = 0;
+        return hipGetDevice(&dev) == hipSuccess ? dev : fallback;
+    }
+
+    Variant v_;
+    const VariantInfo* info_;
+    bool empty_        = true;
+    const void* kernel_ = nullptr;
+    dim3 grid_, block_, prologue_grid_;
+    GemmParams params_{};
+    WideParams wide_{};
+    void* args_[1]          = {nullptr};
+    void* prologue_args_[1] = {nullptr};
+};
+
+}  // namespace
+
+// Registration order is the engine's fallback preference when no Finder
+// contributes (e.g. FTRAIN_DISABLED_FINDERS=ShapeCost): general large tiles
+// first, the universal SIMT kernel last.
+std::vector<std::shared_ptr<const Primitive<GemmProblem>>> GemmFamily::makeRecords() {
+    std::vector<std::shared_ptr<const Primitive<GemmProblem>>> records;
+    for (int i = 0; i < static_cast<int>(Variant::kCount); ++i)
+        records.push_back(std::make_shared<GemmPrimitive>(static_cast<Variant>(i)));
+    return records;
+}
+
+}  // namespace ftrain

@@ -1,0 +1,86 @@
+// Kernel catalog shared by the HIP translation unit (which defines the
+// kernels) and the host Primitives (which launch them).
+//
+// Every kernel computes d = alpha * (a @ b) + beta * c on row-major,
+// contiguous fp32 matrices (a: m x k, b: k x n, c/d: m x n), the semantics of
+// the reference kernel (src/primitive/hygon/gemm/fp32_gemm.hip:18-31): with a
+// null c the beta term is dropped, with a non-null c it is always evaluated
+// (so 0 * NaN propagates).
+#pragma once
+
+#include <cstdint>
+
+namespace ftrain::gemm {
+
+// Kernel parameters, passed by value.  Dimensions are 32-bit (Primitives
+// that launch these kernels require m, n, k < 2^31); element offsets are
+// computed in 64 bits inside the kernels.
+struct GemmParams {
+    const float* a;
+    const float* b;
+    const float* c;  // may be null
+    float* d;
+    float alpha;
+    float beta;
+    int32_t m, n, k;
+    int32_t k_chunk;  // reduction depth per split (a multiple of the kernel's BK); == k when not split
+    int32_t tiles_m, tiles_n;
+};
+
+// 64-bit parameters for the general SIMT kernel and the elementwise prologue.
+struct WideParams {
+    const float* a;
+    const float* b;
+    const float* c;
+    float* d;
+    float alpha;
+    float beta;
+    uint64_t m, n, k;
+};
+
+// Skinny-m kernel geometry: at most kGemvRows rows of a, kGemvCols output
+// columns per workgroup.
+constexpr int kGemvRows = 8;
+constexpr int kGemvCols = 256;
+
+enum class Variant : int {
+    // MFMA tiles, 128-bit global loads (needs k % 4 == 0, n % 4 == 0 and
+    // 16-byte aligned a/b/c/d).  Suffix S = split-k with atomic accumulation.
+    kMfma256x256,
+    kMfma256x256S,
+    kMfma128x128,
+    kMfma128x128S,
+    kMfma64x256,
+    kMfma64x256S,
+    kMfma256x64,
+    kMfma256x64S,
+    // MFMA tiles with per-element loads/stores: any shape, 4-byte alignment.
+    kMfma128x128U,
+    kMfma128x128US,
+    // Skinny m (<= 8): streaming GEMV-style split-k.
+    kGemvS,
+    kGemvUS,
+    // General SIMT kernel with 64-bit indexing.
+    kSimt,
+    kCount
+};
+
+struct VariantInfo {
+    const char* name;  // Primitive name (the FTRAIN_*_PRIMITIVES filter key)
+    int bm, bn, bk;    // output tile and reduction step (gemv: bm = max rows, bn = columns per workgroup)
+    int threads;       // workgroup size
+    int occupancy;     // workgroups expected to share one CU
+    bool vec;          // needs 16-byte alignment and n % 4 == 0, k % 4 == 0
+    bool split;        // split-k with atomic adds after a beta*c prologue
+    bool gemv;
+    bool simt;
+    double efficiency; // fraction of the FP32 matrix peak the tile sustains (cost model)
+};
+
+const VariantInfo& info(Variant v);
+
+// Device entry points (host-side stubs registered by the HIP TU).
+const void* kernelFor(Variant v);
+const void* prologueKernel();  // d = c ? beta*c : 0 over m*n elements (WideParams)
+
+}  // namespace ftrain::gemm

@@ -1,0 +1,308 @@
+"""GPU parity of the HIP GEMM path, called through the C ABI.
+
+Mirrors the reference's device tests (tests/api/gemm_api_test.cpp,
+tests/api/gemm_numerics_test.cpp) and adds the BASELINE configurations,
+every Primitive of each Plan, NaN/Inf propagation and tails.  Every result is
+compared with the CPU oracle (oracle/oracle.py) on the same inputs:
+  * the reference numerics grid with the reference's own bar,
+    |d - ref| <= 2e-5 + 2e-5 |ref| (gemm_numerics_test.cpp:58-59);
+  * everything else with the north-star bar,
+    max|d - ref| <= 1e-4 * sqrt(k) * max|ref| against fp64, identical NaN/Inf masks.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+GRID = [(1, 1, 1), (3, 4, 2), (16, 16, 16), (64, 48, 32), (129, 65, 17), (33, 257, 65), (256, 128, 64)]
+
+
+@pytest.fixture(scope="module")
+def capi():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a visible device")
+    from flash_train import capi as c
+
+    return c
+
+
+@pytest.fixture(scope="module")
+def ops(capi):
+    # Roles added in reverse of the engine's order (gemm_staged_fixture.hpp:20-28).
+    return capi.GemmOps(order=("d", "beta", "alpha", "c", "b", "a"))
+
+
+def dev(x):
+    return torch.as_tensor(np.ascontiguousarray(x, dtype=np.float32)).cuda()
+
+
+def run_plan(capi, ops, a, b, c, d, alpha, beta, index=0):
+    plan = capi.plan_for(a, b, c, d, alpha, beta, ops)
+    plan.execute(index, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return plan
+
+
+def report(oracle, d, ref, k):
+    rep = oracle.tolerance_check(d.cpu().numpy() if hasattr(d, "cpu") else d, ref, k)
+    assert rep["ok"], rep
+    return rep
+
+
+# ---------------------------------------------------------------- reference tests
+
+
+def test_convenience_kat(capi, golden):
+    a, b, c = dev(golden["kat_a"]), dev(golden["kat_b"]), dev(golden["kat_c"])
+    d = torch.empty(2, 2, device="cuda")
+    al, be = capi.HostScalar(2.0), capi.HostScalar(0.5)
+    st = capi.gemm_status(capi.matrix(a), capi.matrix(b), capi.matrix(c), capi.matrix(d), al.view, be.view,
+                          stream=torch.cuda.current_stream().cuda_stream)
+    assert st == capi.SUCCESS, capi.last_message()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(d.cpu().numpy(), golden["kat_expected"])
+    # Inconsistent b: INVALID_ARGUMENT, nothing dispatched.
+    st = capi.gemm_status(capi.matrix(a), capi.matrix(b, [3, 3]), capi.matrix(c), capi.matrix(d), al.view, be.view)
+    assert st == capi.INVALID_ARGUMENT
+
+
+def test_rebinds_addresses_and_outlives_ops_and_args(capi, golden):
+    ops = capi.GemmOps(order=("d", "beta", "alpha", "c", "b", "a"))
+    plans, outs = [], []
+    for tag in ("rebind1", "rebind2"):
+        a, b, c = dev(golden[f"{tag}_a"]), dev(golden[f"{tag}_b"]), dev(golden[f"{tag}_c"])
+        d = torch.empty(3, 4, device="cuda")
+        al, be = golden[f"{tag}_alpha_beta"]
+        plans.append((capi.plan_for(a, b, c, d, float(al), float(be), ops), (a, b, c)))
+        outs.append(d)
+    for p, _ in plans:
+        assert p.workspace_bytes(0) == 0
+    ops.close()  # Plans outlive Ops and Args
+    s = torch.cuda.current_stream().cuda_stream
+    for p, _ in plans:
+        p.execute(0, s)
+    torch.cuda.synchronize()
+    for tag, d in zip(("rebind1", "rebind2"), outs):
+        np.testing.assert_allclose(d.cpu().numpy(), golden[f"{tag}_expected"], rtol=1e-6, atol=1e-6)
+
+
+def test_in_place_c_equals_d(capi, ops, golden):
+    a, b = dev(golden["inplace_a"]), dev(golden["inplace_b"])
+    cd = dev(golden["inplace_cd"])
+    al, be = golden["inplace_alpha_beta"]
+    plan = capi.plan_for(a, b, cd, cd, float(al), float(be), ops)
+    for i in range(len(plan)):
+        cd.copy_(dev(golden["inplace_cd"]))
+        plan.execute(i, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(cd.cpu().numpy(), golden["inplace_expected"], rtol=1e-6, atol=1e-6,
+                                   err_msg=plan.name(i))
+
+
+def test_empty_output_launches_nothing(capi, ops):
+    d = capi.View(None, [0, 4])
+    al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+    args = ops.args(capi.View(None, [0, 2]), capi.View(None, [2, 4]), capi.View(None, [0, 4]), d, al.view, be.view)
+    plan = args.plan()
+    assert plan.workspace_bytes(0) == 0
+    plan.execute(0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+
+
+def test_overflow_and_invalid_shapes(capi, ops):
+    big = (1 << 63) - 1
+    al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+    args = ops.args(capi.View(None, [big, big]), capi.View(None, [big, big]), capi.View(None, [big, big]),
+                    capi.View(None, [big, big]), al.view, be.view)
+    with pytest.raises(capi.FTrainError) as e:
+        args.plan()
+    assert e.value.status == capi.OVERFLOW
+    x = torch.zeros(16, device="cuda")
+    p = x.data_ptr()
+    for a_dims, b_dims, d_dims in (([6], [2, 4], [3, 4]), ([3, 2], [3, 4], [3, 4]), ([3, 2], [2, 4], [4, 3])):
+        args = ops.args(capi.View(p, a_dims), capi.View(p, b_dims), capi.View(p, [3, 4]), capi.View(p, d_dims),
+                        al.view, be.view)
+        with pytest.raises(capi.FTrainError) as e:
+            args.plan()
+        assert e.value.status == capi.INVALID_ARGUMENT
+
+
+def test_unsupported_storage(capi, ops):
+    x = torch.zeros(64, device="cuda")
+    p = x.data_ptr()
+    al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+    args = ops.args(capi.View(p, [3, 2], numeric_type=capi.FP16), capi.View(p, [2, 4]), capi.View(p, [3, 4]),
+                    capi.View(p, [3, 4]), al.view, be.view)
+    with pytest.raises(capi.FTrainError) as e:
+        args.plan()
+    assert e.value.status == capi.UNSUPPORTED
+    assert "Fp32Gemm" in e.value.message and "an operand is not fp32" in e.value.message
+    args = ops.args(capi.View(p, [3, 2], index_type=capi.INDEX_INVALID, strides=[2, 1]), capi.View(p, [2, 4]),
+                    capi.View(p, [3, 4]), capi.View(p, [3, 4]), al.view, be.view)
+    with pytest.raises(capi.FTrainError) as e:
+        args.plan()
+    assert e.value.status == capi.UNSUPPORTED
+    args = ops.args(capi.View(None, [3, 2]), capi.View(p, [2, 4]), capi.View(p, [3, 4]), capi.View(p, [3, 4]),
+                    al.view, be.view)
+    with pytest.raises(capi.FTrainError) as e:
+        args.plan()
+    assert e.value.status == capi.UNSUPPORTED
+    args = ops.args(capi.View(p, [3, 2]), capi.View(p, [2, 4]), capi.View(p, [3, 4]), capi.View(p, [3, 4]),
+                    al.view, be.view, compute_type=capi.FP64)
+    with pytest.raises(capi.FTrainError) as e:
+        args.plan()
+    assert e.value.status == capi.UNSUPPORTED
+    # Misaligned (not 4-byte) address.
+    args = ops.args(capi.View(p + 2, [3, 2]), capi.View(p, [2, 4]), capi.View(p, [3, 4]), capi.View(p, [3, 4]),
+                    al.view, be.view)
+    with pytest.raises(capi.FTrainError) as e:
+        args.plan()
+    assert e.value.status == capi.UNSUPPORTED and "float-aligned" in e.value.message
+
+
+def test_device_mismatch(capi):
+    """A Plan bound to another device id refuses to execute (plan.cpp:43-48)."""
+    t = capi.testing_lib()
+    ops = capi.GemmOps(l=t)
+    a = torch.ones(4, 4, device="cuda")
+    al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+    args = ops.args(capi.matrix(a), capi.matrix(a), capi.matrix(None, [4, 4]), capi.matrix(a), al.view, be.view)
+    h = ctypes.c_void_p()
+    assert t.ftrainTestingPlanCreateOnDevice(ctypes.byref(h), args.handle, torch.cuda.current_device() + 1) == 0
+    plan = capi.Plan(h, t)
+    st = plan.execute_status(0, torch.cuda.current_stream().cuda_stream)
+    assert st == capi.INVALID_ARGUMENT
+    assert "calling thread uses device" in capi.last_message(t)
+    assert plan.execute_status(len(plan), 0) == capi.INVALID_ARGUMENT
+
+
+# ---------------------------------------------------------------- numerics grid
+
+
+@pytest.mark.parametrize("mkn", GRID, ids=lambda s: "x".join(map(str, s)))
+def test_reference_numerics_grid_every_primitive(capi, ops, oracle, golden, mkn):
+    m, k, n = mkn
+    a_h = oracle.fill(m * k, 0).reshape(m, k)
+    b_h = oracle.fill(k * n, 7919).reshape(k, n)
+    c_h = oracle.fill(m * n, 104729).reshape(m, n)
+    a, b, c = dev(a_h), dev(b_h), dev(c_h)
+    rows = golden[f"fill_{m}x{k}x{n}_rows"]
+    for with_c, beta, key in ((False, 0.0, "fresh"), (True, 1.25, "accum")):
+        d = torch.full((m, n), float("nan"), device="cuda")
+        plan = capi.plan_for(a, b, c if with_c else None, d, 1.5, beta, ops)
+        for i, name in enumerate(plan.names()):
+            d.fill_(float("nan"))
+            plan.execute(i, torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            got = d.cpu().numpy()[rows]
+            rep = oracle.reference_grid_check(got, golden[f"fill_{m}x{k}x{n}_{key}"])
+            assert rep["ok"], (name, key, rep)
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (5, 3, 7), (31, 33, 35), (64, 64, 64), (100, 300, 17),
+                                   (129, 257, 65), (257, 129, 520), (8, 1000, 1024), (3, 8192, 260),
+                                   (513, 64, 1500), (64, 8, 2048)])
+def test_random_shapes_every_primitive(capi, ops, oracle, shape):
+    m, n, k = shape
+    g = torch.Generator().manual_seed(m * 1000003 + n * 1009 + k)
+    a_h, b_h, c_h = (torch.randn(m, k, generator=g), torch.randn(k, n, generator=g), torch.randn(m, n, generator=g))
+    ref = oracle.gemm_f64(a_h, b_h, c_h, 0.75, -0.5)
+    a, b, c = a_h.cuda(), b_h.cuda(), c_h.cuda()
+    d = torch.empty(m, n, device="cuda")
+    plan = capi.plan_for(a, b, c, d, 0.75, -0.5, ops)
+    for i, name in enumerate(plan.names()):
+        d.fill_(float("nan"))
+        plan.execute(i, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        rep = oracle.tolerance_check(d.cpu().numpy(), ref, k)
+        assert rep["ok"], (name, shape, rep)
+
+
+def test_zero_depth(capi, ops):
+    m, n = 33, 20
+    c = torch.randn(m, n, device="cuda")
+    d = torch.empty(m, n, device="cuda")
+    al, be = capi.HostScalar(2.0), capi.HostScalar(0.5)
+    args = ops.args(capi.View(None, [m, 0]), capi.View(None, [0, n]), capi.matrix(c), capi.matrix(d), al.view,
+                    be.view)
+    plan = args.plan()
+    for i in range(len(plan)):
+        d.fill_(float("nan"))
+        plan.execute(i, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(d, 0.5 * c, rtol=0, atol=0)
+
+
+def test_nan_inf_propagation(capi, ops, oracle):
+    m, n, k = 70, 68, 96
+    g = torch.Generator().manual_seed(11)
+    a_h, b_h, c_h = torch.randn(m, k, generator=g), torch.randn(k, n, generator=g), torch.randn(m, n, generator=g)
+    a_h[3, 5] = float("nan")
+    a_h[10, 7] = float("inf")
+    b_h[9, 40] = float("-inf")
+    c_h[50, 50] = float("nan")
+    c_h[60, 1] = float("inf")
+    for beta in (0.0, 0.5):
+        ref = oracle.gemm_f64(a_h, b_h, c_h, 1.0, beta)
+        d = torch.empty(m, n, device="cuda")
+        plan = capi.plan_for(a_h.cuda(), b_h.cuda(), c_h.cuda(), d, 1.0, beta, ops)
+        for i, name in enumerate(plan.names()):
+            plan.execute(i, torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            rep = oracle.tolerance_check(d.cpu().numpy(), ref, k)
+            assert rep["masks_equal"], (name, beta)
+            assert rep["ok"], (name, beta, rep)
+
+
+# ---------------------------------------------------------------- BASELINE configs
+
+
+SMALL_CONFIGS = ["readme_128x96x64", "skinny_64x4096x4096", "skinny_4096x64x4096", "splitk_256x256x65536",
+                 "gemv_1x8192x8192", "odd_127x97x33"]
+
+
+@pytest.mark.parametrize("name", SMALL_CONFIGS)
+def test_baseline_config_full_check(capi, ops, oracle, name):
+    a_h, b_h, c_h, cfg = oracle.seeded_inputs(name)
+    ref = oracle.gemm_f64(a_h, b_h, c_h, cfg["alpha"], cfg["beta"])
+    d = torch.empty(cfg["m"], cfg["n"], device="cuda")
+    plan = capi.plan_for(a_h.cuda(), b_h.cuda(), c_h.cuda() if c_h is not None else None, d, cfg["alpha"],
+                         cfg["beta"], ops)
+    print(name, plan.names())
+    for i, pname in enumerate(plan.names()):
+        d.fill_(float("nan"))
+        plan.execute(i, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        rep = oracle.tolerance_check(d.cpu().numpy(), ref, cfg["k"])
+        assert rep["ok"], (name, pname, rep)
+
+
+@pytest.mark.parametrize("name", ["square_4096_beta", "square_8192", "mlp_fwd", "mlp_dgrad"])
+def test_baseline_config_sampled_rows(capi, ops, oracle, name):
+    """Large configs: fp64 reference on 64 seeded rows x all columns (primitive 0)."""
+    a_h, b_h, c_h, cfg = oracle.seeded_inputs(name)
+    rows = np.sort(np.random.default_rng(2026).choice(cfg["m"], size=64, replace=False))
+    ref = oracle.sampled_rows_f64(a_h, b_h, c_h, cfg["alpha"], cfg["beta"], rows)
+    d = torch.empty(cfg["m"], cfg["n"], device="cuda")
+    plan = capi.plan_for(a_h.cuda(), b_h.cuda(), c_h.cuda() if c_h is not None else None, d, cfg["alpha"],
+                         cfg["beta"], ops)
+    print(name, plan.names())
+    plan.execute(0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = d[torch.as_tensor(rows).cuda()].cpu().numpy()
+    rep = oracle.tolerance_check(got, ref, cfg["k"])
+    assert rep["ok"], (name, plan.name(0), rep)
+    # Size-independent property over the whole output: row sums equal a @ (b @ 1).
+    ones = torch.ones(cfg["n"], 1, dtype=torch.float64)
+    row_sums = d.double().cpu() @ ones
+    want = cfg["alpha"] * (a_h.double() @ (b_h.double() @ ones))
+    if c_h is not None:
+        want += cfg["beta"] * (c_h.double() @ ones)
+    err = (row_sums - want).abs().max().item()
+    scale = want.abs().max().item() + np.sqrt(cfg["n"] * cfg["k"])
+    assert err <= 1e-4 * np.sqrt(cfg["k"]) * scale, (name, err, scale)
