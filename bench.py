@@ -107,7 +107,8 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="square_8192")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
-    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-overhead", action="store_true", help="skip the cached-Plan host-overhead probe")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -156,7 +157,7 @@ def main() -> None:
     flops = 2.0 * m * n * k
     tflops = flops / (ms * 1e-3) / 1e12
     alg_bytes = 4.0 * (m * k + k * n + m * n * (2 if c is not None else 1))
-    overhead = plan_overhead()
+    overhead = None if args.no_overhead else plan_overhead()
 
     result = {
         "metric": METRIC,

@@ -13,9 +13,11 @@
 //            the variant's sustained fraction of 256 FP32 matrix FLOP/clk/CU
 //            at 2.4 GHz, scaled by how many workgroups share a CU.
 //   memory : algorithmic bytes (a, b, d, optional c; for split-k also the
-//            prologue pass and one atomic read-modify-write per split) at
-//            80% of 8 TB/s.
-//   time   = max(compute, memory) + launch latency (one more for split-k).
+//            prologue pass) at 80% of 8 TB/s.
+//   atomics: split-k variants add m*n*splits fp32 atomics at a measured
+//            device-scope rate.
+//   time   = max(compute, memory, atomics) + launch latency (one more for
+//            split-k).
 #include <algorithm>
 #include <atomic>
 #include <cmath>
@@ -33,6 +35,7 @@ namespace {
 constexpr double kCuFlopPerMicro = 256.0 * 2.4e3;  // FP32 matrix FLOP per microsecond per CU
 constexpr double kHbmBytesPerMicro = 8.0e6 * 0.8;  // sustained HBM bytes per microsecond
 constexpr double kLaunchMicros = 4.0;
+constexpr double kAtomicsPerMicro = 6.0e4;
 constexpr uint64_t kMinSplitDepth = 256;  // reduction depth worth one split-k workgroup
 constexpr uint64_t kMinGemvDepth  = 64;
 
@@ -55,43 +58,28 @@ int computeUnits(FTrainDeviceId device) {
     return n;
 }
 
-uint32_t chooseSplits(Variant v, const GemmShape& s, int cus) {
-    const VariantInfo& vi = info(v);
-    if (!vi.split) return 1;
-    if (vi.gemv) {
-        const uint64_t col_groups = ceilDiv(std::max<uint64_t>(s.n, 1), kGemvCols);
-        const uint64_t want       = ceilDiv(uint64_t(cus) * vi.occupancy, col_groups);
-        const uint64_t most       = std::max<uint64_t>(1, s.k / kMinGemvDepth);
-        return static_cast<uint32_t>(std::clamp<uint64_t>(std::min(want, most), 1, 1024));
-    }
-    const uint64_t tiles = ceilDiv(s.m, vi.bm) * ceilDiv(s.n, vi.bn);
-    if (tiles == 0) return 0;
-    const uint64_t want = ceilDiv(uint64_t(cus) * vi.occupancy, tiles);
-    const uint64_t most = s.k / kMinSplitDepth;
-    const uint64_t splits = std::min<uint64_t>({want, most, 1024});
-    return splits >= 2 ? static_cast<uint32_t>(splits) : 0;
-}
+namespace {
 
-double estimateMicros(Variant v, const GemmShape& s, bool has_c, int cus) {
-    const VariantInfo& vi = info(v);
+// Modelled time of variant `v` with a given split count (1 = no split).
+double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cus, uint64_t splits) {
     const double m = double(s.m), n = double(s.n), k = double(s.k);
-    double bytes = 4.0 * (m * k + k * n + m * n * (has_c ? 2.0 : 1.0));
-    double launch = kLaunchMicros;
-    uint32_t splits = 1;
+    double bytes      = 4.0 * (m * k + k * n + m * n * (has_c ? 2.0 : 1.0));
+    double launch     = kLaunchMicros;
+    double atomics_us = 0.0;
     if (vi.split) {
-        splits = chooseSplits(v, s, cus);
-        if (splits == 0) return std::numeric_limits<double>::infinity();
-        bytes += 4.0 * m * n * (has_c ? 2.0 : 1.0) + 8.0 * m * n * splits;
+        bytes += 4.0 * m * n * (has_c ? 2.0 : 1.0);  // prologue pass
         launch += kLaunchMicros;
+        // Device-scope fp32 atomics are resolved past the XCD-private L2s;
+        // measured on MI355X at roughly 6e4 per microsecond when many
+        // workgroups hit the same lines.
+        atomics_us = m * n * double(splits) / kAtomicsPerMicro;
     }
     if (vi.gemv) {
-        if (s.m > uint64_t(kGemvRows)) return std::numeric_limits<double>::infinity();
-        return bytes / kHbmBytesPerMicro + launch;
+        const double wgs = double(ceilDiv(std::max<uint64_t>(s.n, 1), kGemvCols) * splits);
+        const double fill = std::min(1.0, wgs / (double(cus) * 4.0));  // too few workgroups cannot reach HBM peak
+        return std::max(bytes / (kHbmBytesPerMicro * fill), atomics_us) + launch;
     }
-    if (vi.simt) {
-        const double rate = cus * kCuFlopPerMicro * 0.5 * vi.efficiency;  // no packed FP32: half the vector rate
-        return std::max(2.0 * m * n * k / rate, bytes / kHbmBytesPerMicro) + launch;
-    }
+    // Work per workgroup includes the tile padding at the m/n edges.
     const uint64_t chunk   = splits == 1 ? s.k : ceilDiv(ceilDiv(s.k, splits), vi.bk) * vi.bk;
     const uint64_t used    = chunk == 0 ? 1 : ceilDiv(s.k, chunk);
     const uint64_t tiles   = ceilDiv(s.m, vi.bm) * ceilDiv(s.n, vi.bn);
@@ -100,8 +88,40 @@ double estimateMicros(Variant v, const GemmShape& s, bool has_c, int cus) {
     const uint64_t rounds  = ceilDiv(wgs, slots);
     const uint64_t sharing = std::min<uint64_t>(vi.occupancy, ceilDiv(wgs, cus));
     const double depth     = double(std::max<uint64_t>(chunk, vi.bk));
-    const double per_round = 2.0 * vi.bm * vi.bn * depth * double(sharing) / (kCuFlopPerMicro * vi.efficiency);
-    return std::max(double(rounds) * per_round, bytes / kHbmBytesPerMicro) + launch;
+    // SIMT FMAs run at half the matrix rate without packed FP32.
+    const double cu_rate   = kCuFlopPerMicro * vi.efficiency * (vi.simt ? 0.5 : 1.0);
+    const double per_round = 2.0 * vi.bm * vi.bn * depth * double(sharing) / cu_rate;
+    return std::max({double(rounds) * per_round, bytes / kHbmBytesPerMicro, atomics_us}) + launch;
+}
+
+}  // namespace
+
+uint32_t chooseSplits(Variant v, const GemmShape& s, int cus) {
+    const VariantInfo& vi = info(v);
+    if (!vi.split) return 1;
+    const uint64_t min_depth = vi.gemv ? kMinGemvDepth : kMinSplitDepth;
+    const uint64_t most      = std::min<uint64_t>(1024, s.k / min_depth);
+    if (vi.gemv && most < 2) return 1;  // the skinny kernel also runs unsplit
+    if (most < 2 || s.m == 0 || s.n == 0) return 0;
+    // Smallest modelled time over powers of two in [2, most] (ties: fewer splits).
+    uint64_t best = 0;
+    double best_t = std::numeric_limits<double>::infinity();
+    for (uint64_t sp = 2; sp <= most; sp *= 2) {
+        const double t = modelMicros(vi, s, false, cus, sp);
+        if (t < best_t * 0.999) {
+            best_t = t;
+            best   = sp;
+        }
+    }
+    return static_cast<uint32_t>(best);
+}
+
+double estimateMicros(Variant v, const GemmShape& s, bool has_c, int cus) {
+    const VariantInfo& vi = info(v);
+    if (vi.gemv && s.m > uint64_t(kGemvRows)) return std::numeric_limits<double>::infinity();
+    const uint32_t splits = vi.split ? chooseSplits(v, s, cus) : 1;
+    if (splits == 0) return std::numeric_limits<double>::infinity();
+    return modelMicros(vi, s, has_c, cus, splits);
 }
 
 }  // namespace gemm

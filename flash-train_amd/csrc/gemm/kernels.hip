@@ -27,6 +27,8 @@
 // read and the epilogue stores and c loads are TN-wide vectors.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "ft/gemm_kernels.hpp"
 
 namespace ftrain::gemm {
@@ -78,12 +80,25 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 
 // ----------------------------------------------------------------------------
 // MFMA tile kernel.
-//   BM x BN output tile per workgroup, BK reduction step per LDS stage,
-//   WM x WN waves, each wave owning a (BM/WM) x (BN/WN) sub-tile of 32x32
-//   MFMA blocks.  VEC: 128-bit global loads/stores (caller guarantees
-//   alignment and k % 4 == n % 4 == 0).  SPLIT: this workgroup reduces over
+//   BM x BN output tile per workgroup, BK reduction depth per stage, WM x WN
+//   waves, each wave owning a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA
+//   blocks.  VEC: 128-bit global loads/stores (caller guarantees alignment and
+//   k % 4 == n % 4 == 0).  SPLIT: this workgroup reduces over
 //   [z*k_chunk, z*k_chunk + k_chunk) and atomically adds alpha*partial into d,
 //   which the prologue kernel initialised to beta*c (or 0).
+//
+// Pipeline (three LDS buffers, stage s in buffer s % 3).  Iteration s:
+//   1. read the operands of stage s+1 from LDS into the spare register set
+//      (its data became visible at the previous barrier);
+//   2. first half of stage s's MFMAs (operands already in registers);
+//   3. write stage s+2 (global loads issued one iteration earlier) to LDS;
+//   4. issue the global loads of stage s+3;
+//   5. second half of the MFMAs;
+//   6. one barrier.
+// The MFMA stream therefore never waits on an LDS read issued in the same
+// stage, and a buffer is rewritten only after the barrier that follows its
+// last read.  Interior tiles (no m/n edge, whole stages) take a copy of the
+// loop without bounds checks.
 // ----------------------------------------------------------------------------
 template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool SPLIT>
 __global__ __launch_bounds__(WM* WN * 64) void mfma_gemm(GemmParams p) {
@@ -95,12 +110,13 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_gemm(GemmParams p) {
     constexpr int SA  = BK + 4;  // A tile row stride in LDS (floats); +4 spreads rows over banks
     constexpr int SB  = BN + 4;  // B tile row stride in LDS (floats)
     constexpr int HK  = BK / 2;  // k steps per stage
+    constexpr int NBUF = 3;
     static_assert(TM >= 1 && TN >= 1 && (TN == 1 || TN == 2 || TN == 4), "wave tile");
     static_assert(BK % 8 == 0, "BK");
     using BVec = typename VecOf<TN>::type;
 
-    __shared__ __attribute__((aligned(16))) float As[2][BM * SA];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BK * SB];
+    __shared__ __attribute__((aligned(16))) float As[NBUF][BM * SA];
+    __shared__ __attribute__((aligned(16))) float Bs[NBUF][BK * SB];
 
     const int tid  = threadIdx.x;
     const int lane = tid & 63;
@@ -117,7 +133,7 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_gemm(GemmParams p) {
     const int M = p.m, N = p.n, K = p.k;
     const int kbeg = SPLIT ? blockIdx.z * p.k_chunk : 0;
     const int kend = SPLIT ? min(K, kbeg + p.k_chunk) : K;
-    const int nstages = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    const int nst  = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 
     const float* __restrict__ A = p.a;
     const float* __restrict__ B = p.b;
@@ -131,74 +147,11 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_gemm(GemmParams p) {
     float ra1[VEC ? 1 : A_LD];
     float rb1[VEC ? 1 : B_LD];
 
-    auto load_stage = [&](int k0) {
-        if constexpr (VEC) {
-#pragma unroll
-            for (int j = 0; j < A_LD; ++j) {
-                const int idx = tid + j * NT;
-                const int row = idx / (BK / 4);
-                const int kq  = idx % (BK / 4);
-                const int gm = m0 + row, gk = k0 + 4 * kq;
-                ra4[j]        = floatx4{0.f, 0.f, 0.f, 0.f};
-                if (gm < M && gk < kend) ra4[j] = *reinterpret_cast<const floatx4*>(A + (size_t)gm * K + gk);
-            }
-#pragma unroll
-            for (int j = 0; j < B_LD; ++j) {
-                const int idx = tid + j * NT;
-                const int r   = idx / (BN / 4);
-                const int cq  = idx % (BN / 4);
-                const int gk = k0 + r, gn = n0 + 4 * cq;
-                rb4[j]        = floatx4{0.f, 0.f, 0.f, 0.f};
-                if (gk < kend && gn < N) rb4[j] = *reinterpret_cast<const floatx4*>(B + (size_t)gk * N + gn);
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < A_LD; ++j) {
-                const int idx = tid + j * NT;
-                const int row = idx / BK;
-                const int kk  = idx % BK;
-                const int gm = m0 + row, gk = k0 + kk;
-                ra1[j]        = (gm < M && gk < kend) ? A[(size_t)gm * K + gk] : 0.f;
-            }
-#pragma unroll
-            for (int j = 0; j < B_LD; ++j) {
-                const int idx = tid + j * NT;
-                const int r   = idx / BN;
-                const int cc  = idx % BN;
-                const int gk = k0 + r, gn = n0 + cc;
-                rb1[j]        = (gk < kend && gn < N) ? B[(size_t)gk * N + gn] : 0.f;
-            }
-        }
-    };
-
-    auto store_stage = [&](int buf) {
-        if constexpr (VEC) {
-#pragma unroll
-            for (int j = 0; j < A_LD; ++j) {
-                const int idx = tid + j * NT;
-                const int row = idx / (BK / 4);
-                const int kq  = idx % (BK / 4);
-                *reinterpret_cast<floatx4*>(&As[buf][row * SA + 4 * kq]) = ra4[j];
-            }
-#pragma unroll
-            for (int j = 0; j < B_LD; ++j) {
-                const int idx = tid + j * NT;
-                const int r   = idx / (BN / 4);
-                const int cq  = idx % (BN / 4);
-                *reinterpret_cast<floatx4*>(&Bs[buf][r * SB + 4 * cq]) = rb4[j];
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < A_LD; ++j) {
-                const int idx                         = tid + j * NT;
-                As[buf][(idx / BK) * SA + idx % BK]   = ra1[j];
-            }
-#pragma unroll
-            for (int j = 0; j < B_LD; ++j) {
-                const int idx                         = tid + j * NT;
-                Bs[buf][(idx / BN) * SB + idx % BN]   = rb1[j];
-            }
-        }
+    // One wave's operands for one stage: A for HK steps of TM blocks, B for
+    // HK steps (TN adjacent columns per lane).
+    struct Operands {
+        floatx4 a[TM][HK / 4];
+        BVec b[HK];
     };
 
     floatx16 acc[TM][TN];
@@ -209,39 +162,138 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_gemm(GemmParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    if (nstages > 0) {
-        load_stage(kbeg);
-        store_stage(0);
-    }
-    __syncthreads();
+    auto store_stage = [&](int buf) {
+        if constexpr (VEC) {
+#pragma unroll
+            for (int j = 0; j < A_LD; ++j) {
+                const int idx = tid + j * NT;
+                *reinterpret_cast<floatx4*>(&As[buf][(idx / (BK / 4)) * SA + 4 * (idx % (BK / 4))]) = ra4[j];
+            }
+#pragma unroll
+            for (int j = 0; j < B_LD; ++j) {
+                const int idx = tid + j * NT;
+                *reinterpret_cast<floatx4*>(&Bs[buf][(idx / (BN / 4)) * SB + 4 * (idx % (BN / 4))]) = rb4[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < A_LD; ++j) {
+                const int idx                       = tid + j * NT;
+                As[buf][(idx / BK) * SA + idx % BK] = ra1[j];
+            }
+#pragma unroll
+            for (int j = 0; j < B_LD; ++j) {
+                const int idx                       = tid + j * NT;
+                Bs[buf][(idx / BN) * SB + idx % BN] = rb1[j];
+            }
+        }
+    };
 
-    for (int st = 0; st < nstages; ++st) {
-        const int cur = st & 1;
-        if (st + 1 < nstages) load_stage(kbeg + (st + 1) * BK);
-
-        // A values of this lane for all HK steps: rows wrow + bi*32 + li,
-        // k = h*HK + 0 .. HK-1.
-        floatx4 av[TM][HK / 4];
+    auto read_operands = [&](int buf, Operands& o) {
 #pragma unroll
         for (int bi = 0; bi < TM; ++bi)
 #pragma unroll
             for (int q = 0; q < HK / 4; ++q)
-                av[bi][q] = *reinterpret_cast<const floatx4*>(&As[cur][(wrow + bi * 32 + li) * SA + h * HK + 4 * q]);
-
+                o.a[bi][q] = *reinterpret_cast<const floatx4*>(&As[buf][(wrow + bi * 32 + li) * SA + h * HK + 4 * q]);
 #pragma unroll
-        for (int s = 0; s < HK; ++s) {
-            const BVec bv = *reinterpret_cast<const BVec*>(&Bs[cur][(h * HK + s) * SB + wcol + li * TN]);
+        for (int s = 0; s < HK; ++s)
+            o.b[s] = *reinterpret_cast<const BVec*>(&Bs[buf][(h * HK + s) * SB + wcol + li * TN]);
+    };
+
+    auto mfma_steps = [&](const Operands& o, auto first, auto last) {
+#pragma unroll
+        for (int s = decltype(first)::value; s < decltype(last)::value; ++s)
 #pragma unroll
             for (int bi = 0; bi < TM; ++bi)
 #pragma unroll
                 for (int bj = 0; bj < TN; ++bj)
-                    acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[bi][s / 4][s % 4], lane_of(bv, bj),
+                    acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[bi][s / 4][s % 4], lane_of(o.b[s], bj),
                                                                        acc[bi][bj], 0, 0, 0);
-        }
+    };
 
-        if (st + 1 < nstages) store_stage(cur ^ 1);
+    auto main_loop = [&](auto checked_tag) {
+        constexpr bool CHECKED = decltype(checked_tag)::value;
+
+        auto load_stage = [&](int k0) {
+            if constexpr (VEC) {
+#pragma unroll
+                for (int j = 0; j < A_LD; ++j) {
+                    const int idx = tid + j * NT;
+                    const int gm = m0 + idx / (BK / 4), gk = k0 + 4 * (idx % (BK / 4));
+                    if (CHECKED) {
+                        ra4[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                        if (gm < M && gk < kend) ra4[j] = *reinterpret_cast<const floatx4*>(A + (size_t)gm * K + gk);
+                    } else {
+                        ra4[j] = *reinterpret_cast<const floatx4*>(A + (size_t)gm * K + gk);
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < B_LD; ++j) {
+                    const int idx = tid + j * NT;
+                    const int gk = k0 + idx / (BN / 4), gn = n0 + 4 * (idx % (BN / 4));
+                    if (CHECKED) {
+                        rb4[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                        if (gk < kend && gn < N) rb4[j] = *reinterpret_cast<const floatx4*>(B + (size_t)gk * N + gn);
+                    } else {
+                        rb4[j] = *reinterpret_cast<const floatx4*>(B + (size_t)gk * N + gn);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < A_LD; ++j) {
+                    const int idx = tid + j * NT;
+                    const int gm = m0 + idx / BK, gk = k0 + idx % BK;
+                    ra1[j]        = (!CHECKED || (gm < M && gk < kend)) ? A[(size_t)gm * K + gk] : 0.f;
+                }
+#pragma unroll
+                for (int j = 0; j < B_LD; ++j) {
+                    const int idx = tid + j * NT;
+                    const int gk = k0 + idx / BN, gn = n0 + idx % BN;
+                    rb1[j]        = (!CHECKED || (gk < kend && gn < N)) ? B[(size_t)gk * N + gn] : 0.f;
+                }
+            }
+        };
+
+        using Zero = std::integral_constant<int, 0>;
+        using Half = std::integral_constant<int, HK / 2>;
+        using Full = std::integral_constant<int, HK>;
+
+        // Prologue: stages 0 and 1 in LDS, stage 2 in flight.
+        if (nst > 0) {
+            load_stage(kbeg);
+            store_stage(0);
+        }
+        if (nst > 1) {
+            load_stage(kbeg + BK);
+            store_stage(1);
+        }
+        if (nst > 2) load_stage(kbeg + 2 * BK);
         __syncthreads();
-    }
+
+        Operands x, y;
+        if (nst > 0) read_operands(0, x);
+
+        auto iteration = [&](int st, Operands& cur, Operands& nxt) {
+            if (st + 1 < nst) read_operands((st + 1) % NBUF, nxt);
+            mfma_steps(cur, Zero{}, Half{});
+            if (st + 2 < nst) store_stage((st + 2) % NBUF);
+            if (st + 3 < nst) load_stage(kbeg + (st + 3) * BK);
+            mfma_steps(cur, Half{}, Full{});
+            __syncthreads();
+        };
+
+        int st = 0;
+        for (; st + 1 < nst; st += 2) {
+            iteration(st, x, y);
+            iteration(st + 1, y, x);
+        }
+        if (st < nst) iteration(st, x, y);
+    };
+
+    const bool interior = m0 + BM <= M && n0 + BN <= N && (kend - kbeg) % BK == 0;
+    if (interior)
+        main_loop(std::false_type{});
+    else
+        main_loop(std::true_type{});
 
     // Epilogue.
     const float alpha = p.alpha;

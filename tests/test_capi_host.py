@@ -1,0 +1,646 @@
+"""Host-side contract of the C ABI -- no GPU needed.
+
+Mirrors the reference's host tests: tests/api/common_api_test.cpp (thread
+local status), tests/api/pattern_api_test.cpp and tests/pattern_test.cpp
+(Pattern validation), tests/matcher_test.cpp (order-insensitive matching),
+tests/storage_view_test.cpp, tests/tensor_test.cpp, tests/ops_args_test.cpp,
+tests/api/gemm_api_test.cpp:140-328 (plan-creation statuses),
+tests/cache/cache_test.cpp and tests/engine/engine_test.cpp (selection cache,
+environment filters).  Plan creation on a CPU host goes through the test
+hook ftrainTestingPlanCreateOnDevice (libflash_train_testing.so), which runs
+the same engine for an explicit device id; addresses are never dereferenced
+before execution, so fake device addresses are used.
+"""
+
+import ctypes
+import os
+import shutil
+import subprocess
+import sys
+import threading
+
+import pytest
+
+from flash_train import capi as c
+
+FAKE = 0x7F0000000000  # 16-byte aligned stand-in device address (never dereferenced)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return c.lib()
+
+
+@pytest.fixture(scope="module")
+def tlib():
+    return c.testing_lib()
+
+
+# ------------------------------------------------------------------ library
+
+
+def test_library_exports_exactly_the_reference_symbols():
+    assert os.path.exists(c.LIBRARY_PATH)
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", "--defined-only", c.LIBRARY_PATH], capture_output=True, text=True).stdout
+    exported = sorted(line.split()[-1] for line in out.splitlines() if line.split() and line.split()[1] in "TW")
+    assert exported == sorted(c.EXPORTED_SYMBOLS)
+
+
+def test_every_declared_symbol_resolves(lib):
+    for name in c.EXPORTED_SYMBOLS:
+        assert getattr(lib, name) is not None
+
+
+def test_header_declares_every_exported_symbol():
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    text = open(os.path.join(repo, "include", "flash_train", "common.h")).read()
+    text += open(os.path.join(repo, "include", "flash_train", "flash_train.h")).read()
+    for name in c.EXPORTED_SYMBOLS:
+        assert f" {name}(" in text, name
+
+
+# ------------------------------------------------------------------ thread-local status
+
+
+def test_last_status_semantics(lib):
+    p = ctypes.c_void_p()
+    assert lib.ftrainPatternCreate(None) == c.INVALID_ARGUMENT
+    assert lib.ftrainGetLastStatus() == c.INVALID_ARGUMENT
+    msg = lib.ftrainGetLastMessage()
+    assert b"must not be null" in msg
+    # Queries do not change the recorded result.
+    assert lib.ftrainGetLastStatus() == c.INVALID_ARGUMENT
+    assert lib.ftrainGetLastMessage() == msg
+    # Success clears it.
+    assert lib.ftrainPatternCreate(ctypes.byref(p)) == c.SUCCESS
+    assert lib.ftrainGetLastStatus() == c.SUCCESS and lib.ftrainGetLastMessage() == b""
+    assert lib.ftrainPatternDestroy(p) == c.SUCCESS
+
+
+def test_last_status_is_per_thread(lib):
+    assert lib.ftrainPatternDestroy(None) == c.INVALID_ARGUMENT
+    seen = {}
+
+    def worker():
+        seen["fresh"] = (lib.ftrainGetLastStatus(), lib.ftrainGetLastMessage())
+        lib.ftrainOpsDestroy(None)
+        seen["after"] = lib.ftrainGetLastStatus()
+
+    t = threading.Thread(target=worker)
+    t.start()
+    t.join()
+    assert seen["fresh"] == (c.SUCCESS, b"")
+    assert seen["after"] == c.INVALID_ARGUMENT
+    assert lib.ftrainGetLastStatus() == c.INVALID_ARGUMENT
+    assert b"ftrainPatternDestroy" in lib.ftrainGetLastMessage()
+
+
+def test_null_handles_rejected(lib):
+    h = ctypes.c_void_p()
+    n = ctypes.c_uint64(77)
+    s = ctypes.c_char_p()
+    rid = c.RoleId(5)
+    assert lib.ftrainOpsCreate(ctypes.byref(h), None) == c.INVALID_ARGUMENT
+    assert lib.ftrainOpsCreate(None, None) == c.INVALID_ARGUMENT
+    assert lib.ftrainArgsCreate(ctypes.byref(h), None) == c.INVALID_ARGUMENT
+    assert lib.ftrainArgsDestroy(None) == c.INVALID_ARGUMENT
+    assert lib.ftrainArgsSetTensor(None, rid, c.View(FAKE, [2, 2]).sv) == c.INVALID_ARGUMENT
+    assert lib.ftrainArgsSetGemm(None, rid, c.FP32) == c.INVALID_ARGUMENT
+    assert lib.ftrainPlanCreate(ctypes.byref(h), None) == c.INVALID_ARGUMENT
+    assert lib.ftrainPlanDestroy(None) == c.INVALID_ARGUMENT
+    assert lib.ftrainPlanGetNumPrimitives(None, ctypes.byref(n)) == c.INVALID_ARGUMENT and n.value == 77
+    assert lib.ftrainPlanGetPrimitiveName(None, 0, ctypes.byref(s)) == c.INVALID_ARGUMENT and s.value is None
+    assert lib.ftrainPlanGetPrimitiveRequiredWorkspaceBytes(None, 0, ctypes.byref(n)) == c.INVALID_ARGUMENT
+    assert lib.ftrainPlanExecutePrimitive(None, 0, None, 0, None) == c.INVALID_ARGUMENT
+    assert h.value is None
+
+
+# ------------------------------------------------------------------ Pattern / Ops
+
+
+def new_pattern(lib):
+    p = ctypes.c_void_p()
+    c.check(lib.ftrainPatternCreate(ctypes.byref(p)), l=lib)
+    return p
+
+
+def add_tensors(lib, p, n):
+    ids = []
+    for _ in range(n):
+        r = c.RoleId()
+        c.check(lib.ftrainPatternAddTensor(p, ctypes.byref(r)), l=lib)
+        ids.append(r)
+    return ids
+
+
+def ops_status(lib, p):
+    o = ctypes.c_void_p()
+    st = lib.ftrainOpsCreate(ctypes.byref(o), p)
+    if st == c.SUCCESS:
+        lib.ftrainOpsDestroy(o)
+    else:
+        assert o.value is None
+    return st
+
+
+def test_role_ids_are_sequential_and_outputs_untouched_on_failure(lib):
+    p = new_pattern(lib)
+    t, tl, gt = c.RoleId(99), c.RoleId(99), c.RoleId(99)
+    assert lib.ftrainPatternAddTensor(p, ctypes.byref(t)) == c.SUCCESS
+    assert lib.ftrainPatternAddTensorList(p, ctypes.byref(tl)) == c.SUCCESS
+    assert lib.ftrainPatternAddGroupedTensor(p, ctypes.byref(gt)) == c.SUCCESS
+    assert (t.opaque, tl.opaque, gt.opaque) == (0, 1, 2)
+    probe = c.RoleId(73)
+    assert lib.ftrainPatternAddTensor(None, ctypes.byref(probe)) == c.INVALID_ARGUMENT
+    assert probe.opaque == 73
+    lib.ftrainPatternDestroy(p)
+
+
+@pytest.mark.parametrize("order", [(0, 1, 2, 3, 4, 5), (5, 4, 3, 2, 1, 0), (3, 0, 5, 1, 4, 2)])
+def test_gemm_pattern_matches_in_any_insertion_order(lib, order):
+    p = new_pattern(lib)
+    ids = add_tensors(lib, p, 6)
+    a, b, cc, d, al, be = [ids[i] for i in order]
+    op = c.RoleId()
+    assert lib.ftrainPatternAddGemm(p, ctypes.byref(op), a, b, cc, d, al, be) == c.SUCCESS
+    assert ops_status(lib, p) == c.SUCCESS
+    lib.ftrainPatternDestroy(p)
+
+
+@pytest.mark.parametrize("ports,status", [
+    ((0, 0, 2, 3, 4, 5), c.INVALID_ARGUMENT),   # repeated input
+    ((0, 1, 2, 0, 4, 5), c.INVALID_ARGUMENT),   # output reuses an input
+    ((0, 1, 2, 6, 4, 5), c.INVALID_ARGUMENT),   # out-of-range operand (id 9)
+])
+def test_conflicting_structures_are_rejected_when_built(lib, ports, status):
+    p = new_pattern(lib)
+    ids = add_tensors(lib, p, 6)
+    ids.append(c.RoleId(9))
+    op = c.RoleId(83)
+    # Appending never validates (reference pattern_api_test.cpp:171-186).
+    assert lib.ftrainPatternAddGemm(p, ctypes.byref(op), *[ids[i] for i in ports]) == c.SUCCESS
+    assert ops_status(lib, p) == status
+    lib.ftrainPatternDestroy(p)
+
+
+def test_two_producers_and_cycles_are_rejected(lib):
+    p = new_pattern(lib)
+    ids = add_tensors(lib, p, 7)
+    op = c.RoleId()
+    lib.ftrainPatternAddGemm(p, ctypes.byref(op), ids[0], ids[1], ids[2], ids[3], ids[4], ids[5])
+    lib.ftrainPatternAddGemm(p, ctypes.byref(op), ids[1], ids[0], ids[2], ids[3], ids[4], ids[6])
+    assert ops_status(lib, p) == c.INVALID_ARGUMENT
+    assert b"already has a producer" in lib.ftrainGetLastMessage()
+    lib.ftrainPatternDestroy(p)
+    # a -> d1 via op0, d1 -> a via op1: a dependency cycle.
+    p = new_pattern(lib)
+    ids = add_tensors(lib, p, 8)
+    lib.ftrainPatternAddGemm(p, ctypes.byref(op), ids[0], ids[1], ids[2], ids[3], ids[4], ids[5])
+    lib.ftrainPatternAddGemm(p, ctypes.byref(op), ids[3], ids[6], ids[7], ids[0], ids[4], ids[5])
+    assert ops_status(lib, p) == c.INVALID_ARGUMENT
+    assert b"cycle" in lib.ftrainGetLastMessage()
+    lib.ftrainPatternDestroy(p)
+
+
+def test_unsupported_patterns(lib):
+    op = c.RoleId()
+    # Extra isolated operand.
+    p = new_pattern(lib)
+    ids = add_tensors(lib, p, 7)
+    lib.ftrainPatternAddGemm(p, ctypes.byref(op), *ids[:6])
+    assert ops_status(lib, p) == c.UNSUPPORTED
+    lib.ftrainPatternDestroy(p)
+    # Two chained Gemms.
+    p = new_pattern(lib)
+    ids = add_tensors(lib, p, 9)
+    lib.ftrainPatternAddGemm(p, ctypes.byref(op), ids[0], ids[1], ids[2], ids[3], ids[4], ids[5])
+    lib.ftrainPatternAddGemm(p, ctypes.byref(op), ids[3], ids[6], ids[7], ids[8], ids[4], ids[5])
+    assert ops_status(lib, p) == c.UNSUPPORTED
+    lib.ftrainPatternDestroy(p)
+    # Empty pattern and a grouped Gemm (declared, no engine).
+    p = new_pattern(lib)
+    assert ops_status(lib, p) == c.UNSUPPORTED
+    g = []
+    for _ in range(4):
+        r = c.RoleId()
+        lib.ftrainPatternAddGroupedTensor(p, ctypes.byref(r))
+        g.append(r)
+    al, be = add_tensors(lib, p, 2)
+    assert lib.ftrainPatternAddGroupedABCDGemm(p, ctypes.byref(op), g[0], g[1], g[2], g[3], al, be) == c.SUCCESS
+    assert ops_status(lib, p) == c.UNSUPPORTED
+    lib.ftrainPatternDestroy(p)
+    # A TensorList in a Gemm port.
+    p = new_pattern(lib)
+    ids = add_tensors(lib, p, 5)
+    tl = c.RoleId()
+    lib.ftrainPatternAddTensorList(p, ctypes.byref(tl))
+    lib.ftrainPatternAddGemm(p, ctypes.byref(op), tl, ids[0], ids[1], ids[2], ids[3], ids[4])
+    assert ops_status(lib, p) == c.UNSUPPORTED
+    lib.ftrainPatternDestroy(p)
+
+
+def test_ops_outlives_pattern(lib):
+    ops = c.GemmOps(order=("beta", "d", "a", "alpha", "c", "b"))
+    args = c.Args.__new__(c.Args)  # noqa: F841 (constructed below through ops)
+    al, be = c.HostScalar(1.0), c.HostScalar(0.0)
+    a = ops.args(c.View(FAKE, [4, 4]), c.View(FAKE, [4, 4]), c.View(None, [4, 4]), c.View(FAKE, [4, 4]), al.view,
+                 be.view)
+    a.close()
+    ops.close()
+
+
+# ------------------------------------------------------------------ Args / StorageView
+
+
+@pytest.fixture
+def gemm_ops():
+    ops = c.GemmOps()
+    yield ops
+    ops.close()
+
+
+def args_handle(lib, ops):
+    h = ctypes.c_void_p()
+    c.check(lib.ftrainArgsCreate(ctypes.byref(h), ops.ops), l=lib)
+    return h
+
+
+@pytest.mark.parametrize("view,why", [
+    (c.View(FAKE, [2, 2], numeric_type=0), "numeric_type"),
+    (c.View(FAKE, [2, 2], numeric_type=c.NUMERIC_TYPE_COUNT), "numeric_type"),
+    (c.View(FAKE, [2, 2], index_type=c.INDEX_TYPE_COUNT), "index_type"),
+    (c.View(None, []), "scalar"),
+    (c.View(FAKE, [2, -1]), "non-negative"),
+    (c.View(FAKE, [2, 2], index_type=c.INDEX_INVALID), "strides"),
+    (c.View(FAKE, [2, 2], strides=[2, 1]), "strides must be null"),
+])
+def test_storage_view_validation(lib, gemm_ops, view, why):
+    h = args_handle(lib, gemm_ops)
+    assert lib.ftrainArgsSetTensor(h, gemm_ops.ids["a"], view.sv) == c.INVALID_ARGUMENT
+    assert why.encode() in lib.ftrainGetLastMessage()
+    lib.ftrainArgsDestroy(h)
+
+
+def test_storage_view_null_dims_for_nonscalar(lib, gemm_ops):
+    h = args_handle(lib, gemm_ops)
+    sv = c.StorageView(FAKE, None, None, 2, c.FP32, c.INDEX_CONTINUOUS, False)
+    assert lib.ftrainArgsSetTensor(h, gemm_ops.ids["a"], sv) == c.INVALID_ARGUMENT
+    lib.ftrainArgsDestroy(h)
+
+
+def test_args_role_checks(lib, gemm_ops):
+    h = args_handle(lib, gemm_ops)
+    v = c.View(FAKE, [2, 2])
+    assert lib.ftrainArgsSetTensor(h, c.RoleId(6), v.sv) == c.INVALID_ARGUMENT          # out of range
+    assert lib.ftrainArgsSetTensorList(h, gemm_ops.ids["a"], ctypes.byref(v.sv), 1) == c.INVALID_ARGUMENT
+    assert b"storage family" in lib.ftrainGetLastMessage()
+    assert lib.ftrainArgsSetTensorList(h, gemm_ops.ids["a"], None, 3) == c.INVALID_ARGUMENT
+    assert lib.ftrainArgsSetGemm(h, gemm_ops.gemm_id, 0) == c.INVALID_ARGUMENT
+    assert lib.ftrainArgsSetGemm(h, gemm_ops.gemm_id, c.NUMERIC_TYPE_COUNT) == c.INVALID_ARGUMENT
+    assert lib.ftrainArgsSetGemm(h, c.RoleId(1), c.FP32) == c.INVALID_ARGUMENT
+    assert lib.ftrainArgsSetGroupedABCDGemm(h, gemm_ops.gemm_id, c.FP32) == c.INVALID_ARGUMENT
+    assert b"operation kind" in lib.ftrainGetLastMessage()
+    assert lib.ftrainArgsSetGemm(h, gemm_ops.gemm_id, c.FP32) == c.SUCCESS
+    lib.ftrainArgsDestroy(h)
+
+
+def test_grouped_tensor_validation(lib, gemm_ops):
+    h = args_handle(lib, gemm_ops)
+    data = c.View(FAKE, [8, 4])
+    bad_offsets = c.View(FAKE, [3])          # num_groups is 2
+    ok_offsets = c.View(FAKE, [2])
+    assert lib.ftrainArgsSetGroupedTensor(h, gemm_ops.ids["a"], 2, data.sv, ctypes.byref(bad_offsets.sv), None,
+                                          None) == c.INVALID_ARGUMENT
+    assert b"offsets" in lib.ftrainGetLastMessage()
+    sizes = (c.StorageView * 2)(c.View(FAKE, [2]).sv, c.View(FAKE, [2, 1]).sv)
+    assert lib.ftrainArgsSetGroupedTensor(h, gemm_ops.ids["a"], 2, data.sv, ctypes.byref(ok_offsets.sv), sizes,
+                                          None) == c.INVALID_ARGUMENT
+    assert b"dim_sizes" in lib.ftrainGetLastMessage()
+    # A valid GroupedTensor value still cannot bind to a Tensor role.
+    assert lib.ftrainArgsSetGroupedTensor(h, gemm_ops.ids["a"], 2, data.sv, ctypes.byref(ok_offsets.sv), None,
+                                          None) == c.INVALID_ARGUMENT
+    assert b"storage family" in lib.ftrainGetLastMessage()
+    lib.ftrainArgsDestroy(h)
+
+
+# ------------------------------------------------------------------ Plan creation (device id given)
+
+
+def plan_status(tlib, ops, a, b, cc, d, alpha=1.0, beta=0.0, compute=c.FP32, device=0, alpha_view=None,
+                beta_view=None):
+    al, be = c.HostScalar(alpha), c.HostScalar(beta)
+    args = ops.args(a, b, cc, d, alpha_view or al.view, beta_view or be.view, compute_type=compute)
+    h = ctypes.c_void_p()
+    st = tlib.ftrainTestingPlanCreateOnDevice(ctypes.byref(h), args.handle, device)
+    msg = c.last_message(tlib)
+    plan = c.Plan(h, tlib) if st == c.SUCCESS else None
+    args.close()
+    return st, msg, plan
+
+
+@pytest.fixture(scope="module")
+def tops(tlib):
+    return c.GemmOps(order=("d", "beta", "alpha", "c", "b", "a"), l=tlib)
+
+
+def V(dims, mem=FAKE, **kw):
+    return c.View(mem, dims, **kw)
+
+
+def test_incomplete_args(tlib, tops):
+    h = ctypes.c_void_p()
+    tlib.ftrainArgsCreate(ctypes.byref(h), tops.ops)
+    p = ctypes.c_void_p()
+    assert tlib.ftrainTestingPlanCreateOnDevice(ctypes.byref(p), h, 0) == c.INVALID_ARGUMENT
+    assert b"unset" in tlib.ftrainGetLastMessage()
+    tlib.ftrainArgsDestroy(h)
+
+
+def test_plan_success_and_queries(tlib, tops):
+    st, msg, plan = plan_status(tlib, tops, V([64, 32]), V([32, 48]), V([64, 48]), V([64, 48]))
+    assert st == c.SUCCESS, msg
+    names = plan.names()
+    assert len(names) >= 1 and len(set(names)) == len(names)
+    assert all(plan.workspace_bytes(i) == 0 for i in range(len(names)))
+    s = ctypes.c_char_p()
+    assert tlib.ftrainPlanGetPrimitiveName(plan.handle, len(names), ctypes.byref(s)) == c.INVALID_ARGUMENT
+    n = ctypes.c_uint64()
+    assert tlib.ftrainPlanGetPrimitiveRequiredWorkspaceBytes(plan.handle, 99, ctypes.byref(n)) == c.INVALID_ARGUMENT
+    assert "Fp32Gemm" in names  # the universal kernel applies to every valid fp32 problem
+    plan.close()
+
+
+@pytest.mark.parametrize("a,b,cc,d", [
+    (V([6]), V([2, 4]), V([3, 4]), V([3, 4])),
+    (V([3, 2]), V([3, 4]), V([3, 4]), V([3, 4])),
+    (V([3, 2]), V([2, 4]), V([3, 4]), V([4, 3])),
+    (V([3, 2]), V([2, 4]), V([3, 5]), V([3, 4])),
+    (V([3, 2], host=True), V([2, 4]), V([3, 4]), V([3, 4])),
+])
+def test_invalid_shapes_and_placement(tlib, tops, a, b, cc, d):
+    st, msg, _ = plan_status(tlib, tops, a, b, cc, d)
+    assert st == c.INVALID_ARGUMENT, msg
+
+
+def test_scalar_rules(tlib, tops):
+    x = ctypes.c_float(1.0)
+    st, msg, _ = plan_status(tlib, tops, V([3, 2]), V([2, 4]), V([3, 4]), V([3, 4]),
+                             alpha_view=c.View(ctypes.addressof(x), [1], host=True))
+    assert st == c.INVALID_ARGUMENT and "scalar" in msg
+    st, msg, _ = plan_status(tlib, tops, V([3, 2]), V([2, 4]), V([3, 4]), V([3, 4]),
+                             alpha_view=c.View(FAKE, []))  # device scalar
+    assert st == c.INVALID_ARGUMENT and "host" in msg
+
+
+def test_overflow(tlib, tops):
+    big = (1 << 63) - 1
+    st, msg, _ = plan_status(tlib, tops, V([big, big], None), V([big, big], None), V([big, big], None),
+                             V([big, big], None))
+    assert st == c.OVERFLOW, msg
+
+
+@pytest.mark.parametrize("kw,why", [
+    (dict(a=V([3, 2], numeric_type=c.FP16)), "an operand is not fp32"),
+    (dict(b=V([2, 4], numeric_type=c.FP64)), "an operand is not fp32"),
+    (dict(a=V([3, 2], index_type=c.INDEX_INVALID, strides=[2, 1])), "continuously indexed"),
+    (dict(compute=c.FP64), "compute type is not fp32"),
+    (dict(a=V([3, 2], None)), "required operand address is null"),
+    (dict(d=V([3, 4], None)), "required operand address is null"),
+    (dict(a=V([3, 2], FAKE + 2)), "not float-aligned"),
+])
+def test_unsupported_reasons_name_every_primitive(tlib, tops, kw, why):
+    args = dict(a=V([3, 2]), b=V([2, 4]), cc=V([3, 4]), d=V([3, 4]))
+    args.update({k: v for k, v in kw.items() if k != "compute"})
+    st, msg, _ = plan_status(tlib, tops, args["a"], args["b"], args["cc"], args["d"],
+                             compute=kw.get("compute", c.FP32))
+    assert st == c.UNSUPPORTED, msg
+    assert why in msg
+    for v in range(tlib.ftrainTestingVariantCount()):
+        assert tlib.ftrainTestingVariantName(v).decode() in msg
+
+
+def test_empty_output_needs_no_storage(tlib, tops):
+    st, msg, plan = plan_status(tlib, tops, V([0, 2], None), V([2, 4], None), V([0, 4], None), V([0, 4], None))
+    assert st == c.SUCCESS, msg
+    assert plan.workspace_bytes(0) == 0
+
+
+def test_zero_depth_needs_no_a_or_b(tlib, tops):
+    st, msg, plan = plan_status(tlib, tops, V([3, 0], None), V([0, 4], None), V([3, 4]), V([3, 4]))
+    assert st == c.SUCCESS, msg
+    assert not any(n.startswith("Fp32MfmaGemm") and n.endswith("SplitK") for n in plan.names())
+
+
+# ------------------------------------------------------------------ Finder choices
+
+
+def rank(tlib, m, n, k, addr=FAKE, with_c=False, device=0):
+    views = (c.StorageView * 6)()
+    keep = [V([m, k], addr), V([k, n], addr), V([m, n], addr if with_c else None), V([m, n], addr)]
+    al, be = c.HostScalar(1.0), c.HostScalar(0.0)
+    for i, v in enumerate(keep + [al.view, be.view]):
+        views[i] = v.sv
+    buf = ctypes.create_string_buffer(4096)
+    st = tlib.ftrainTestingRankGemm(views, c.FP32, device, buf, 4096)
+    assert st == c.SUCCESS, c.last_message(tlib)
+    return buf.value.decode().split(",")
+
+
+def test_finder_choices_for_the_baseline_configs(tlib):
+    assert rank(tlib, 8192, 8192, 8192)[0] == "Fp32MfmaGemm_256x256"
+    assert rank(tlib, 16384, 14336, 4096)[0] == "Fp32MfmaGemm_256x256"
+    assert rank(tlib, 16384, 4096, 14336)[0] == "Fp32MfmaGemm_256x256"
+    assert rank(tlib, 4096, 4096, 4096, with_c=True)[0].startswith("Fp32MfmaGemm_")
+    assert rank(tlib, 1, 8192, 8192)[0] == "Fp32Gemv_SplitK"
+    assert rank(tlib, 256, 256, 65536)[0].endswith("_SplitK")
+    assert rank(tlib, 64, 4096, 4096)[0].endswith("_SplitK")
+    assert rank(tlib, 4096, 64, 4096)[0].endswith("_SplitK")
+    # Odd sizes: no 128-bit variant applies.
+    odd = rank(tlib, 127, 97, 33)
+    assert odd and all(("Unaligned" in n) or n == "Fp32Gemm" for n in odd)
+
+
+def test_finder_respects_alignment_and_row_limits(tlib):
+    names = rank(tlib, 512, 512, 512, addr=FAKE + 4)
+    assert names and all(("Unaligned" in n) or n == "Fp32Gemm" for n in names)
+    assert not any(n.startswith("Fp32Gemv") for n in rank(tlib, 9, 8192, 8192))
+    assert "Fp32Gemv_SplitK" in rank(tlib, 8, 8192, 8192)
+
+
+def test_plan_order_matches_finder_rank(tlib, tops):
+    st, msg, plan = plan_status(tlib, tops, V([1, 8192]), V([8192, 8192]), V([1, 8192], None), V([1, 8192]))
+    assert st == c.SUCCESS, msg
+    assert plan.names() == rank(tlib, 1, 8192, 8192)
+
+
+def test_cost_model_is_monotone_in_work(tlib):
+    for v in range(tlib.ftrainTestingVariantCount()):
+        small = tlib.ftrainTestingEstimateMicros(v, 1024, 1024, 1024, False, 256)
+        large = tlib.ftrainTestingEstimateMicros(v, 4096, 4096, 4096, False, 256)
+        if small != float("inf"):
+            assert large >= small, tlib.ftrainTestingVariantName(v)
+
+
+def test_split_counts(tlib):
+    names = {tlib.ftrainTestingVariantName(v).decode(): v for v in range(tlib.ftrainTestingVariantCount())}
+    s = tlib.ftrainTestingChooseSplits(names["Fp32MfmaGemm_128x128_SplitK"], 256, 256, 65536, 256)
+    assert 2 <= s <= 65536 // 256
+    assert tlib.ftrainTestingChooseSplits(names["Fp32MfmaGemm_128x128_SplitK"], 256, 256, 300, 256) == 0
+    assert tlib.ftrainTestingChooseSplits(names["Fp32MfmaGemm_128x128"], 256, 256, 65536, 256) == 1
+    assert tlib.ftrainTestingChooseSplits(names["Fp32Gemv_SplitK"], 1, 64, 16, 256) == 1
+
+
+# ------------------------------------------------------------------ environment filters
+
+
+def run_with_env(env: dict, code: str) -> str:
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    full = dict(os.environ, **env)
+    prog = ("import sys; sys.path[:0]=[%r, %r]\n" % (os.path.join(repo, "flash-train_amd"), repo)) + code
+    out = subprocess.run([sys.executable, "-c", prog], env=full, capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    return out.stdout.strip()
+
+
+PLAN_NAMES = """
+import ctypes
+from flash_train import capi as c
+t = c.testing_lib()
+ops = c.GemmOps(l=t)
+al, be = c.HostScalar(1.0), c.HostScalar(0.0)
+F = 0x7F0000000000
+args = ops.args(c.View(F, [2048, 2048]), c.View(F, [2048, 2048]), c.View(None, [2048, 2048]),
+                c.View(F, [2048, 2048]), al.view, be.view)
+h = ctypes.c_void_p()
+st = t.ftrainTestingPlanCreateOnDevice(ctypes.byref(h), args.handle, 0)
+print(",".join(c.Plan(h, t).names()) if st == 0 else "status=%d %s" % (st, c.last_message(t)))
+"""
+
+
+def test_env_disabled_primitive():
+    names = run_with_env({"FTRAIN_DISABLED_PRIMITIVES": " Fp32MfmaGemm_256x256 ,\tFp32Gemm"}, PLAN_NAMES).split(",")
+    assert "Fp32MfmaGemm_256x256" not in names and "Fp32Gemm" not in names and names
+
+
+def test_env_enabled_primitives():
+    names = run_with_env({"FTRAIN_ENABLED_PRIMITIVES": "Fp32Gemm,NoSuchPrimitive"}, PLAN_NAMES).split(",")
+    assert names == ["Fp32Gemm"]
+
+
+def test_env_all_filtered_is_unsupported():
+    out = run_with_env({"FTRAIN_ENABLED_PRIMITIVES": "NoSuchPrimitive"}, PLAN_NAMES)
+    assert out.startswith("status=4")
+
+
+def test_env_disabled_finder_falls_back_to_registration_order():
+    names = run_with_env({"FTRAIN_DISABLED_FINDERS": "ShapeCost"}, PLAN_NAMES).split(",")
+    t = c.testing_lib()
+    catalog = [t.ftrainTestingVariantName(v).decode() for v in range(t.ftrainTestingVariantCount())]
+    assert names == [n for n in catalog if n in names]  # registration order
+    assert names[-1] == "Fp32Gemm"
+
+
+def test_env_disable_cache_still_selects_the_same():
+    assert run_with_env({"FTRAIN_DISABLE_CACHE": "1"}, PLAN_NAMES) == run_with_env({"FTRAIN_DISABLE_CACHE": "0"},
+                                                                                  PLAN_NAMES)
+
+
+def test_name_list_and_switch_parsing(tlib):
+    buf = ctypes.create_string_buffer(256)
+    tlib.ftrainTestingParseNameList(b" a ,b,,\tc\t, a", buf, 256)
+    assert buf.value == b"a|b|c"
+    tlib.ftrainTestingParseNameList(None, buf, 256)
+    assert buf.value == b""
+    assert not tlib.ftrainTestingParseSwitch(None)
+    assert not tlib.ftrainTestingParseSwitch(b" 0 ")
+    assert not tlib.ftrainTestingParseSwitch(b"  ")
+    assert tlib.ftrainTestingParseSwitch(b"1") and tlib.ftrainTestingParseSwitch(b" yes")
+
+
+# ------------------------------------------------------------------ selection cache
+
+
+def arr(xs):
+    return (ctypes.c_uint64 * max(len(xs), 1))(*xs), len(xs)
+
+
+def cache_publish(t, cache, ct, pt, pos):
+    a, na = arr(ct)
+    b, nb = arr(pt)
+    p, npos = arr(pos)
+    return t.ftrainTestingCachePublish(cache, a, na, b, nb, p, npos)
+
+
+def cache_find(t, cache, ct, pt):
+    a, na = arr(ct)
+    b, nb = arr(pt)
+    out = (ctypes.c_uint64 * 64)()
+    n = t.ftrainTestingCacheFind(cache, a, na, b, nb, out, 64)
+    return None if n < 0 else list(out[:n])
+
+
+def test_cache_publish_once_and_key_separation(tlib):
+    cache = tlib.ftrainTestingCacheCreate(1000, 4)
+    assert cache_find(tlib, cache, [0], [1, 2, 3]) is None
+    assert cache_publish(tlib, cache, [0], [1, 2, 3], [4, 2]) == c.SUCCESS
+    assert cache_publish(tlib, cache, [0], [1, 2, 3], [9]) == c.SUCCESS  # publish-once: keeps [4, 2]
+    assert cache_find(tlib, cache, [0], [1, 2, 3]) == [4, 2]
+    assert cache_find(tlib, cache, [1], [1, 2, 3]) is None   # other device
+    assert cache_find(tlib, cache, [0, 1], [2, 3]) is None   # token boundary moves
+    assert cache_publish(tlib, cache, [0], [7], []) == c.INVALID_ARGUMENT
+    assert tlib.ftrainTestingCacheSize(cache) == 1
+    tlib.ftrainTestingCacheDestroy(cache)
+    assert tlib.ftrainTestingCacheCreate(0, 4) is None
+    assert tlib.ftrainTestingCacheCreate(10, 0) is None
+
+
+def test_cache_evicts_least_hit_batch(tlib):
+    cache = tlib.ftrainTestingCacheCreate(16, 1)
+    for i in range(16):
+        cache_publish(tlib, cache, [0], [i], [i])
+    for _ in range(3):
+        for i in range(8, 16):
+            assert cache_find(tlib, cache, [0], [i]) == [i]
+    cache_publish(tlib, cache, [0], [100], [100])
+    assert tlib.ftrainTestingCacheSize(cache) == 16 - 2 + 1  # one batch of 16/8 evicted
+    assert all(cache_find(tlib, cache, [0], [i]) == [i] for i in range(8, 16))  # hot entries survive
+    assert cache_find(tlib, cache, [0], [100]) == [100]
+    tlib.ftrainTestingCacheDestroy(cache)
+
+
+def test_cache_concurrent_publishers(tlib):
+    cache = tlib.ftrainTestingCacheCreate(100000, 256)
+
+    def work(seed):
+        for i in range(500):
+            cache_publish(tlib, cache, [seed % 2], [i], [seed])
+
+    threads = [threading.Thread(target=work, args=(s,)) for s in range(8)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert tlib.ftrainTestingCacheSize(cache) == 1000
+    for dev in (0, 1):
+        for i in (0, 250, 499):
+            assert cache_find(tlib, cache, [dev], [i])[0] % 2 == dev
+    tlib.ftrainTestingCacheDestroy(cache)
+
+
+def test_concurrent_plan_creation_agrees(tlib, tops):
+    results = []
+
+    def work():
+        st, msg, plan = plan_status(tlib, tops, V([1000, 1000]), V([1000, 1000]), V([1000, 1000], None),
+                                    V([1000, 1000]))
+        results.append((st, tuple(plan.names()) if plan else msg))
+
+    threads = [threading.Thread(target=work) for _ in range(8)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert len(set(results)) == 1 and results[0][0] == c.SUCCESS
