@@ -48,12 +48,13 @@ def plan_overhead() -> dict | None:
         return {"error": str(e)}
 
 
-def traffic_from_profiles(kernel: str) -> float | None:
-    """HBM bytes per launch for `kernel`, from the committed rocprofv3 PMC summary (if any)."""
+def traffic_from_profiles(workload: str) -> float | None:
+    """HBM bytes per launch of the workload's kernel: the committed rocprofv3 PMC figure
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration), if one exists."""
     path = os.path.join(REPO, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get(kernel, {}).get("hbm_bytes_per_launch")
+            return json.load(f).get(workload, {}).get("hbm_bytes_per_launch")
     except (OSError, ValueError):
         return None
 
@@ -109,7 +110,21 @@ def main() -> None:
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-overhead", action="store_true", help="skip the cached-Plan host-overhead probe")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 5 device copies of 256 MiB (the known-size kernel that scales the PMC "
+                         "FETCH_SIZE / WRITE_SIZE counters into bytes)")
     args = ap.parse_args()
+
+    if args.copy_calibration:
+        import torch
+
+        x = torch.empty(64 * 1024 * 1024, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(5):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": x.numel() * 4, "bytes_written": y.numel() * 4}))
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs the GEMM path on a single MI355X "
@@ -157,6 +172,17 @@ def main() -> None:
     flops = 2.0 * m * n * k
     tflops = flops / (ms * 1e-3) / 1e12
     alg_bytes = 4.0 * (m * k + k * n + m * n * (2 if c is not None else 1))
+    gbs = alg_bytes / (ms * 1e-3) / 1e9
+    # Roofline bound: arithmetic intensity against the ridge point (157.3 TFLOP/s / 8 TB/s).
+    hbm_bound = flops / alg_bytes < FP32_MATRIX_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+    if hbm_bound:
+        roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    else:
+        roofline = {"bound": "mfma", "achieved": round(tflops, 3), "peak": FP32_MATRIX_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(tflops / FP32_MATRIX_PEAK_TFLOPS, 4)}
+    roofline.update({"traffic": traffic_from_profiles(args.workload), "algorithmic_bytes": alg_bytes,
+                     "algorithmic_flops": flops, "kernel_ms": round(ms, 4), "kernel": name})
     overhead = None if args.no_overhead else plan_overhead()
 
     result = {
@@ -171,14 +197,11 @@ def main() -> None:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic (seeded CPU torch.Generator 2026, U(-1,1) for 8192^3)",
+        "data": "synthetic (seeded CPU torch.Generator 2026; BASELINE.json distributions)",
         "config": {"workload": args.workload, "m": m, "n": n, "k": k, "alpha": cfg["alpha"], "beta": cfg["beta"],
                    "c": c is not None, "primitive": name, "parallelism": "single GPU"},
         "pct_of_fp32_matrix_peak": round(100.0 * tflops / FP32_MATRIX_PEAK_TFLOPS, 2),
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": FP32_MATRIX_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / FP32_MATRIX_PEAK_TFLOPS, 4),
-                     "traffic": traffic_from_profiles(name), "algorithmic_bytes": alg_bytes,
-                     "kernel_ms": round(ms, 4)},
+        "roofline": roofline,
         "plan_overhead": overhead,
         "parity": {"rows_checked": int(len(rows)), "max_abs_err": rep["max_abs_err"], "bound": rep["bound"],
                    "ok": rep["ok"]},
