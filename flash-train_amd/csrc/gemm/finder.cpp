@@ -12,9 +12,10 @@
 //            (CUs * occupancy); a round lasts one workgroup's MFMA work at
 //            the variant's sustained fraction of 256 FP32 matrix FLOP/clk/CU
 //            at 2.4 GHz, scaled by how many workgroups share a CU.
-//   memory : algorithmic bytes (a, b, d, optional c; for split-k also the
-//            prologue pass) at 80% of 8 TB/s.
-//   atomics: split-k variants add m*n*splits fp32 atomics at a measured
+//   memory : algorithmic bytes (a, b, d, optional c) at 80% of 8 TB/s, plus
+//            the partial tiles (written and read once) for split-k with a
+//            reduction, or the beta*c prologue pass for atomic split-k.
+//   atomics: atomic split-k adds m*n*splits fp32 atomics at a measured
 //            device-scope rate.
 //   time   = max(compute, memory, atomics) + launch latency (one more for
 //            split-k).
@@ -36,6 +37,7 @@ constexpr double kCuFlopPerMicro = 256.0 * 2.4e3;  // FP32 matrix FLOP per micro
 constexpr double kHbmBytesPerMicro = 8.0e6 * 0.8;  // sustained HBM bytes per microsecond
 constexpr double kLaunchMicros = 4.0;
 constexpr double kAtomicsPerMicro = 6.0e4;
+constexpr double kPoolMicros      = 2.0;  // stream-ordered workspace acquire + release
 constexpr uint64_t kMinSplitDepth = 256;  // reduction depth worth one split-k workgroup
 constexpr uint64_t kMinGemvDepth  = 64;
 
@@ -66,13 +68,16 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
     double bytes      = 4.0 * (m * k + k * n + m * n * (has_c ? 2.0 : 1.0));
     double launch     = kLaunchMicros;
     double atomics_us = 0.0;
-    if (vi.split) {
+    if (vi.split == SplitKind::kAtomic) {
         bytes += 4.0 * m * n * (has_c ? 2.0 : 1.0);  // prologue pass
         launch += kLaunchMicros;
         // Device-scope fp32 atomics are resolved past the XCD-private L2s;
         // measured on MI355X at roughly 6e4 per microsecond when many
         // workgroups hit the same lines.
         atomics_us = m * n * double(splits) / kAtomicsPerMicro;
+    } else if (vi.split == SplitKind::kPartial) {
+        bytes += 8.0 * m * n * double(splits);  // partial tiles written, then read by the reduction
+        launch += kLaunchMicros + kPoolMicros;
     }
     if (vi.gemv) {
         const double wgs = double(ceilDiv(std::max<uint64_t>(s.n, 1), kGemvCols) * splits);
@@ -98,9 +103,11 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
 
 uint32_t chooseSplits(Variant v, const GemmShape& s, int cus) {
     const VariantInfo& vi = info(v);
-    if (!vi.split) return 1;
+    if (vi.split == SplitKind::kNone) return 1;
     const uint64_t min_depth = vi.gemv ? kMinGemvDepth : kMinSplitDepth;
-    const uint64_t most      = std::min<uint64_t>(1024, s.k / min_depth);
+    uint64_t most            = std::min<uint64_t>(1024, s.k / min_depth);
+    if (vi.split == SplitKind::kPartial && s.m * s.n > 0)
+        most = std::min<uint64_t>(most, kMaxPartialBytes / (s.m * s.n * sizeof(float)));
     if (vi.gemv && most < 2) return 1;  // the skinny kernel also runs unsplit
     if (most < 2 || s.m == 0 || s.n == 0) return 0;
     // Smallest modelled time over powers of two in [2, most] (ties: fewer splits).
@@ -119,7 +126,7 @@ uint32_t chooseSplits(Variant v, const GemmShape& s, int cus) {
 double estimateMicros(Variant v, const GemmShape& s, bool has_c, int cus) {
     const VariantInfo& vi = info(v);
     if (vi.gemv && s.m > uint64_t(kGemvRows)) return std::numeric_limits<double>::infinity();
-    const uint32_t splits = vi.split ? chooseSplits(v, s, cus) : 1;
+    const uint32_t splits = vi.split != SplitKind::kNone ? chooseSplits(v, s, cus) : 1;
     if (splits == 0) return std::numeric_limits<double>::infinity();
     return modelMicros(vi, s, has_c, cus, splits);
 }

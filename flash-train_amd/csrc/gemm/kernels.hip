@@ -78,14 +78,21 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
     tn                   = within / band_rows;
 }
 
+enum SplitMode : int { kWhole = 0, kAtomic = 1, kPartial = 2 };
+
 // ----------------------------------------------------------------------------
 // MFMA tile kernel.
 //   BM x BN output tile per workgroup, BK reduction depth per stage, WM x WN
 //   waves, each wave owning a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA
-//   blocks.  VEC: 128-bit global loads/stores (caller guarantees alignment and
-//   k % 4 == n % 4 == 0).  SPLIT: this workgroup reduces over
-//   [z*k_chunk, z*k_chunk + k_chunk) and atomically adds alpha*partial into d,
-//   which the prologue kernel initialised to beta*c (or 0).
+//   blocks; MINB workgroups per CU bound the register budget.  VEC: 128-bit global loads/stores (caller guarantees alignment and
+//   k % 4 == n % 4 == 0).  SPLIT selects the epilogue:
+//     kWhole   - this workgroup owns the whole reduction: d = alpha*acc + beta*c;
+//     kAtomic  - it reduces [z*k_chunk, z*k_chunk + k_chunk) and atomically
+//                adds alpha*partial into d, which the prologue kernel set to
+//                beta*c (or 0);
+//     kPartial - same k range, but the raw partial tile is stored to slice z
+//                of the workspace p.d (z*m*n floats); splitk_reduce then forms
+//                d = alpha * sum_z(partial_z) + beta*c in fixed z order.
 //
 // Pipeline (three LDS buffers, stage s in buffer s % 3).  Iteration s:
 //   1. read the operands of stage s+1 from LDS into the spare register set
@@ -100,8 +107,8 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 // last read.  Interior tiles (no m/n edge, whole stages) take a copy of the
 // loop without bounds checks.
 // ----------------------------------------------------------------------------
-template <int BM, int BN, int BK, int WM, int WN, bool VEC, bool SPLIT>
-__global__ __launch_bounds__(WM* WN * 64) void mfma_gemm(GemmParams p) {
+template <int BM, int BN, int BK, int WM, int WN, int NBUF, int MINB, bool VEC, int SPLIT>
+__global__ __launch_bounds__(WM* WN * 64, MINB) void mfma_gemm(GemmParams p) {
     constexpr int NT  = WM * WN * 64;
     constexpr int WTM = BM / WM;
     constexpr int WTN = BN / WN;
@@ -110,9 +117,9 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_gemm(GemmParams p) {
     constexpr int SA  = BK + 4;  // A tile row stride in LDS (floats); +4 spreads rows over banks
     constexpr int SB  = BN + 4;  // B tile row stride in LDS (floats)
     constexpr int HK  = BK / 2;  // k steps per stage
-    constexpr int NBUF = 3;
     static_assert(TM >= 1 && TN >= 1 && (TN == 1 || TN == 2 || TN == 4), "wave tile");
     static_assert(BK % 8 == 0, "BK");
+    static_assert(NBUF == 2 || NBUF == 3, "two or three LDS stages");
     using BVec = typename VecOf<TN>::type;
 
     __shared__ __attribute__((aligned(16))) float As[NBUF][BM * SA];
@@ -131,8 +138,8 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_gemm(GemmParams p) {
     const int m0 = tm * BM;
     const int n0 = tn * BN;
     const int M = p.m, N = p.n, K = p.k;
-    const int kbeg = SPLIT ? blockIdx.z * p.k_chunk : 0;
-    const int kend = SPLIT ? min(K, kbeg + p.k_chunk) : K;
+    const int kbeg = SPLIT != kWhole ? blockIdx.z * p.k_chunk : 0;
+    const int kend = SPLIT != kWhole ? min(K, kbeg + p.k_chunk) : K;
     const int nst  = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 
     const float* __restrict__ A = p.a;
@@ -257,36 +264,58 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_gemm(GemmParams p) {
         using Half = std::integral_constant<int, HK / 2>;
         using Full = std::integral_constant<int, HK>;
 
-        // Prologue: stages 0 and 1 in LDS, stage 2 in flight.
-        if (nst > 0) {
-            load_stage(kbeg);
-            store_stage(0);
-        }
-        if (nst > 1) {
-            load_stage(kbeg + BK);
-            store_stage(1);
-        }
-        if (nst > 2) load_stage(kbeg + 2 * BK);
-        __syncthreads();
-
-        Operands x, y;
-        if (nst > 0) read_operands(0, x);
-
-        auto iteration = [&](int st, Operands& cur, Operands& nxt) {
-            if (st + 1 < nst) read_operands((st + 1) % NBUF, nxt);
-            mfma_steps(cur, Zero{}, Half{});
-            if (st + 2 < nst) store_stage((st + 2) % NBUF);
-            if (st + 3 < nst) load_stage(kbeg + (st + 3) * BK);
-            mfma_steps(cur, Half{}, Full{});
+        if constexpr (NBUF == 3) {
+            // Prologue: stages 0 and 1 in LDS, stage 2 in flight.
+            if (nst > 0) {
+                load_stage(kbeg);
+                store_stage(0);
+            }
+            if (nst > 1) {
+                load_stage(kbeg + BK);
+                store_stage(1);
+            }
+            if (nst > 2) load_stage(kbeg + 2 * BK);
             __syncthreads();
-        };
 
-        int st = 0;
-        for (; st + 1 < nst; st += 2) {
-            iteration(st, x, y);
-            iteration(st + 1, y, x);
+            Operands x, y;
+            if (nst > 0) read_operands(0, x);
+
+            auto iteration = [&](int st, Operands& cur, Operands& nxt) {
+                if (st + 1 < nst) read_operands((st + 1) % NBUF, nxt);
+                mfma_steps(cur, Zero{}, Half{});
+                if (st + 2 < nst) store_stage((st + 2) % NBUF);
+                if (st + 3 < nst) load_stage(kbeg + (st + 3) * BK);
+                mfma_steps(cur, Half{}, Full{});
+                __syncthreads();
+            };
+
+            int st = 0;
+            for (; st + 1 < nst; st += 2) {
+                iteration(st, x, y);
+                iteration(st + 1, y, x);
+            }
+            if (st < nst) iteration(st, x, y);
+        } else {
+            // Two LDS stages, one operand set: the stage's operands are read
+            // at the top of the iteration (co-resident workgroups cover the
+            // read latency), stage s+1 is written mid-stream, stage s+2 loads
+            // are issued, one barrier.
+            if (nst > 0) {
+                load_stage(kbeg);
+                store_stage(0);
+            }
+            if (nst > 1) load_stage(kbeg + BK);
+            __syncthreads();
+            Operands x;
+            for (int st = 0; st < nst; ++st) {
+                read_operands(st & 1, x);
+                mfma_steps(x, Zero{}, Half{});
+                if (st + 1 < nst) store_stage((st + 1) & 1);
+                if (st + 2 < nst) load_stage(kbeg + (st + 2) * BK);
+                mfma_steps(x, Half{}, Full{});
+                __syncthreads();
+            }
         }
-        if (st < nst) iteration(st, x, y);
     };
 
     const bool interior = m0 + BM <= M && n0 + BN <= N && (kend - kbeg) % BK == 0;
@@ -308,10 +337,23 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_gemm(GemmParams p) {
             const int row = m0 + wrow + bi * 32 + 8 * (r / 4) + 4 * h + (r % 4);
             if (row >= M) continue;
             const size_t base = (size_t)row * N + col;
-            if constexpr (SPLIT) {
+            if constexpr (SPLIT == kAtomic) {
 #pragma unroll
                 for (int bj = 0; bj < TN; ++bj)
                     if (col + bj < N) unsafeAtomicAdd(D + base + bj, alpha * acc[bi][bj][r]);
+            } else if constexpr (SPLIT == kPartial) {
+                float* W = D + (size_t)blockIdx.z * M * N;
+                if constexpr (VEC && TN > 1) {
+                    if (col >= N) continue;
+                    BVec out;
+#pragma unroll
+                    for (int bj = 0; bj < TN; ++bj) out[bj] = acc[bi][bj][r];
+                    *reinterpret_cast<BVec*>(W + base) = out;
+                } else {
+#pragma unroll
+                    for (int bj = 0; bj < TN; ++bj)
+                        if (col + bj < N) W[base + bj] = acc[bi][bj][r];
+                }
             } else if constexpr (VEC) {
                 if (col >= N) continue;
                 BVec out;
@@ -341,11 +383,12 @@ __global__ __launch_bounds__(WM* WN * 64) void mfma_gemm(GemmParams p) {
 // Skinny-m streaming kernel (m <= 8).  Each workgroup covers 256 columns and
 // one k range; its 4 waves interleave over the k rows of that range, each
 // lane streaming 4 adjacent columns of b.  The waves' partial sums meet in
-// LDS and alpha*sum is added atomically into d (initialised by the
-// prologue).  Bound by the one pass over b.
+// LDS; alpha*sum is then added atomically into d (initialised by the
+// prologue) or, with PARTIAL, stored raw to slice z of the workspace for
+// splitk_reduce.  Bound by the one pass over b.
 // ----------------------------------------------------------------------------
 
-template <bool VEC>
+template <bool VEC, bool PARTIAL>
 __global__ __launch_bounds__(256) void gemv_splitk(GemmParams p) {
     const int tid  = threadIdx.x;
     const int lane = tid & 63;
@@ -404,7 +447,10 @@ __global__ __launch_bounds__(256) void gemv_splitk(GemmParams p) {
     if (col < N) {
         for (int i = 0; i < M; ++i) {
             const float s = part[0][i][tid] + part[1][i][tid] + part[2][i][tid] + part[3][i][tid];
-            unsafeAtomicAdd(p.d + (size_t)i * N + col, p.alpha * s);
+            if constexpr (PARTIAL)
+                p.d[(size_t)blockIdx.z * M * N + (size_t)i * N + col] = s;
+            else
+                unsafeAtomicAdd(p.d + (size_t)i * N + col, p.alpha * s);
         }
     }
 }
@@ -418,6 +464,41 @@ __global__ __launch_bounds__(256) void prologue(WideParams p) {
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride)
         p.d[i] = p.c != nullptr ? p.beta * p.c[i] : 0.f;
+}
+
+// ----------------------------------------------------------------------------
+// Split-k reduction: d = alpha * sum_{z < splits} W[z] + (c ? beta*c : 0),
+// summing the partial slices in increasing z (deterministic).  VEC: four
+// adjacent elements per thread (m*n % 4 == 0 and 16-byte aligned c, d, W).
+// ----------------------------------------------------------------------------
+template <bool VEC>
+__global__ __launch_bounds__(256) void splitk_reduce(ReduceParams p) {
+    const uint64_t total  = p.count;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    if constexpr (VEC) {
+        const floatx4* __restrict__ W = reinterpret_cast<const floatx4*>(p.partials);
+        const uint64_t vecs           = total / 4;
+        for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < vecs; i += stride) {
+            floatx4 s = W[i];
+            for (int z = 1; z < p.splits; ++z) s += W[(uint64_t)z * vecs + i];
+            floatx4 out = p.alpha * s;
+            if (p.c != nullptr) {
+                const floatx4 cv = reinterpret_cast<const floatx4*>(p.c)[i];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) out[j] = p.alpha * s[j] + p.beta * cv[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) out[j] = p.alpha * s[j] + 0.f;
+            }
+            reinterpret_cast<floatx4*>(p.d)[i] = out;
+        }
+    } else {
+        for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+            float s = p.partials[i];
+            for (int z = 1; z < p.splits; ++z) s += p.partials[(uint64_t)z * total + i];
+            p.d[i] = p.alpha * s + (p.c != nullptr ? p.beta * p.c[i] : 0.f);
+        }
+    }
 }
 
 // ----------------------------------------------------------------------------
@@ -487,23 +568,29 @@ __global__ __launch_bounds__(256) void simt_gemm(WideParams p) {
 
 const void* kernelFor(Variant v) {
     switch (v) {
-        case Variant::kMfma256x256: return reinterpret_cast<const void*>(&mfma_gemm<256, 256, 16, 2, 2, true, false>);
-        case Variant::kMfma256x256S: return reinterpret_cast<const void*>(&mfma_gemm<256, 256, 16, 2, 2, true, true>);
-        case Variant::kMfma128x128: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, true, false>);
-        case Variant::kMfma128x128S: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, true, true>);
-        case Variant::kMfma64x256: return reinterpret_cast<const void*>(&mfma_gemm<64, 256, 16, 1, 4, true, false>);
-        case Variant::kMfma64x256S: return reinterpret_cast<const void*>(&mfma_gemm<64, 256, 16, 1, 4, true, true>);
-        case Variant::kMfma256x64: return reinterpret_cast<const void*>(&mfma_gemm<256, 64, 16, 4, 1, true, false>);
-        case Variant::kMfma256x64S: return reinterpret_cast<const void*>(&mfma_gemm<256, 64, 16, 4, 1, true, true>);
-        case Variant::kMfma128x128U: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, false, false>);
-        case Variant::kMfma128x128US: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, false, true>);
-        case Variant::kGemvS: return reinterpret_cast<const void*>(&gemv_splitk<true>);
-        case Variant::kGemvUS: return reinterpret_cast<const void*>(&gemv_splitk<false>);
+        case Variant::kMfma256x256: return reinterpret_cast<const void*>(&mfma_gemm<256, 256, 16, 2, 2, 3, 1, true, kWhole>);
+        case Variant::kMfma256x256S: return reinterpret_cast<const void*>(&mfma_gemm<256, 256, 16, 2, 2, 3, 1, true, kPartial>);
+        case Variant::kMfma128x128: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, 3, 1, true, kWhole>);
+        case Variant::kMfma128x128S: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, 3, 1, true, kPartial>);
+        case Variant::kMfma64x256: return reinterpret_cast<const void*>(&mfma_gemm<64, 256, 16, 1, 4, 3, 1, true, kWhole>);
+        case Variant::kMfma64x256S: return reinterpret_cast<const void*>(&mfma_gemm<64, 256, 16, 1, 4, 3, 1, true, kPartial>);
+        case Variant::kMfma256x64: return reinterpret_cast<const void*>(&mfma_gemm<256, 64, 16, 4, 1, 3, 1, true, kWhole>);
+        case Variant::kMfma256x64S: return reinterpret_cast<const void*>(&mfma_gemm<256, 64, 16, 4, 1, 3, 1, true, kPartial>);
+        case Variant::kMfma64x64: return reinterpret_cast<const void*>(&mfma_gemm<64, 64, 16, 2, 2, 3, 1, true, kWhole>);
+        case Variant::kMfma64x64S: return reinterpret_cast<const void*>(&mfma_gemm<64, 64, 16, 2, 2, 3, 1, true, kPartial>);
+        case Variant::kMfma128x128U: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, 3, 1, false, kWhole>);
+        case Variant::kMfma128x128US: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, 3, 1, false, kPartial>);
+        case Variant::kGemvS: return reinterpret_cast<const void*>(&gemv_splitk<true, false>);
+        case Variant::kGemvUS: return reinterpret_cast<const void*>(&gemv_splitk<false, false>);
         case Variant::kSimt: return reinterpret_cast<const void*>(&simt_gemm);
         default: return nullptr;
     }
 }
 
 const void* prologueKernel() { return reinterpret_cast<const void*>(&prologue); }
+
+const void* reduceKernel(bool vec) {
+    return vec ? reinterpret_cast<const void*>(&splitk_reduce<true>) : reinterpret_cast<const void*>(&splitk_reduce<false>);
+}
 
 }  // namespace ftrain::gemm

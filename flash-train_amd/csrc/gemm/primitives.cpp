@@ -10,11 +10,14 @@
 #include <hip/hip_runtime.h>
 
 #include "ft/gemm.hpp"
+#include "ft/workspace.hpp"
 
 namespace ftrain {
 namespace {
 
 using gemm::GemmParams;
+using gemm::ReduceParams;
+using gemm::SplitKind;
 using gemm::Variant;
 using gemm::VariantInfo;
 using gemm::WideParams;
@@ -76,7 +79,7 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
         }
         if (info_->gemv && s.m > uint64_t(gemm::kGemvRows))
             return Result(FTRAIN_STATUS_UNSUPPORTED, "m exceeds the skinny-kernel row limit");
-        if (info_->split && !info_->gemv &&
+        if (info_->split == SplitKind::kPartial &&
             gemm::chooseSplits(v_, s, gemm::computeUnits(constraints.device())) == 0)
             return Result(FTRAIN_STATUS_UNSUPPORTED, "reduction depth too shallow to split");
         return Result{};
@@ -99,13 +102,13 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
         if (info_->simt) {
             const uint64_t tiles = ceilDiv(s.m, 64) * ceilDiv(s.n, 64);
             grid_                = dim3(static_cast<uint32_t>(std::min<uint64_t>(tiles, 1u << 20)));
-            args_[0]             = &wide_;
             return;
         }
-        const int cus        = gemm::computeUnits(getCurrentDeviceIdOr(0));
-        uint32_t splits      = info_->split ? gemm::chooseSplits(v_, s, cus) : 1;
-        uint64_t chunk       = s.k;
-        if (info_->split) {
+        const int cus   = gemm::computeUnits(getCurrentDeviceIdOr(0));
+        const bool split = info_->split != SplitKind::kNone;
+        uint32_t splits = split ? gemm::chooseSplits(v_, s, cus) : 1;
+        uint64_t chunk  = s.k;
+        if (split) {
             const uint64_t step = info_->gemv ? 1 : uint64_t(info_->bk);
             chunk               = ceilDiv(ceilDiv(s.k, splits), step) * step;
             splits              = chunk == 0 ? 1 : static_cast<uint32_t>(ceilDiv(s.k, chunk));
@@ -118,31 +121,61 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
             params_.tiles_n = int32_t(ceilDiv(s.n, info_->bn));
             grid_           = dim3(uint32_t(params_.tiles_m) * uint32_t(params_.tiles_n), 1, splits);
         }
-        args_[0] = &params_;
-        if (info_->split) {
-            prologue_args_[0] = &wide_;
-            prologue_grid_    = dim3(static_cast<uint32_t>(std::min<uint64_t>(ceilDiv(s.m * s.n, 256), 16384)));
+        const uint64_t count = s.m * s.n;
+        if (info_->split == SplitKind::kAtomic)
+            aux_grid_ = dim3(static_cast<uint32_t>(std::min<uint64_t>(ceilDiv(count, 256), 16384)));
+        if (info_->split == SplitKind::kPartial) {
+            partial_bytes_ = uint64_t(splits) * count * sizeof(float);
+            reduce_        = ReduceParams{nullptr, c, d, alpha, beta, count, int32_t(splits)};
+            reduce_vec_    = info_->vec && count % 4 == 0;
+            aux_grid_ = dim3(static_cast<uint32_t>(std::min<uint64_t>(ceilDiv(reduce_vec_ ? count / 4 : count, 256), 8192)));
         }
     }
 
   protected:
     void run(const Resources& r) override {
         if (empty_) return;
-        if (info_->split)
-            check(hipLaunchKernel(gemm::prologueKernel(), prologue_grid_, dim3(256), prologue_args_, 0, r.stream),
-                  "GEMM prologue");
-        check(hipLaunchKernel(kernel_, grid_, block_, args_, 0, r.stream), info_->name);
+        if (info_->simt) {
+            void* args[] = {&wide_};
+            check(hipLaunchKernel(kernel_, grid_, block_, args, 0, r.stream), info_->name);
+            return;
+        }
+        GemmParams params = params_;
+        void* args[]      = {&params};
+        switch (info_->split) {
+            case SplitKind::kNone:
+                check(hipLaunchKernel(kernel_, grid_, block_, args, 0, r.stream), info_->name);
+                break;
+            case SplitKind::kAtomic: {
+                void* pro[] = {&wide_};
+                check(hipLaunchKernel(gemm::prologueKernel(), aux_grid_, dim3(256), pro, 0, r.stream), "GEMM prologue");
+                check(hipLaunchKernel(kernel_, grid_, block_, args, 0, r.stream), info_->name);
+                break;
+            }
+            case SplitKind::kPartial: {
+                // Partial tiles go to the caller's workspace when it is large
+                // and aligned enough, else to a stream-ordered pool buffer.
+                const bool caller = r.workspace != nullptr && r.workspace_bytes >= partial_bytes_ &&
+                                    reinterpret_cast<uintptr_t>(r.workspace) % 16 == 0;
+                void* ws           = caller ? r.workspace : acquireWorkspace(partial_bytes_, r.stream);
+                params.d           = static_cast<float*>(ws);
+                ReduceParams red   = reduce_;
+                red.partials       = static_cast<const float*>(ws);
+                void* rargs[]      = {&red};
+                hipError_t e       = hipLaunchKernel(kernel_, grid_, block_, args, 0, r.stream);
+                if (e == hipSuccess)
+                    e = hipLaunchKernel(gemm::reduceKernel(reduce_vec_), aux_grid_, dim3(256), rargs, 0, r.stream);
+                if (!caller) releaseWorkspace(ws, r.stream);
+                check(e, info_->name);
+                break;
+            }
+        }
     }
 
   public:
     // clone() copies; the launch argument arrays must then point at the
     // copy's own parameter blocks.
-    GemmPrimitive(const GemmPrimitive& o)
-        : Primitive<GemmProblem>(o), v_(o.v_), info_(o.info_), empty_(o.empty_), kernel_(o.kernel_), grid_(o.grid_),
-          block_(o.block_), prologue_grid_(o.prologue_grid_), params_(o.params_), wide_(o.wide_) {
-        args_[0]          = info_->simt ? static_cast<void*>(&wide_) : static_cast<void*>(&params_);
-        prologue_args_[0] = &wide_;
-    }
+    GemmPrimitive(const GemmPrimitive&) = default;
     GemmPrimitive& operator=(const GemmPrimitive&) = delete;
 
   private:
@@ -153,13 +186,14 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
 
     Variant v_;
     const VariantInfo* info_;
-    bool empty_        = true;
+    bool empty_         = true;
     const void* kernel_ = nullptr;
-    dim3 grid_, block_, prologue_grid_;
+    dim3 grid_, block_, aux_grid_;
     GemmParams params_{};
     WideParams wide_{};
-    void* args_[1]          = {nullptr};
-    void* prologue_args_[1] = {nullptr};
+    ReduceParams reduce_{};
+    bool reduce_vec_        = false;
+    uint64_t partial_bytes_ = 0;
 };
 
 }  // namespace

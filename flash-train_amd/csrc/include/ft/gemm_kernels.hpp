@@ -38,6 +38,17 @@ struct WideParams {
     uint64_t m, n, k;
 };
 
+// Parameters of the split-k reduction (d = alpha * sum_z partials[z] + beta*c).
+struct ReduceParams {
+    const float* partials;  // splits slices of count floats
+    const float* c;         // may be null
+    float* d;
+    float alpha;
+    float beta;
+    uint64_t count;  // m * n
+    int32_t splits;
+};
+
 // Skinny-m kernel geometry: at most kGemvRows rows of a, kGemvCols output
 // columns per workgroup.
 constexpr int kGemvRows = 8;
@@ -45,7 +56,8 @@ constexpr int kGemvCols = 256;
 
 enum class Variant : int {
     // MFMA tiles, 128-bit global loads (needs k % 4 == 0, n % 4 == 0 and
-    // 16-byte aligned a/b/c/d).  Suffix S = split-k with atomic accumulation.
+    // 16-byte aligned a/b/c/d).  Suffix S = split-k: per-split partial tiles
+    // to a workspace, then a deterministic reduction kernel.
     kMfma256x256,
     kMfma256x256S,
     kMfma128x128,
@@ -54,15 +66,23 @@ enum class Variant : int {
     kMfma64x256S,
     kMfma256x64,
     kMfma256x64S,
+    kMfma64x64,
+    kMfma64x64S,
     // MFMA tiles with per-element loads/stores: any shape, 4-byte alignment.
     kMfma128x128U,
     kMfma128x128US,
-    // Skinny m (<= 8): streaming GEMV-style split-k.
+    // Skinny m (<= 8): streaming GEMV-style split-k with atomic accumulation.
     kGemvS,
     kGemvUS,
     // General SIMT kernel with 64-bit indexing.
     kSimt,
     kCount
+};
+
+enum class SplitKind : int {
+    kNone,     // one workgroup owns each output tile's whole reduction
+    kPartial,  // partial tiles to a workspace, then splitk_reduce
+    kAtomic,   // beta*c prologue, then fp32 atomic adds
 };
 
 struct VariantInfo {
@@ -71,16 +91,20 @@ struct VariantInfo {
     int threads;       // workgroup size
     int occupancy;     // workgroups expected to share one CU
     bool vec;          // needs 16-byte alignment and n % 4 == 0, k % 4 == 0
-    bool split;        // split-k with atomic adds after a beta*c prologue
+    SplitKind split;
     bool gemv;
     bool simt;
-    double efficiency; // fraction of the FP32 matrix peak the tile sustains (cost model)
+    double efficiency;  // fraction of the FP32 matrix peak the tile sustains (cost model)
 };
+
+// Largest split-k workspace (partial tiles) a Primitive will use.
+constexpr uint64_t kMaxPartialBytes = 256ull << 20;
 
 const VariantInfo& info(Variant v);
 
 // Device entry points (host-side stubs registered by the HIP TU).
 const void* kernelFor(Variant v);
-const void* prologueKernel();  // d = c ? beta*c : 0 over m*n elements (WideParams)
+const void* prologueKernel();            // d = c ? beta*c : 0 over m*n elements (WideParams)
+const void* reduceKernel(bool vec);      // split-k reduction (ReduceParams)
 
 }  // namespace ftrain::gemm
