@@ -48,6 +48,31 @@ def plan_overhead() -> dict | None:
         return {"error": str(e)}
 
 
+def torch_binding_overhead(iters: int = 2000) -> dict:
+    """Host microseconds per flash_train.torch.gemm call on BASELINE config 5e (127, 97, 33)."""
+    import torch
+
+    import flash_train.torch as ftt
+
+    g = torch.Generator().manual_seed(2026)
+    a = torch.randn(127, 33, generator=g).cuda()
+    b = torch.randn(33, 97, generator=g).cuda()
+    for _ in range(50):
+        ftt.gemm(a, b)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        ftt.gemm(a, b)
+    host = (time.perf_counter() - t0) / iters * 1e6
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(iters):
+        torch.matmul(a, b)
+    ref = (time.perf_counter() - t1) / iters * 1e6
+    torch.cuda.synchronize()
+    return {"flash_train_torch_gemm_host_us": round(host, 2), "torch_matmul_host_us": round(ref, 2), "iters": iters}
+
+
 def traffic_from_profiles(workload: str) -> float | None:
     """HBM bytes per launch of the workload's kernel: the committed rocprofv3 PMC figure
     (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration), if one exists."""
@@ -184,6 +209,8 @@ def main() -> None:
     roofline.update({"traffic": traffic_from_profiles(args.workload), "algorithmic_bytes": alg_bytes,
                      "algorithmic_flops": flops, "kernel_ms": round(ms, 4), "kernel": name})
     overhead = None if args.no_overhead else plan_overhead()
+    if overhead is not None and "error" not in overhead:
+        overhead["torch_binding"] = torch_binding_overhead()
 
     result = {
         "metric": METRIC,

@@ -6,6 +6,8 @@
 // status codes (Exception -> its status, bad_alloc -> OUT_OF_MEMORY, any
 // other exception -> INTERNAL_ERROR) and records the status and message as
 // the thread's last result (reference src/include/flash_train/api.hpp:37-62).
+#include <algorithm>
+#include <cstring>
 #include <exception>
 #include <new>
 #include <optional>
@@ -65,6 +67,83 @@ FTrainStatus setOperation(FTrainArgs args, uint64_t op, OperationKind kind, FTra
         args->args.setOperation(op, OperationAttributes{kind, compute_type});
     });
 }
+
+// Plans created by ftrainGemm, kept per thread and reused when a later call
+// describes exactly the same problem: the same six views (addresses, dims,
+// strides, types, placement), the same host alpha/beta values, compute type
+// and device.  A Plan binds exactly those values, so reuse is
+// indistinguishable from creating it again.  Least recently used entries are
+// destroyed beyond kCapacity.  Skipped when FTRAIN_DISABLE_CACHE is set.
+class ConveniencePlans {
+  public:
+    static constexpr std::size_t kCapacity = 32;
+
+    static ConveniencePlans& local() {
+        static thread_local ConveniencePlans cache;
+        return cache;
+    }
+
+    // Host scalars must be readable fp32 values of rank 0 for the key.
+    static bool describable(const FTrainStorageView* const views[6]) {
+        for (int i = 4; i < 6; ++i) {
+            const FTrainStorageView& v = *views[i];
+            if (v.memory == nullptr || v.num_dims != 0 || !v.is_host_memory ||
+                v.numeric_type != FTRAIN_NUMERIC_TYPE_FP32)
+                return false;
+        }
+        for (int i = 0; i < 4; ++i)
+            if (views[i]->num_dims != 0 && views[i]->dims == nullptr) return false;
+        return true;
+    }
+
+    static std::vector<uint64_t> describe(const FTrainStorageView* const views[6], FTrainNumericType compute_type,
+                                          int device) {
+        std::vector<uint64_t> k;
+        k.reserve(48);
+        k.push_back(uint64_t(uint32_t(device)));
+        k.push_back(compute_type);
+        for (int i = 0; i < 6; ++i) {
+            const FTrainStorageView& v = *views[i];
+            k.push_back(reinterpret_cast<uintptr_t>(v.memory));
+            k.push_back(uint64_t(v.num_dims) | uint64_t(v.numeric_type) << 8 | uint64_t(v.index_type) << 16 |
+                        uint64_t(v.is_host_memory) << 24 | uint64_t(v.strides != nullptr) << 25);
+            for (uint8_t j = 0; j < v.num_dims; ++j) k.push_back(uint64_t(v.dims[j]));
+            if (v.strides != nullptr)
+                for (uint8_t j = 0; j < v.num_dims; ++j) k.push_back(uint64_t(v.strides[j]));
+            if (i >= 4) {
+                uint32_t bits;
+                std::memcpy(&bits, v.memory, sizeof(bits));
+                k.push_back(bits);
+            }
+        }
+        return k;
+    }
+
+    FTrainPlan find(const std::vector<uint64_t>& key) {
+        for (std::size_t i = 0; i < entries_.size(); ++i) {
+            if (entries_[i].first == key) {
+                if (i != 0) std::rotate(entries_.begin(), entries_.begin() + i, entries_.begin() + i + 1);
+                return entries_.front().second;
+            }
+        }
+        return nullptr;
+    }
+
+    void insert(std::vector<uint64_t> key, FTrainPlan plan) {
+        entries_.insert(entries_.begin(), {std::move(key), plan});
+        while (entries_.size() > kCapacity) {
+            delete entries_.back().second;
+            entries_.pop_back();
+        }
+    }
+
+    ~ConveniencePlans() {
+        for (auto& e : entries_) delete e.second;
+    }
+
+  private:
+    std::vector<std::pair<std::vector<uint64_t>, FTrainPlan>> entries_;  // most recent first
+};
 
 }  // namespace
 }  // namespace ftrain
@@ -314,6 +393,18 @@ FTrainStatus ftrainGemm(FTrainStorageView a, FTrainStorageView b, FTrainStorageV
     }();
     if (entry.status != FTRAIN_STATUS_SUCCESS) return entry.status;
 
+    const FTrainStorageView* views[6] = {&a, &b, &c, &d, &alpha, &beta};
+    const bool cacheable              = !selectionCacheDisabled() && ConveniencePlans::describable(views);
+    int device                        = -1;
+    std::vector<uint64_t> key;
+    if (cacheable && hipGetDevice(&device) == hipSuccess) {
+        key = ConveniencePlans::describe(views, compute_type, device);
+        if (FTrainPlan cached = ConveniencePlans::local().find(key))
+            return ftrainPlanExecutePrimitive(cached, 0, workspace, workspace_bytes, stream);
+    } else {
+        (void)hipGetLastError();
+    }
+
     FTrainArgs args = nullptr;
     FTrainPlan plan = nullptr;
     FTrainStatus s  = ftrainArgsCreate(&args, entry.ops);
@@ -326,7 +417,12 @@ FTrainStatus ftrainGemm(FTrainStorageView a, FTrainStorageView b, FTrainStorageV
     if (s == FTRAIN_STATUS_SUCCESS) s = ftrainPlanExecutePrimitive(plan, 0, workspace, workspace_bytes, stream);
     // Keep the failing step's diagnostic across the clean-up calls.
     const Result failure = s != FTRAIN_STATUS_SUCCESS ? lastResult() : Result{};
-    if (plan != nullptr) ftrainPlanDestroy(plan);
+    if (plan != nullptr) {
+        if (s == FTRAIN_STATUS_SUCCESS && !key.empty())
+            ConveniencePlans::local().insert(std::move(key), plan);  // the cache now owns it
+        else
+            ftrainPlanDestroy(plan);
+    }
     if (args != nullptr) ftrainArgsDestroy(args);
     if (s != FTRAIN_STATUS_SUCCESS) lastResult() = failure;
     return s;

@@ -20,6 +20,7 @@ constexpr VariantInfo kInfo[] = {
     {"Fp32MfmaGemm_64x64_SplitK", 64, 64, 16, 256, 4, true, P, false, false, 0.50},
     {"Fp32MfmaGemm_128x128_Unaligned", 128, 128, 16, 256, 2, false, N, false, false, 0.70},
     {"Fp32MfmaGemm_128x128_Unaligned_SplitK", 128, 128, 16, 256, 2, false, P, false, false, 0.45},
+    {"Fp32MfmaGemm_64x64_Unaligned", 64, 64, 16, 256, 4, false, N, false, false, 0.45},
     {"Fp32Gemv_SplitK", kGemvRows, kGemvCols, 1, 256, 8, true, A, true, false, 0.0},
     {"Fp32Gemv_Unaligned_SplitK", kGemvRows, kGemvCols, 1, 256, 8, false, A, true, false, 0.0},
     {"Fp32Gemm", 64, 64, 16, 256, 2, false, N, false, true, 0.20},

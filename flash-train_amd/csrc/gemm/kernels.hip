@@ -580,6 +580,7 @@ const void* kernelFor(Variant v) {
         case Variant::kMfma64x64S: return reinterpret_cast<const void*>(&mfma_gemm<64, 64, 16, 2, 2, 3, 1, true, kPartial>);
         case Variant::kMfma128x128U: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, 3, 1, false, kWhole>);
         case Variant::kMfma128x128US: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, 3, 1, false, kPartial>);
+        case Variant::kMfma64x64U: return reinterpret_cast<const void*>(&mfma_gemm<64, 64, 16, 2, 2, 3, 1, false, kWhole>);
         case Variant::kGemvS: return reinterpret_cast<const void*>(&gemv_splitk<true, false>);
         case Variant::kGemvUS: return reinterpret_cast<const void*>(&gemv_splitk<false, false>);
         case Variant::kSimt: return reinterpret_cast<const void*>(&simt_gemm);

@@ -71,6 +71,7 @@ enum class Variant : int {
     // MFMA tiles with per-element loads/stores: any shape, 4-byte alignment.
     kMfma128x128U,
     kMfma128x128US,
+    kMfma64x64U,
     // Skinny m (<= 8): streaming GEMV-style split-k with atomic accumulation.
     kGemvS,
     kGemvUS,

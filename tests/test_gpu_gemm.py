@@ -306,3 +306,70 @@ def test_baseline_config_sampled_rows(capi, ops, oracle, name):
     err = (row_sums - want).abs().max().item()
     scale = want.abs().max().item() + np.sqrt(cfg["n"] * cfg["k"])
     assert err <= 1e-4 * np.sqrt(cfg["k"]) * scale, (name, err, scale)
+
+
+def test_convenience_calls_reuse_plans_without_changing_results(capi, oracle):
+    """ftrainGemm keeps recently used Plans; repeated calls must still honour
+    new buffer contents, new alpha/beta values and new addresses."""
+    m, n, k = 96, 80, 64
+    g = torch.Generator().manual_seed(3)
+    a_h, b_h, c_h = torch.randn(m, k, generator=g), torch.randn(k, n, generator=g), torch.randn(m, n, generator=g)
+    a, b, c = a_h.cuda(), b_h.cuda(), c_h.cuda()
+    d = torch.empty(m, n, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+
+    def call(alpha, beta, dd=d):
+        al, be = capi.HostScalar(alpha), capi.HostScalar(beta)
+        st = capi.gemm_status(capi.matrix(a), capi.matrix(b), capi.matrix(c), capi.matrix(dd), al.view, be.view,
+                              stream=s)
+        assert st == capi.SUCCESS, capi.last_message()
+        torch.cuda.synchronize()
+        return dd.cpu().numpy()
+
+    for alpha, beta in ((1.0, 0.0), (1.0, 0.0), (2.0, 0.5), (1.0, 0.0)):
+        rep = oracle.tolerance_check(call(alpha, beta), oracle.gemm_f64(a.cpu(), b.cpu(), c.cpu(), alpha, beta), k)
+        assert rep["ok"], (alpha, beta, rep)
+    a.mul_(-1.0)  # same addresses, new contents
+    rep = oracle.tolerance_check(call(1.0, 0.0), oracle.gemm_f64(a.cpu(), b.cpu(), c.cpu(), 1.0, 0.0), k)
+    assert rep["ok"], rep
+    d2 = torch.empty(m, n, device="cuda")  # new output address
+    rep = oracle.tolerance_check(call(1.0, 1.0, d2), oracle.gemm_f64(a.cpu(), b.cpu(), c.cpu(), 1.0, 1.0), k)
+    assert rep["ok"], rep
+
+
+def test_caller_workspace_is_used_for_split_k(capi, ops, oracle):
+    """A split-k Primitive takes its partial tiles from the caller's workspace
+    when one is passed, and from the library pool otherwise; results agree."""
+    m, n, k = 64, 512, 8192
+    g = torch.Generator().manual_seed(5)
+    a_h, b_h = torch.randn(m, k, generator=g), torch.randn(k, n, generator=g)
+    ref = oracle.gemm_f64(a_h, b_h)
+    d = torch.empty(m, n, device="cuda")
+    plan = capi.plan_for(a_h.cuda(), b_h.cuda(), None, d, 1.0, 0.0, ops)
+    split = [i for i, nm in enumerate(plan.names()) if nm.startswith("Fp32MfmaGemm") and nm.endswith("_SplitK")]
+    assert split, plan.names()
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    for i in split:
+        for workspace in (0, ws.data_ptr()):
+            d.fill_(float("nan"))
+            plan.execute(i, s, workspace, ws.numel() if workspace else 0)
+            torch.cuda.synchronize()
+            rep = oracle.tolerance_check(d.cpu().numpy(), ref, k)
+            assert rep["ok"], (plan.name(i), workspace != 0, rep)
+
+
+def test_split_k_is_deterministic(capi, ops):
+    m, n, k = 64, 1024, 16384
+    g = torch.Generator().manual_seed(9)
+    a, b = torch.randn(m, k, generator=g).cuda(), torch.randn(k, n, generator=g).cuda()
+    d = torch.empty(m, n, device="cuda")
+    plan = capi.plan_for(a, b, None, d, 1.0, 0.0, ops)
+    assert plan.name(0).endswith("_SplitK") and plan.name(0).startswith("Fp32MfmaGemm"), plan.names()
+    s = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for _ in range(3):
+        plan.execute(0, s)
+        torch.cuda.synchronize()
+        outs.append(d.clone())
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
