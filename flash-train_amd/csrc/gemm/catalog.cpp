@@ -8,10 +8,11 @@ namespace {
 // name, bm, bn, bk, threads, occupancy, vec, split, gemv, simt, efficiency
 constexpr SplitKind N = SplitKind::kNone, P = SplitKind::kPartial, A = SplitKind::kAtomic;
 constexpr VariantInfo kInfo[] = {
-    {"Fp32MfmaGemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, 0.84},
+    {"Fp32MfmaGemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, 0.85},
     {"Fp32MfmaGemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, 0.25},
-    {"Fp32MfmaGemm_128x128", 128, 128, 16, 256, 2, true, N, false, false, 0.80},
-    {"Fp32MfmaGemm_128x128_SplitK", 128, 128, 16, 256, 2, true, P, false, false, 0.55},
+    {"Fp32MfmaGemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, 0.84},
+    {"Fp32MfmaGemm_128x128", 128, 128, 16, 256, 3, true, N, false, false, 0.865},
+    {"Fp32MfmaGemm_128x128_SplitK", 128, 128, 16, 256, 3, true, P, false, false, 0.55},
     {"Fp32MfmaGemm_64x256", 64, 256, 16, 256, 2, true, N, false, false, 0.76},
     {"Fp32MfmaGemm_64x256_SplitK", 64, 256, 16, 256, 2, true, P, false, false, 0.55},
     {"Fp32MfmaGemm_256x64", 256, 64, 16, 256, 2, true, N, false, false, 0.76},

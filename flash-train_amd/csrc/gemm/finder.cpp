@@ -8,10 +8,10 @@
 // caches the surviving order per problem key.
 //
 // Model, per variant (microseconds):
-//   compute: workgroups = tiles * splits are issued in rounds of
-//            (CUs * occupancy); a round lasts one workgroup's MFMA work at
-//            the variant's sustained fraction of 256 FP32 matrix FLOP/clk/CU
-//            at 2.4 GHz, scaled by how many workgroups share a CU.
+//   compute: workgroups = tiles * splits; each CU runs ceil(wgs / CUs) of
+//            them back to back at the variant's sustained fraction of 256
+//            FP32 matrix FLOP/clk/CU at 2.4 GHz (lower while fewer than its
+//            resident-workgroup count are available).
 //   memory : algorithmic bytes (a, b, d, optional c) at 80% of 8 TB/s, plus
 //            the partial tiles (written and read once) for split-k with a
 //            reduction, or the beta*c prologue pass for atomic split-k.
@@ -68,6 +68,7 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
     double bytes      = 4.0 * (m * k + k * n + m * n * (has_c ? 2.0 : 1.0));
     double launch     = kLaunchMicros;
     double atomics_us = 0.0;
+    double serial_us  = 0.0;  // work in a second kernel that cannot overlap the first
     if (vi.split == SplitKind::kAtomic) {
         bytes += 4.0 * m * n * (has_c ? 2.0 : 1.0);  // prologue pass
         launch += kLaunchMicros;
@@ -76,27 +77,33 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
         // workgroups hit the same lines.
         atomics_us = m * n * double(splits) / kAtomicsPerMicro;
     } else if (vi.split == SplitKind::kPartial) {
-        bytes += 8.0 * m * n * double(splits);  // partial tiles written, then read by the reduction
+        // The GEMM kernel writes splits partial tiles instead of d; the
+        // reduction kernel then reads them (and c) and writes d.
+        bytes += 4.0 * m * n * (double(splits) - 1.0 - (has_c ? 1.0 : 0.0));
+        serial_us = 4.0 * m * n * (double(splits) + (has_c ? 2.0 : 1.0)) / kHbmBytesPerMicro;
         launch += kLaunchMicros + kPoolMicros;
     }
     if (vi.gemv) {
         const double wgs = double(ceilDiv(std::max<uint64_t>(s.n, 1), kGemvCols) * splits);
         const double fill = std::min(1.0, wgs / (double(cus) * 4.0));  // too few workgroups cannot reach HBM peak
-        return std::max(bytes / (kHbmBytesPerMicro * fill), atomics_us) + launch;
+        return std::max(bytes / (kHbmBytesPerMicro * fill), atomics_us) + serial_us + launch;
     }
-    // Work per workgroup includes the tile padding at the m/n edges.
+    // Work per workgroup includes the tile padding at the m/n edges.  The
+    // dispatcher refills a CU as soon as one of its workgroups retires, so a
+    // CU's load is its share of workgroups, ceil(wgs / CUs), each at the
+    // CU's sustained rate; below `occupancy` resident workgroups a CU runs
+    // correspondingly below that rate.
     const uint64_t chunk   = splits == 1 ? s.k : ceilDiv(ceilDiv(s.k, splits), vi.bk) * vi.bk;
     const uint64_t used    = chunk == 0 ? 1 : ceilDiv(s.k, chunk);
     const uint64_t tiles   = ceilDiv(s.m, vi.bm) * ceilDiv(s.n, vi.bn);
     const uint64_t wgs     = tiles * used;
-    const uint64_t slots   = uint64_t(cus) * vi.occupancy;
-    const uint64_t rounds  = ceilDiv(wgs, slots);
-    const uint64_t sharing = std::min<uint64_t>(vi.occupancy, ceilDiv(wgs, cus));
+    const uint64_t per_cu  = ceilDiv(wgs, cus);
+    const double fill      = std::sqrt(std::min(1.0, double(per_cu) / double(vi.occupancy)));
     const double depth     = double(std::max<uint64_t>(chunk, vi.bk));
     // SIMT FMAs run at half the matrix rate without packed FP32.
-    const double cu_rate   = kCuFlopPerMicro * vi.efficiency * (vi.simt ? 0.5 : 1.0);
-    const double per_round = 2.0 * vi.bm * vi.bn * depth * double(sharing) / cu_rate;
-    return std::max({double(rounds) * per_round, bytes / kHbmBytesPerMicro, atomics_us}) + launch;
+    const double cu_rate   = kCuFlopPerMicro * vi.efficiency * (vi.simt ? 0.5 : 1.0) * (vi.occupancy > 1 ? fill : 1.0);
+    const double compute   = double(per_cu) * 2.0 * vi.bm * vi.bn * depth / cu_rate;
+    return std::max({compute, bytes / kHbmBytesPerMicro, atomics_us}) + serial_us + launch;
 }
 
 }  // namespace

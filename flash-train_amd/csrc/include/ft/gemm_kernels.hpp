@@ -60,6 +60,7 @@ enum class Variant : int {
     // to a workspace, then a deterministic reduction kernel.
     kMfma256x256,
     kMfma256x256S,
+    kMfma256x128,
     kMfma128x128,
     kMfma128x128S,
     kMfma64x256,

@@ -450,9 +450,11 @@ def rank(tlib, m, n, k, addr=FAKE, with_c=False, device=0):
 
 
 def test_finder_choices_for_the_baseline_configs(tlib):
-    assert rank(tlib, 8192, 8192, 8192)[0] == "Fp32MfmaGemm_256x256"
-    assert rank(tlib, 16384, 14336, 4096)[0] == "Fp32MfmaGemm_256x256"
-    assert rank(tlib, 16384, 4096, 14336)[0] == "Fp32MfmaGemm_256x256"
+    assert rank(tlib, 8192, 8192, 8192)[0] == "Fp32MfmaGemm_128x128"
+    assert rank(tlib, 16384, 14336, 4096)[0] == "Fp32MfmaGemm_128x128"
+    assert rank(tlib, 16384, 4096, 14336)[0] == "Fp32MfmaGemm_128x128"
+    # 6144^3: 256x256 tiles would leave 2.25 tiles per CU; the 128x128 tile divides evenly.
+    assert rank(tlib, 6144, 6144, 6144)[0] == "Fp32MfmaGemm_128x128"
     assert rank(tlib, 4096, 4096, 4096, with_c=True)[0].startswith("Fp32MfmaGemm_")
     assert rank(tlib, 1, 8192, 8192)[0] == "Fp32Gemv_SplitK"
     assert rank(tlib, 256, 256, 65536)[0].endswith("_SplitK")
