@@ -93,11 +93,14 @@ def cpu_baseline(a, b, alpha: float, beta: float, budget_s: float) -> dict:
     k = a.shape[1]
     n = b.shape[1]
     a_np, b_np = a.numpy(), b.numpy()
+    # Two probes: the first (4 rows) also pays thread start-up, so it sizes a
+    # second ~1 s probe whose rate then sizes the sample to budget_s.
     rows = 4
-    t0 = time.perf_counter()
-    oracle.gemm_ref(a_np[:rows], b_np, None, alpha, beta)
-    dt = max(time.perf_counter() - t0, 1e-6)
-    rows = int(min(a.shape[0], max(rows, rows * budget_s / dt)))
+    for target_s in (1.0, budget_s):
+        t0 = time.perf_counter()
+        oracle.gemm_ref(a_np[:rows], b_np, None, alpha, beta)
+        dt = max(time.perf_counter() - t0, 1e-6)
+        rows = int(min(a.shape[0], max(rows, rows * target_s / dt)))
     t0 = time.perf_counter()
     oracle.gemm_ref(a_np[:rows], b_np, None, alpha, beta)
     dt = time.perf_counter() - t0
