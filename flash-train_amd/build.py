@@ -55,6 +55,9 @@ LIB_SOURCES = [
     "csrc/gemm/finder.cpp",
     "csrc/gemm/primitives.cpp",
     "csrc/gemm/kernels.hip",
+    "csrc/gemm/kernels_layout_tn.hip",
+    "csrc/gemm/kernels_layout_nt.hip",
+    "csrc/gemm/kernels_layout_tt.hip",
     "csrc/api/c_api.cpp",
 ]
 TESTING_SOURCES = ["csrc/api/testing_api.cpp"]

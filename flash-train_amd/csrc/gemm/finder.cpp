@@ -141,7 +141,9 @@ double estimateMicros(Variant v, const GemmShape& s, bool has_c, int cus) {
 }  // namespace gemm
 
 std::vector<std::string> ShapeCostFinder::candidates(const GemmProblem& problem, const Constraints& constraints) {
-    const GemmShape s = problem.shape();
+    // Rank on the shape the kernels run: a column-major d swaps m and n.
+    GemmLaunch g;
+    const GemmShape s = problem.launch(g) == nullptr ? g.shape : problem.shape();
     const int cus     = gemm::computeUnits(constraints.device());
     const bool has_c  = problem.c().memory() != nullptr;
     std::vector<std::pair<double, int>> ranked;

@@ -33,9 +33,13 @@ Result commonChecks(const GemmProblem& p) {
     for (int i = 0; i < 6; ++i)
         if (p.port(i).numericType() != FTRAIN_NUMERIC_TYPE_FP32)
             return Result(FTRAIN_STATUS_UNSUPPORTED, "an operand is not fp32");
-    for (int i = 0; i < 6; ++i)
+    // alpha and beta: continuous scalars.  a, b, c, d: continuous, or
+    // explicit strides with one unit dimension (GemmProblem::launch).
+    for (int i = 4; i < 6; ++i)
         if (p.port(i).indexType() != FTRAIN_INDEX_TYPE_CONTINUOUS)
             return Result(FTRAIN_STATUS_UNSUPPORTED, "an operand is not continuously indexed");
+    GemmLaunch g;
+    if (const char* why = p.launch(g)) return Result(FTRAIN_STATUS_UNSUPPORTED, why);
     for (int i = 0; i < 6; ++i)
         if (!floatAligned(p.port(i).memory()))
             return Result(FTRAIN_STATUS_UNSUPPORTED, "an operand address is not float-aligned");
@@ -62,7 +66,11 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
     Result isApplicable(const GemmProblem& p, const Constraints& constraints) const override {
         Result r = commonChecks(p);
         if (!r.isSuccess() || p.emptyOutput()) return r;
-        const GemmShape s = p.shape();
+        GemmLaunch g;
+        (void)p.launch(g);  // succeeded in commonChecks
+        const GemmShape s = g.shape;
+        if (gemm::kernelFor(v_, g.ta, g.tb) == nullptr)
+            return Result(FTRAIN_STATUS_UNSUPPORTED, "this variant has no kernel for these operand orientations");
         if (!info_->simt) {
             constexpr uint64_t kMax = std::numeric_limits<int32_t>::max();
             if (s.m > kMax || s.n > kMax || s.k > kMax)
@@ -71,8 +79,14 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
                 return Result(FTRAIN_STATUS_UNSUPPORTED, "the tile count exceeds the grid limit");
         }
         if (info_->vec) {
-            if (s.n % 4 != 0 || s.k % 4 != 0)
-                return Result(FTRAIN_STATUS_UNSUPPORTED, "n or k is not a multiple of 4 (128-bit loads)");
+            // 128-bit accesses along each matrix's contiguous dimension:
+            // that extent and every leading dimension a multiple of 4.
+            const uint64_t a_run = g.ta ? s.m : s.k, b_run = g.tb ? s.k : s.n;
+            if (s.n % 4 != 0 || a_run % 4 != 0 || b_run % 4 != 0)
+                return Result(FTRAIN_STATUS_UNSUPPORTED,
+                              "n or a contiguous matrix extent is not a multiple of 4 (128-bit loads)");
+            if (g.lda % 4 != 0 || g.ldb % 4 != 0 || g.ldc % 4 != 0 || g.ldd % 4 != 0)
+                return Result(FTRAIN_STATUS_UNSUPPORTED, "a leading dimension is not a multiple of 4 (128-bit loads)");
             for (int i = 0; i < 4; ++i)
                 if (!vecAligned(p.port(i).memory()))
                     return Result(FTRAIN_STATUS_UNSUPPORTED, "a matrix address is not 16-byte aligned");
@@ -86,18 +100,22 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
     }
 
     void configure(const GemmProblem& p) override {
-        const GemmShape s = p.shape();
-        empty_            = p.emptyOutput();
+        empty_ = p.emptyOutput();
+        if (empty_) return;
+        GemmLaunch g;
+        if (const char* why = p.launch(g)) throw Exception(FTRAIN_STATUS_UNSUPPORTED, "%s", why);
+        const GemmShape s = g.shape;
         const float alpha = *static_cast<const float*>(p.alpha().memory());
         const float beta  = *static_cast<const float*>(p.beta().memory());
-        const auto* a     = static_cast<const float*>(p.a().memory());
-        const auto* b     = static_cast<const float*>(p.b().memory());
-        const auto* c     = static_cast<const float*>(p.c().memory());
-        auto* d           = static_cast<float*>(p.d().memory());
-        wide_             = WideParams{a, b, c, d, alpha, beta, s.m, s.n, s.k};
-        if (empty_) return;
+        const auto* a     = static_cast<const float*>(g.a);
+        const auto* b     = static_cast<const float*>(g.b);
+        const auto* c     = static_cast<const float*>(g.c);
+        auto* d           = static_cast<float*>(g.d);
+        const int64_t a_rs = g.ta ? 1 : g.lda, a_cs = g.ta ? g.lda : 1;
+        const int64_t b_rs = g.tb ? 1 : g.ldb, b_cs = g.tb ? g.ldb : 1;
+        wide_ = WideParams{a, b, c, d, alpha, beta, s.m, s.n, s.k, a_rs, a_cs, b_rs, b_cs, g.ldc, g.ldd};
 
-        kernel_ = gemm::kernelFor(v_);
+        kernel_ = gemm::kernelFor(v_, g.ta, g.tb);
         block_  = dim3(info_->threads);
         if (info_->simt) {
             const uint64_t tiles = ceilDiv(s.m, 64) * ceilDiv(s.n, 64);
@@ -113,7 +131,8 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
             chunk               = ceilDiv(ceilDiv(s.k, splits), step) * step;
             splits              = chunk == 0 ? 1 : static_cast<uint32_t>(ceilDiv(s.k, chunk));
         }
-        params_ = GemmParams{a, b, c, d, alpha, beta, int32_t(s.m), int32_t(s.n), int32_t(s.k), int32_t(chunk), 0, 0};
+        params_ = GemmParams{a,      b,      c,     d,     alpha, beta,   int32_t(s.m), int32_t(s.n), int32_t(s.k),
+                             int32_t(chunk), 0, 0, g.lda, g.ldb, g.ldc, g.ldd};
         if (info_->gemv) {
             grid_ = dim3(static_cast<uint32_t>(ceilDiv(s.n, gemm::kGemvCols)), 1, splits);
         } else {
@@ -126,8 +145,9 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
             aux_grid_ = dim3(static_cast<uint32_t>(std::min<uint64_t>(ceilDiv(count, 256), 16384)));
         if (info_->split == SplitKind::kPartial) {
             partial_bytes_ = uint64_t(splits) * count * sizeof(float);
-            reduce_        = ReduceParams{nullptr, c, d, alpha, beta, count, int32_t(splits)};
-            reduce_vec_    = info_->vec && count % 4 == 0;
+            reduce_        = ReduceParams{nullptr, c, d, alpha, beta, count, s.n, g.ldc, g.ldd, int32_t(splits)};
+            // isApplicable guaranteed n, ldc, ldd % 4 == 0 and 16-byte bases for vec variants.
+            reduce_vec_    = info_->vec;
             aux_grid_ = dim3(static_cast<uint32_t>(std::min<uint64_t>(ceilDiv(reduce_vec_ ? count / 4 : count, 256), 8192)));
         }
     }

@@ -1,5 +1,6 @@
 // GemmProblem validation and selection key; GemmFamily pattern and Args
 // extraction.  Validation follows src/family/gemm/problem.cpp:13-56.
+#include <algorithm>
 #include <limits>
 
 #include "ft/gemm.hpp"
@@ -30,6 +31,62 @@ GemmProblem::GemmProblem(Tensor a, Tensor b, Tensor c, Tensor d, Tensor alpha, T
     const auto over          = [max_elems](uint64_t x, uint64_t y) { return y != 0 && x > max_elems / y; };
     if (over(s.m, s.k) || over(s.k, s.n) || over(s.m, s.n))
         throw Exception(FTRAIN_STATUS_OVERFLOW, "Gemm matrix byte size overflows uint64_t");
+}
+
+const char* matrixLayout(const StorageView& v, MatrixLayout& out) {
+    const int64_t r = v.dims()[0], c = v.dims()[1];
+    if (v.indexType() == FTRAIN_INDEX_TYPE_CONTINUOUS) {
+        out = MatrixLayout{false, std::max<int64_t>(c, 1)};
+        return nullptr;
+    }
+    if (v.indexType() != FTRAIN_INDEX_TYPE_INVALID) return "an operand is not continuously indexed";
+    const int64_t s0 = v.strides()[0], s1 = v.strides()[1];
+    if (s0 < 0 || s1 < 0) return "a matrix stride is negative";
+    const bool unit_cols = c <= 1 || s1 == 1;  // consecutive columns adjacent
+    const bool unit_rows = r <= 1 || s0 == 1;  // consecutive rows adjacent
+    if (unit_cols && (r <= 1 || s0 == c))
+        return "explicit strides restate the continuous layout (use FTRAIN_INDEX_TYPE_CONTINUOUS)";
+    // Largest element offset must stay addressable.
+    const int64_t max_off = std::numeric_limits<int64_t>::max() / int64_t(sizeof(double));
+    const auto span       = [max_off](int64_t n, int64_t s) { return n <= 1 ? 0 : (s > max_off / (n - 1) ? max_off : (n - 1) * s); };
+    if (span(r, s0) >= max_off || span(c, s1) >= max_off || span(r, s0) + span(c, s1) >= max_off)
+        return "a matrix extent overflows the address range";
+    if (unit_cols && s0 >= c) {
+        out = MatrixLayout{false, r <= 1 ? std::max<int64_t>(c, 1) : s0};
+        return nullptr;
+    }
+    if (unit_rows && (c <= 1 || s1 >= r)) {
+        out = MatrixLayout{true, c <= 1 ? std::max<int64_t>(r, 1) : s1};
+        return nullptr;
+    }
+    return "matrix strides need a unit stride in one dimension and a non-overlapping leading dimension";
+}
+
+const char* GemmProblem::launch(GemmLaunch& out) const {
+    MatrixLayout la, lb, lc, ld;
+    if (const char* why = matrixLayout(a_.view, la)) return why;
+    if (const char* why = matrixLayout(b_.view, lb)) return why;
+    if (const char* why = matrixLayout(c_.view, lc)) return why;
+    if (const char* why = matrixLayout(d_.view, ld)) return why;
+    const GemmShape s = shape();
+    const bool has_c  = c_.view.memory() != nullptr;
+    // A 1-row or 1-column matrix fits either orientation; take d's.
+    if (has_c && lc.col_major != ld.col_major) {
+        if (s.m <= 1 || s.n <= 1)
+            lc = MatrixLayout{ld.col_major, ld.col_major ? std::max<int64_t>(int64_t(s.m), 1) : std::max<int64_t>(int64_t(s.n), 1)};
+        else
+            return "c and d must share one orientation";
+    }
+    if (!ld.col_major) {
+        out = GemmLaunch{s, a_.view.memory(), b_.view.memory(), c_.view.memory(), d_.view.memory(),
+                         la.col_major, lb.col_major, la.ld, lb.ld, lc.ld, ld.ld};
+    } else {
+        // d^T (n x m, row-major with row stride ld) = b^T a^T + c^T.
+        out = GemmLaunch{GemmShape{s.n, s.m, s.k}, b_.view.memory(), a_.view.memory(), c_.view.memory(),
+                         d_.view.memory(), !lb.col_major, !la.col_major, lb.ld, la.ld, lc.ld, ld.ld};
+    }
+    if (!has_c) out.ldc = out.ldd;
+    return nullptr;
 }
 
 const StorageView& GemmProblem::port(int i) const noexcept {

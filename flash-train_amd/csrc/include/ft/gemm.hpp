@@ -22,6 +22,36 @@ struct GemmShape {
     uint64_t m, n, k;
 };
 
+// How a rank-2 matrix view is laid out in memory: element (i, j) sits at
+// i*ld + j (row-major) or i + j*ld (column-major).
+struct MatrixLayout {
+    bool col_major = false;
+    int64_t ld     = 0;
+};
+
+// Returns nullptr and fills `out` when the view is a layout the kernels can
+// read: FTRAIN_INDEX_TYPE_CONTINUOUS (row-major, ld = columns), or explicit
+// non-negative strides with a unit stride in one dimension and a leading
+// dimension that covers the other.  Otherwise returns the UNSUPPORTED reason.
+// Explicit strides that restate the continuous layout are rejected, as the
+// reference rejects every explicit-stride view
+// (src/primitive/hygon/gemm/fp32_gemm.cpp:39-46): callers name that layout
+// with the index type.
+const char* matrixLayout(const StorageView& view, MatrixLayout& out);
+
+// The problem rewritten for the kernels: a and b in either orientation, c
+// and d row-major.  A column-major d is computed as d^T = b^T a^T (m and n
+// swap, a and b swap and flip orientation).
+struct GemmLaunch {
+    GemmShape shape;
+    const void* a;
+    const void* b;
+    const void* c;
+    void* d;
+    bool ta, tb;  // a / b column-major
+    int64_t lda, ldb, ldc, ldd;
+};
+
 class GemmProblem {
   public:
     // Validates structure: rank-2 a/b/c/d, scalar alpha/beta, a/b/c/d in
@@ -46,6 +76,11 @@ class GemmProblem {
     const StorageView& alpha() const noexcept { return alpha_.view; }
     const StorageView& beta() const noexcept { return beta_.view; }
     bool inPlace() const noexcept { return c_.view.memory() == d_.view.memory(); }
+
+    // Fills `out` and returns nullptr, or returns the UNSUPPORTED reason
+    // (a matrix layout the kernels cannot read, or c and d in different
+    // orientations).
+    const char* launch(GemmLaunch& out) const;
 
     // Selection-cache tokens: everything that can change applicability or
     // the Finder's ranking -- per port: numeric type, index type, null-ness,

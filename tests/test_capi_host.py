@@ -405,7 +405,14 @@ def test_overflow(tlib, tops):
 @pytest.mark.parametrize("kw,why", [
     (dict(a=V([3, 2], numeric_type=c.FP16)), "an operand is not fp32"),
     (dict(b=V([2, 4], numeric_type=c.FP64)), "an operand is not fp32"),
-    (dict(a=V([3, 2], index_type=c.INDEX_INVALID, strides=[2, 1])), "continuously indexed"),
+    # The reference rejects every explicit-stride view (gemm_api_test.cpp:279-287); strides that only
+    # restate the continuous layout are still rejected here, other layouts are accepted below.
+    (dict(a=V([3, 2], index_type=c.INDEX_INVALID, strides=[2, 1])), "restate the continuous layout"),
+    (dict(a=V([3, 2], index_type=c.INDEX_GROUPED_CONTINUOUS)), "continuously indexed"),
+    (dict(a=V([3, 2], index_type=c.INDEX_INVALID, strides=[-2, 1])), "stride is negative"),
+    (dict(a=V([3, 2], index_type=c.INDEX_INVALID, strides=[4, 2])), "unit stride"),
+    (dict(a=V([3, 2], index_type=c.INDEX_INVALID, strides=[1, 2])), "unit stride"),  # columns overlap
+    (dict(d=V([3, 4], index_type=c.INDEX_INVALID, strides=[1, 3])), "one orientation"),
     (dict(compute=c.FP64), "compute type is not fp32"),
     (dict(a=V([3, 2], None)), "required operand address is null"),
     (dict(d=V([3, 4], None)), "required operand address is null"),
@@ -420,6 +427,43 @@ def test_unsupported_reasons_name_every_primitive(tlib, tops, kw, why):
     assert why in msg
     for v in range(tlib.ftrainTestingVariantCount()):
         assert tlib.ftrainTestingVariantName(v).decode() in msg
+
+
+def S(dims, strides, mem=FAKE):
+    """Explicit-stride device view."""
+    return c.View(mem, dims, index_type=c.INDEX_INVALID, strides=strides)
+
+
+@pytest.mark.parametrize("a,b,cc,d", [
+    (S([64, 32], [1, 64]), V([32, 48]), V([64, 48]), V([64, 48])),          # a column-major
+    (V([64, 32]), S([32, 48], [1, 32]), V([64, 48]), V([64, 48])),          # b column-major
+    (S([64, 32], [1, 64]), S([32, 48], [1, 32]), V([64, 48]), V([64, 48])),  # both
+    (S([64, 32], [40, 1]), S([32, 48], [52, 1]), S([64, 48], [56, 1]), S([64, 48], [60, 1])),  # padded rows
+    (V([64, 32]), V([32, 48]), S([64, 48], [1, 64]), S([64, 48], [1, 68])),  # c, d column-major
+    (V([64, 32]), V([32, 48]), V([64, 48], None), S([64, 48], [1, 64])),     # d column-major, no c
+])
+def test_strided_layouts_get_plans(tlib, tops, a, b, cc, d):
+    st, msg, plan = plan_status(tlib, tops, a, b, cc, d)
+    assert st == c.SUCCESS, msg
+    names = plan.names()
+    assert "Fp32Gemm" in names
+    # Variants built for row-major a and b only drop out when an operand is column-major.
+    if any(v.sv.index_type == c.INDEX_INVALID and v.sv.strides[0] == 1 for v in (a, b, d)):
+        assert "Fp32MfmaGemm_256x256" not in names
+    plan.close()
+
+
+def test_strided_alignment_rules(tlib, tops):
+    # Leading dimension not a multiple of 4: only per-element variants remain.
+    st, msg, plan = plan_status(tlib, tops, S([64, 32], [1, 65]), V([32, 48]), V([64, 48]), V([64, 48]))
+    assert st == c.SUCCESS, msg
+    assert all("Unaligned" in n or n == "Fp32Gemm" for n in plan.names()), plan.names()
+    plan.close()
+    # Column-major a with m % 4 != 0 cannot use 128-bit loads along m.
+    st, msg, plan = plan_status(tlib, tops, S([63, 32], [1, 64]), V([32, 48]), V([63, 48]), V([63, 48]))
+    assert st == c.SUCCESS, msg
+    assert all("Unaligned" in n or n == "Fp32Gemm" for n in plan.names()), plan.names()
+    plan.close()
 
 
 def test_empty_output_needs_no_storage(tlib, tops):
