@@ -136,6 +136,9 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="square_8192")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
+    ap.add_argument("--layout", default="nn", choices=("nn", "tn", "nt", "tt"),
+                    help="operand orientation: t = a (first letter) or b (second) stored column-major, "
+                         "passed with explicit strides")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-overhead", action="store_true", help="skip the cached-Plan host-overhead probe")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -167,7 +170,9 @@ def main() -> None:
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     a_h, b_h, c_h, cfg = oracle.seeded_inputs(args.workload)
     m, n, k = cfg["m"], cfg["n"], cfg["k"]
-    a, b = a_h.cuda(), b_h.cuda()
+    # Column-major operands: the transpose is stored contiguously and viewed back.
+    a = a_h.t().contiguous().cuda().t() if args.layout[0] == "t" else a_h.cuda()
+    b = b_h.t().contiguous().cuda().t() if args.layout[1] == "t" else b_h.cuda()
     c = c_h.cuda() if c_h is not None else None
     d = torch.empty(m, n, device="cuda")
     stream = torch.cuda.Stream()
@@ -228,7 +233,8 @@ def main() -> None:
         "vs_baseline": None,
         "dtype": "fp32",
         "data": "synthetic (seeded CPU torch.Generator 2026; BASELINE.json distributions)",
-        "config": {"workload": args.workload, "m": m, "n": n, "k": k, "alpha": cfg["alpha"], "beta": cfg["beta"],
+        "config": {"workload": args.workload, "layout": args.layout, "m": m, "n": n, "k": k,
+                   "alpha": cfg["alpha"], "beta": cfg["beta"],
                    "c": c is not None, "primitive": name, "parallelism": "single GPU"},
         "pct_of_fp32_matrix_peak": round(100.0 * tflops / FP32_MATRIX_PEAK_TFLOPS, 2),
         "roofline": roofline,

@@ -190,9 +190,14 @@ class View:
 
 
 def matrix(t: Optional[torch.Tensor], shape: Optional[Sequence[int]] = None, **kw) -> View:
-    """Device matrix view over a tensor (or a null-memory view of `shape`)."""
+    """Device matrix view over a tensor (or a null-memory view of `shape`).
+
+    A contiguous tensor gets FTRAIN_INDEX_TYPE_CONTINUOUS; a non-contiguous
+    one (a transpose, a column slice) its explicit element strides."""
     if t is None:
         return View(None, list(shape), **kw)
+    if not t.is_contiguous() and shape is None and "index_type" not in kw and "strides" not in kw:
+        return View(t.data_ptr(), list(t.shape), index_type=INDEX_INVALID, strides=list(t.stride()), **kw)
     return View(t.data_ptr(), list(shape) if shape is not None else list(t.shape), **kw)
 
 
