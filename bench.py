@@ -28,6 +28,7 @@ for _p in (PKG_ROOT, REPO):
         sys.path.insert(0, _p)
 
 FP32_MATRIX_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix (AMD spec)
+HALF_MATRIX_PEAK_TFLOPS = 2500.0  # MI355X dense BF16 / FP16 matrix (AMD spec, no sparsity)
 HBM_PEAK_GBS = 8000.0
 METRIC = "FP32 GEMM TFLOP/s and % of MFMA FP32 peak at 8192³; µs/call on cached Plan"
 
@@ -139,6 +140,8 @@ def main() -> None:
     ap.add_argument("--layout", default="nn", choices=("nn", "tn", "nt", "tt"),
                     help="operand orientation: t = a (first letter) or b (second) stored column-major, "
                          "passed with explicit strides")
+    ap.add_argument("--dtype", default="fp32", choices=("fp32", "bf16", "fp16"),
+                    help="element type of a and b (c and d stay fp32; accumulation is fp32)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-overhead", action="store_true", help="skip the cached-Plan host-overhead probe")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -170,6 +173,11 @@ def main() -> None:
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     a_h, b_h, c_h, cfg = oracle.seeded_inputs(args.workload)
     m, n, k = cfg["m"], cfg["n"], cfg["k"]
+    half = args.dtype != "fp32"
+    if half:
+        # The 16-bit inputs are the fp32 draws rounded; the parity reference uses the rounded values.
+        dt = torch.bfloat16 if args.dtype == "bf16" else torch.float16
+        a_h, b_h = a_h.to(dt), b_h.to(dt)
     # Column-major operands: the transpose is stored contiguously and viewed back.
     a = a_h.t().contiguous().cuda().t() if args.layout[0] == "t" else a_h.cuda()
     b = b_h.t().contiguous().cuda().t() if args.layout[1] == "t" else b_h.cuda()
@@ -199,22 +207,25 @@ def main() -> None:
     import numpy as np
 
     rows = np.sort(np.random.default_rng(1).choice(m, size=min(64, m), replace=False))
-    ref = oracle.sampled_rows_f64(a_h, b_h, c_h, cfg["alpha"], cfg["beta"], rows)
+    ref = oracle.sampled_rows_f64(a_h.float(), b_h.float(), c_h, cfg["alpha"], cfg["beta"], rows)
     rep = oracle.tolerance_check(d[torch.as_tensor(rows).cuda()].cpu().numpy(), ref, k)
 
     flops = 2.0 * m * n * k
     tflops = flops / (ms * 1e-3) / 1e12
-    alg_bytes = 4.0 * (m * k + k * n + m * n * (2 if c is not None else 1))
+    in_bytes = 2.0 if half else 4.0
+    alg_bytes = in_bytes * (m * k + k * n) + 4.0 * m * n * (2 if c is not None else 1)
+    peak_tflops = HALF_MATRIX_PEAK_TFLOPS if half else FP32_MATRIX_PEAK_TFLOPS
     gbs = alg_bytes / (ms * 1e-3) / 1e9
     # Roofline bound: arithmetic intensity against the ridge point (157.3 TFLOP/s / 8 TB/s).
-    hbm_bound = flops / alg_bytes < FP32_MATRIX_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+    hbm_bound = flops / alg_bytes < peak_tflops * 1e12 / (HBM_PEAK_GBS * 1e9)
     if hbm_bound:
         roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
     else:
-        roofline = {"bound": "mfma", "achieved": round(tflops, 3), "peak": FP32_MATRIX_PEAK_TFLOPS,
-                    "unit": "TFLOP/s", "frac": round(tflops / FP32_MATRIX_PEAK_TFLOPS, 4)}
-    roofline.update({"traffic": traffic_from_profiles(args.workload), "algorithmic_bytes": alg_bytes,
+        roofline = {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak_tflops,
+                    "unit": "TFLOP/s", "frac": round(tflops / peak_tflops, 4)}
+    traffic_key = args.workload + ("" if args.dtype == "fp32" and args.layout == "nn" else f"_{args.dtype}_{args.layout}")
+    roofline.update({"traffic": traffic_from_profiles(traffic_key), "algorithmic_bytes": alg_bytes,
                      "algorithmic_flops": flops, "kernel_ms": round(ms, 4), "kernel": name})
     overhead = None if args.no_overhead else plan_overhead()
     if overhead is not None and "error" not in overhead:
@@ -231,19 +242,19 @@ def main() -> None:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": args.dtype,
         "data": "synthetic (seeded CPU torch.Generator 2026; BASELINE.json distributions)",
         "config": {"workload": args.workload, "layout": args.layout, "m": m, "n": n, "k": k,
                    "alpha": cfg["alpha"], "beta": cfg["beta"],
                    "c": c is not None, "primitive": name, "parallelism": "single GPU"},
-        "pct_of_fp32_matrix_peak": round(100.0 * tflops / FP32_MATRIX_PEAK_TFLOPS, 2),
+        "pct_of_matrix_peak": round(100.0 * tflops / peak_tflops, 2),
         "roofline": roofline,
         "plan_overhead": overhead,
         "parity": {"rows_checked": int(len(rows)), "max_abs_err": rep["max_abs_err"], "bound": rep["bound"],
                    "ok": rep["ok"]},
         "wall_s_timed": round(wall, 3),
     }
-    if not args.no_cpu:
+    if not args.no_cpu and not half:
         result["cpu_baseline"] = cpu_baseline(a_h, b_h, cfg["alpha"], cfg["beta"], args.cpu_budget)
         result["cpu_torch_matmul"] = torch_cpu_matmul(a_h, b_h, min(args.cpu_budget, 5.0))
     print(json.dumps(result), flush=True)

@@ -58,6 +58,14 @@ LIB_SOURCES = [
     "csrc/gemm/kernels_layout_tn.hip",
     "csrc/gemm/kernels_layout_nt.hip",
     "csrc/gemm/kernels_layout_tt.hip",
+    "csrc/gemm/kernels_half_bf16_nn.hip",
+    "csrc/gemm/kernels_half_bf16_tn.hip",
+    "csrc/gemm/kernels_half_bf16_nt.hip",
+    "csrc/gemm/kernels_half_bf16_tt.hip",
+    "csrc/gemm/kernels_half_fp16_nn.hip",
+    "csrc/gemm/kernels_half_fp16_tn.hip",
+    "csrc/gemm/kernels_half_fp16_nt.hip",
+    "csrc/gemm/kernels_half_fp16_tt.hip",
     "csrc/api/c_api.cpp",
 ]
 TESTING_SOURCES = ["csrc/api/testing_api.cpp"]

@@ -33,7 +33,7 @@ namespace ftrain {
 namespace gemm {
 
 namespace {
-constexpr double kCuFlopPerMicro = 256.0 * 2.4e3;  // FP32 matrix FLOP per microsecond per CU
+constexpr double kClockPerMicro = 2.4e3;  // peak engine clock (MHz)
 constexpr double kHbmBytesPerMicro = 8.0e6 * 0.8;  // sustained HBM bytes per microsecond
 constexpr double kLaunchMicros = 4.0;
 constexpr double kAtomicsPerMicro = 6.0e4;
@@ -65,7 +65,9 @@ namespace {
 // Modelled time of variant `v` with a given split count (1 = no split).
 double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cus, uint64_t splits) {
     const double m = double(s.m), n = double(s.n), k = double(s.k);
-    double bytes      = 4.0 * (m * k + k * n + m * n * (has_c ? 2.0 : 1.0));
+    // a and b in the variant's input type; c and d counted at the same size.
+    const double eb   = vi.input == FTRAIN_NUMERIC_TYPE_FP32 ? 4.0 : 2.0;
+    double bytes      = eb * (m * k + k * n + m * n * (has_c ? 2.0 : 1.0));
     double launch     = kLaunchMicros;
     double atomics_us = 0.0;
     double serial_us  = 0.0;  // work in a second kernel that cannot overlap the first
@@ -101,7 +103,8 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
     const double fill      = std::sqrt(std::min(1.0, double(per_cu) / double(vi.occupancy)));
     const double depth     = double(std::max<uint64_t>(chunk, vi.bk));
     // SIMT FMAs run at half the matrix rate without packed FP32.
-    const double cu_rate   = kCuFlopPerMicro * vi.efficiency * (vi.simt ? 0.5 : 1.0) * (vi.occupancy > 1 ? fill : 1.0);
+    const double cu_rate   = vi.flop_per_clk * kClockPerMicro * vi.efficiency * (vi.simt ? 0.5 : 1.0) *
+                           (vi.occupancy > 1 ? fill : 1.0);
     const double compute   = double(per_cu) * 2.0 * vi.bm * vi.bn * depth / cu_rate;
     return std::max({compute, bytes / kHbmBytesPerMicro, atomics_us}) + serial_us + launch;
 }
@@ -148,6 +151,8 @@ std::vector<std::string> ShapeCostFinder::candidates(const GemmProblem& problem,
     const bool has_c  = problem.c().memory() != nullptr;
     std::vector<std::pair<double, int>> ranked;
     for (int i = 0; i < static_cast<int>(gemm::Variant::kCount); ++i) {
+        // Only variants for a's element type compete.
+        if (gemm::info(static_cast<gemm::Variant>(i)).input != problem.a().numericType()) continue;
         const double t = gemm::estimateMicros(static_cast<gemm::Variant>(i), s, has_c, cus);
         if (std::isfinite(t)) ranked.emplace_back(t, i);
     }

@@ -1,0 +1,384 @@
+// BF16 / FP16 MFMA tile kernel template (fp32 accumulation), shared by the
+// per-type, per-layout HIP translation units kernels_half_*.hip.  Device
+// code only.
+//
+// d = alpha * (a @ b) + beta * c with a, b in bf16 or fp16 (one type for
+// both), products accumulated in fp32, the epilogue evaluated in fp32, and
+// c / d either fp32 or the input type (rounded to nearest even).  The
+// reference's numeric-type enum names both input types
+// (include/flash_train/common.h:38-65); its only kernel is fp32
+// (src/primitive/hygon/gemm/fp32_gemm.hip:18-31), whose semantics this
+// follows: with a null c the beta term is dropped, with a non-null c it is
+// always evaluated.
+//
+// MFMA: v_mfma_f32_32x32x16_{bf16,f16} (gfx950).  One instruction multiplies
+// a 32x16 block of A by a 16x32 block of B into a 32x32 fp32 block:
+//   A operand: lane l holds 8 values A[row = l % 32][one k group of 8]
+//   B operand: lane l holds 8 values B[same k group][col = l % 32]
+//   result   : lane l, register r holds D[row = 8*(r/4) + 4*(l/32) + r%4][col = l % 32]
+// The k group of lane half h = l / 32 at step s is assigned
+// k = h*BK/2 + 8*s + (0..7): the pairing only has to agree between A and B,
+// and this choice makes each lane's operand one 16-byte LDS read.
+//
+// LDS: both tiles are stored k-contiguous, [BM][BK + 8] for A and
+// [BN][BK + 8] for B.  The 8-element pad makes the row stride 36 dwords, so
+// the 16 lanes of one 128-bit read pass (consecutive rows) hit 16 disjoint
+// 4-bank groups.
+//
+// Global -> LDS, per operand orientation:
+//   k-contiguous in memory (row-major a, column-major b): 16-byte loads of 8
+//     consecutive k, written to LDS as they are;
+//   row/column-contiguous (column-major a, row-major b): each thread loads an
+//     8 x 8 block as 8 rows of 8 consecutive m (or n) at consecutive k,
+//     transposes it in registers with 16-bit shuffles (v_perm_b32), and writes
+//     8 k-contiguous vectors.
+// Consecutive threads walk each matrix's contiguous dimension, so the loads
+// stay coalesced for every orientation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "ft/gemm_kernels.hpp"
+
+namespace ftrain::gemm::hdev {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+
+enum SplitMode : int { kWhole = 0, kPartial = 2 };
+
+// 16-bit storage <-> fp32.
+template <bool BF16>
+__device__ __forceinline__ float to_float(unsigned short v) {
+    if constexpr (BF16)
+        return __builtin_bit_cast(float, static_cast<unsigned int>(v) << 16);
+    else
+        return static_cast<float>(__builtin_bit_cast(_Float16, v));
+}
+template <bool BF16>
+__device__ __forceinline__ unsigned short from_float(float v) {
+    // Round to nearest even (the compiler's conversions; NaN stays NaN).
+    if constexpr (BF16)
+        return __builtin_bit_cast(unsigned short, static_cast<__bf16>(v));
+    else
+        return __builtin_bit_cast(unsigned short, static_cast<_Float16>(v));
+}
+
+template <bool BF16>
+__device__ __forceinline__ floatx16 mfma(u32x4 a, u32x4 b, floatx16 acc) {
+    if constexpr (BF16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       acc, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(halfx8, a), __builtin_bit_cast(halfx8, b),
+                                                      acc, 0, 0, 0);
+}
+
+// Transposes an 8 x 8 block of 16-bit values held as 8 vectors (v[i] =
+// row i, elements 0..7) into w[j] = column j (elements v[0][j] .. v[7][j]).
+__device__ __forceinline__ void transpose8x8(const u32x4 (&v)[8], u32x4 (&w)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            // w[j] dword q = (v[2q][j], v[2q+1][j]): low half from row 2q.
+            // Element j of a row sits in dword j/2, low half when j is even.
+            // (The compiler turns each pair into one v_perm_b32.)
+            const unsigned int lo = v[2 * q][j / 2], hi = v[2 * q + 1][j / 2];
+            w[j][q] = (j & 1) ? (lo >> 16) | (hi & 0xFFFF0000u) : (lo & 0xFFFFu) | (hi << 16);
+        }
+}
+
+// Same XCD-aware tile order as the fp32 kernels: each XCD (workgroup id mod
+// 8) receives a contiguous range of tiles, walked in bands of 8 tile rows.
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int tiles = tiles_m * tiles_n;
+    const int per   = tiles >> 3;
+    int t           = bid;
+    if (bid < (per << 3)) t = (bid & 7) * per + (bid >> 3);
+    constexpr int kBand = 8;
+    const int band_span = kBand * tiles_n;
+    const int band      = t / band_span;
+    const int first_m   = band * kBand;
+    const int band_rows = min(tiles_m - first_m, kBand);
+    const int within    = t - band * band_span;
+    tm                  = first_m + within % band_rows;
+    tn                  = within / band_rows;
+}
+
+// ----------------------------------------------------------------------------
+// BM x BN tile, BK k per stage, WM x WN waves (each (BM/WM) x (BN/WN) of
+// 32x32 blocks), two LDS stages, one barrier per stage.  VEC: 16-byte global
+// accesses (bases 16-byte aligned, leading dimensions and each matrix's
+// contiguous extent multiples of 8); otherwise per-element loads, any shape.
+// SPLIT: kWhole writes d; kPartial writes the raw fp32 partial tile to slice
+// z of the workspace (dense m x n) for splitk_reduce.
+// ----------------------------------------------------------------------------
+template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, int SPLIT, bool TA, bool TB>
+__global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p) {
+    using u16           = unsigned short;
+    constexpr int NT    = WM * WN * 64;
+    constexpr int WTM   = BM / WM;
+    constexpr int WTN   = BN / WN;
+    constexpr int TM    = WTM / 32;
+    constexpr int TN    = WTN / 32;
+    constexpr int STEPS = BK / 16;  // MFMA k-steps per stage
+    constexpr int SK    = BK + 8;   // LDS row stride (elements)
+    static_assert(TM >= 1 && TN >= 1 && BK % 16 == 0, "tile");
+
+    __shared__ __attribute__((aligned(16))) u16 As[2][BM * SK];
+    __shared__ __attribute__((aligned(16))) u16 Bs[2][BN * SK];
+
+    const int tid  = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int li   = lane & 31;
+    const int h    = lane >> 5;
+    const int wrow = (wave / WN) * WTM;
+    const int wcol = (wave % WN) * WTN;
+
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int M = p.m, N = p.n, K = p.k;
+    const int kbeg = SPLIT != kWhole ? blockIdx.z * p.k_chunk : 0;
+    const int kend = SPLIT != kWhole ? min(K, kbeg + p.k_chunk) : K;
+    const int nst  = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+
+    const u16* __restrict__ A = static_cast<const u16*>(p.a);
+    const u16* __restrict__ B = static_cast<const u16*>(p.b);
+    const size_t lda = p.lda, ldb = p.ldb;
+
+    // Element (r, k) of a and (k, c) of b in global memory.
+    auto a_at = [&](int gm, int gk) { return A + (TA ? (size_t)gk * lda + gm : (size_t)gm * lda + gk); };
+    auto b_at = [&](int gk, int gn) { return B + (TB ? (size_t)gn * ldb + gk : (size_t)gk * ldb + gn); };
+
+    // Staging registers.  VEC, k-contiguous operand: ROWS*BK/8 vectors of 8 k;
+    // VEC, transposed operand: ROWS*BK/64 blocks of 8 x 8; scalar: ROWS*BK
+    // elements.  Threads beyond the count idle for that operand.
+    constexpr int A_VECS = VEC ? (TA ? BM * BK / 64 : BM * BK / 8) : 0;
+    constexpr int B_VECS = VEC ? (TB ? BN * BK / 8 : BN * BK / 64) : 0;
+    constexpr int A_PER  = VEC ? (A_VECS + NT - 1) / NT : BM * BK / NT;
+    constexpr int B_PER  = VEC ? (B_VECS + NT - 1) / NT : BN * BK / NT;
+    constexpr int A_REGS = VEC && TA ? 8 : 1;   // vectors per staging slot
+    constexpr int B_REGS = VEC && !TB ? 8 : 1;
+    static_assert(VEC || (BM * BK % NT == 0 && BN * BK % NT == 0), "scalar staging");
+    u32x4 ra[VEC ? A_PER : 1][A_REGS];
+    u32x4 rb[VEC ? B_PER : 1][B_REGS];
+    u16 sa[VEC ? 1 : A_PER];
+    u16 sb[VEC ? 1 : B_PER];
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const u32x4 zero4 = u32x4{0u, 0u, 0u, 0u};
+
+    auto main_loop = [&](auto checked_tag) {
+        constexpr bool CHECKED = decltype(checked_tag)::value;
+
+        // Global loads of one stage (k range [k0, k0 + BK)) into registers.
+        auto load_stage = [&](int k0) {
+            if constexpr (VEC) {
+#pragma unroll
+                for (int j = 0; j < A_PER; ++j) {
+                    const int idx = tid + j * NT;
+                    if (A_VECS % NT != 0 && idx >= A_VECS) continue;
+                    if constexpr (!TA) {  // (r, 8 k) vectors, 8 threads per row of BK = 64
+                        const int r = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
+                        const int gm = m0 + r, gk = k0 + kq;
+                        ra[j][0] = zero4;
+                        if (!CHECKED || (gm < M && gk < kend)) ra[j][0] = *reinterpret_cast<const u32x4*>(a_at(gm, gk));
+                    } else {  // 8 x 8 blocks: 8 consecutive m at k = kb..kb+7
+                        const int r = 8 * (idx % (BM / 8)), kb = 8 * (idx / (BM / 8));
+                        const int gm = m0 + r;
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            const int gk = k0 + kb + i;
+                            ra[j][i]     = zero4;
+                            if (!CHECKED || (gm < M && gk < kend))
+                                ra[j][i] = *reinterpret_cast<const u32x4*>(a_at(gm, gk));
+                        }
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < B_PER; ++j) {
+                    const int idx = tid + j * NT;
+                    if (B_VECS % NT != 0 && idx >= B_VECS) continue;
+                    if constexpr (TB) {  // (c, 8 k) vectors
+                        const int c = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
+                        const int gn = n0 + c, gk = k0 + kq;
+                        rb[j][0] = zero4;
+                        if (!CHECKED || (gn < N && gk < kend)) rb[j][0] = *reinterpret_cast<const u32x4*>(b_at(gk, gn));
+                    } else {  // 8 x 8 blocks: 8 consecutive n at k = kb..kb+7
+                        const int c = 8 * (idx % (BN / 8)), kb = 8 * (idx / (BN / 8));
+                        const int gn = n0 + c;
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            const int gk = k0 + kb + i;
+                            rb[j][i]     = zero4;
+                            if (!CHECKED || (gn < N && gk < kend))
+                                rb[j][i] = *reinterpret_cast<const u32x4*>(b_at(gk, gn));
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < A_PER; ++j) {
+                    const int idx = tid + j * NT;
+                    const int r = TA ? idx % BM : idx / BK, k = TA ? idx / BM : idx % BK;
+                    const int gm = m0 + r, gk = k0 + k;
+                    sa[j]        = (!CHECKED || (gm < M && gk < kend)) ? *a_at(gm, gk) : u16(0);
+                }
+#pragma unroll
+                for (int j = 0; j < B_PER; ++j) {
+                    const int idx = tid + j * NT;
+                    const int c = TB ? idx / BK : idx % BN, k = TB ? idx % BK : idx / BN;
+                    const int gn = n0 + c, gk = k0 + k;
+                    sb[j]        = (!CHECKED || (gk < kend && gn < N)) ? *b_at(gk, gn) : u16(0);
+                }
+            }
+        };
+
+        // Registers -> LDS buffer `buf` (k-contiguous rows).
+        auto store_stage = [&](int buf) {
+            if constexpr (VEC) {
+#pragma unroll
+                for (int j = 0; j < A_PER; ++j) {
+                    const int idx = tid + j * NT;
+                    if (A_VECS % NT != 0 && idx >= A_VECS) continue;
+                    if constexpr (!TA) {
+                        const int r = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
+                        *reinterpret_cast<u32x4*>(&As[buf][r * SK + kq]) = ra[j][0];
+                    } else {
+                        const int r = 8 * (idx % (BM / 8)), kb = 8 * (idx / (BM / 8));
+                        u32x4 w[8];
+                        transpose8x8(ra[j], w);
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(&As[buf][(r + i) * SK + kb]) = w[i];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < B_PER; ++j) {
+                    const int idx = tid + j * NT;
+                    if (B_VECS % NT != 0 && idx >= B_VECS) continue;
+                    if constexpr (TB) {
+                        const int c = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
+                        *reinterpret_cast<u32x4*>(&Bs[buf][c * SK + kq]) = rb[j][0];
+                    } else {
+                        const int c = 8 * (idx % (BN / 8)), kb = 8 * (idx / (BN / 8));
+                        u32x4 w[8];
+                        transpose8x8(rb[j], w);
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(&Bs[buf][(c + i) * SK + kb]) = w[i];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < A_PER; ++j) {
+                    const int idx = tid + j * NT;
+                    const int r = TA ? idx % BM : idx / BK, k = TA ? idx / BM : idx % BK;
+                    As[buf][r * SK + k] = sa[j];
+                }
+#pragma unroll
+                for (int j = 0; j < B_PER; ++j) {
+                    const int idx = tid + j * NT;
+                    const int c = TB ? idx / BK : idx % BN, k = TB ? idx % BK : idx / BN;
+                    Bs[buf][c * SK + k] = sb[j];
+                }
+            }
+        };
+
+        // All MFMAs of one stage; operands of step s+1 are read while step
+        // s's MFMAs run (the compiler hoists the reads of the unrolled loop).
+        auto compute_stage = [&](int buf) {
+#pragma unroll
+            for (int s = 0; s < STEPS; ++s) {
+                const int kk = h * (BK / 2) + 8 * s;
+                u32x4 av[TM], bv[TN];
+#pragma unroll
+                for (int bi = 0; bi < TM; ++bi)
+                    av[bi] = *reinterpret_cast<const u32x4*>(&As[buf][(wrow + bi * 32 + li) * SK + kk]);
+#pragma unroll
+                for (int bj = 0; bj < TN; ++bj)
+                    bv[bj] = *reinterpret_cast<const u32x4*>(&Bs[buf][(wcol + bj * 32 + li) * SK + kk]);
+#pragma unroll
+                for (int bi = 0; bi < TM; ++bi)
+#pragma unroll
+                    for (int bj = 0; bj < TN; ++bj) acc[bi][bj] = mfma<BF16>(av[bi], bv[bj], acc[bi][bj]);
+            }
+        };
+
+        if (nst > 0) {
+            load_stage(kbeg);
+            store_stage(0);
+        }
+        __syncthreads();
+        for (int st = 0; st < nst; ++st) {
+            if (st + 1 < nst) load_stage(kbeg + (st + 1) * BK);
+            compute_stage(st & 1);
+            if (st + 1 < nst) store_stage((st + 1) & 1);
+            __syncthreads();
+        }
+    };
+
+    const bool interior = m0 + BM <= M && n0 + BN <= N && (kend - kbeg) % BK == 0;
+    if (interior)
+        main_loop(std::false_type{});
+    else
+        main_loop(std::true_type{});
+
+    // Epilogue: lane li owns column wcol + bj*32 + li of each block; c and d
+    // are row-major (row strides ldc, ldd) in fp32 or the input type.
+    const float alpha = p.alpha, beta = p.beta;
+#pragma unroll
+    for (int bi = 0; bi < TM; ++bi)
+#pragma unroll
+        for (int bj = 0; bj < TN; ++bj) {
+            const int col = n0 + wcol + bj * 32 + li;
+            if (col >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wrow + bi * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+                if (row >= M) continue;
+                if constexpr (SPLIT == kPartial) {
+                    static_cast<float*>(p.d)[(size_t)blockIdx.z * M * N + (size_t)row * N + col] = acc[bi][bj][r];
+                } else {
+                    const size_t ci = (size_t)row * p.ldc + col, di = (size_t)row * p.ldd + col;
+                    float cv = 0.f;
+                    if (p.c != nullptr)
+                        cv = p.cd_half ? to_float<BF16>(static_cast<const u16*>(p.c)[ci]) : static_cast<const float*>(p.c)[ci];
+                    const float out = alpha * acc[bi][bj][r] + (p.c != nullptr ? beta * cv : 0.f);
+                    if (p.cd_half)
+                        static_cast<u16*>(p.d)[di] = from_float<BF16>(out);
+                    else
+                        static_cast<float*>(p.d)[di] = out;
+                }
+            }
+        }
+}
+
+// The half-precision tiles (index as in kHalfTiles) for one input type and
+// one operand orientation.
+template <bool BF16, bool TA, bool TB>
+const void* halfKernel(int tile) {
+    switch (tile) {
+        case 0: return reinterpret_cast<const void*>(&half_gemm<BF16, 256, 256, 64, 2, 2, 1, true, kWhole, TA, TB>);
+        case 1: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kWhole, TA, TB>);
+        case 2: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kPartial, TA, TB>);
+        case 3: return reinterpret_cast<const void*>(&half_gemm<BF16, 64, 64, 32, 2, 2, 2, false, kWhole, TA, TB>);
+        default: return nullptr;
+    }
+}
+
+}  // namespace ftrain::gemm::hdev

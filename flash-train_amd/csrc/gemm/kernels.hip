@@ -118,12 +118,32 @@ __global__ __launch_bounds__(256) void prologue(WideParams p) {
 // four adjacent elements per thread (n, ldc, ldd multiples of 4 and 16-byte
 // aligned c, d, W).
 // ----------------------------------------------------------------------------
+__device__ __forceinline__ float load_cd(const void* p, uint64_t i, int32_t type) {
+    if (type == kCdFp32) return static_cast<const float*>(p)[i];
+    const unsigned short v = static_cast<const unsigned short*>(p)[i];
+    if (type == kCdBf16) return __builtin_bit_cast(float, static_cast<unsigned int>(v) << 16);
+    return static_cast<float>(__builtin_bit_cast(_Float16, v));
+}
+
+__device__ __forceinline__ void store_cd(void* p, uint64_t i, int32_t type, float x) {
+    // Half types round to nearest even (the compiler's conversions).
+    if (type == kCdFp32)
+        static_cast<float*>(p)[i] = x;
+    else if (type == kCdBf16)
+        static_cast<unsigned short*>(p)[i] = __builtin_bit_cast(unsigned short, static_cast<__bf16>(x));
+    else
+        static_cast<unsigned short*>(p)[i] = __builtin_bit_cast(unsigned short, static_cast<_Float16>(x));
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(256) void splitk_reduce(ReduceParams p) {
     const uint64_t total  = p.count;
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     if constexpr (VEC) {
+        // fp32 c and d only.
         const floatx4* __restrict__ W = reinterpret_cast<const floatx4*>(p.partials);
+        const float* C                = static_cast<const float*>(p.c);
+        float* D                      = static_cast<float*>(p.d);
         const uint64_t vecs           = total / 4;
         const uint64_t row_vecs       = p.n / 4;
         for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < vecs; i += stride) {
@@ -131,22 +151,23 @@ __global__ __launch_bounds__(256) void splitk_reduce(ReduceParams p) {
             floatx4 s = W[i];
             for (int z = 1; z < p.splits; ++z) s += W[(uint64_t)z * vecs + i];
             floatx4 out;
-            if (p.c != nullptr) {
-                const floatx4 cv = *reinterpret_cast<const floatx4*>(p.c + r * p.ldc + c);
+            if (C != nullptr) {
+                const floatx4 cv = *reinterpret_cast<const floatx4*>(C + r * p.ldc + c);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) out[j] = p.alpha * s[j] + p.beta * cv[j];
             } else {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) out[j] = p.alpha * s[j] + 0.f;
             }
-            *reinterpret_cast<floatx4*>(p.d + r * p.ldd + c) = out;
+            *reinterpret_cast<floatx4*>(D + r * p.ldd + c) = out;
         }
     } else {
         for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
             const uint64_t r = i / p.n, c = i - r * p.n;
             float s = p.partials[i];
             for (int z = 1; z < p.splits; ++z) s += p.partials[(uint64_t)z * total + i];
-            p.d[r * p.ldd + c] = p.alpha * s + (p.c != nullptr ? p.beta * p.c[r * p.ldc + c] : 0.f);
+            const float out = p.alpha * s + (p.c != nullptr ? p.beta * load_cd(p.c, r * p.ldc + c, p.cd_type) : 0.f);
+            store_cd(p.d, r * p.ldd + c, p.cd_type, out);
         }
     }
 }
@@ -218,6 +239,15 @@ __global__ __launch_bounds__(256) void simt_gemm(WideParams p) {
 }  // namespace
 
 const void* kernelFor(Variant v, bool ta, bool tb) {
+    if (v >= Variant::kBf16Mfma256x256 && v < Variant::kCount) {
+        const int i    = static_cast<int>(v) - static_cast<int>(Variant::kBf16Mfma256x256);
+        const int tile = i % kHalfTiles;
+        using Fn       = const void* (*)(int);
+        static constexpr Fn table[2][4] = {
+            {halfKernelBf16NN, halfKernelBf16TN, halfKernelBf16NT, halfKernelBf16TT},
+            {halfKernelFp16NN, halfKernelFp16TN, halfKernelFp16NT, halfKernelFp16TT}};
+        return table[i / kHalfTiles][(ta ? 1 : 0) + (tb ? 2 : 0)](tile);
+    }
     if (ta || tb) {
         if (v == Variant::kSimt) return reinterpret_cast<const void*>(&simt_gemm);  // strides are runtime values
         if (v == Variant::kGemvS && !tb && ta) return reinterpret_cast<const void*>(&gemv_splitk<true, false, true>);

@@ -1,0 +1,9 @@
+// BF16 half-precision MFMA tiles for row-major a, column-major b (see gemm/half_tile.hpp).
+// One translation unit per type and layout keeps the build parallel.
+#include "half_tile.hpp"
+
+namespace ftrain::gemm {
+
+const void* halfKernelBf16NT(int tile) { return hdev::halfKernel<true, false, true>(tile); }
+
+}  // namespace ftrain::gemm

@@ -16,6 +16,7 @@ namespace ftrain {
 namespace {
 
 using gemm::GemmParams;
+using gemm::HalfGemmParams;
 using gemm::ReduceParams;
 using gemm::SplitKind;
 using gemm::Variant;
@@ -26,13 +27,38 @@ uint64_t ceilDiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
 bool floatAligned(const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % alignof(float) == 0; }
 bool vecAligned(const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+bool aligned(const void* p, uintptr_t n) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % n == 0; }
 
-// Rules every variant shares (reference fp32_gemm.cpp:27-62).
-Result commonChecks(const GemmProblem& p) {
+uintptr_t elementBytes(FTrainNumericType t) { return t == FTRAIN_NUMERIC_TYPE_FP32 ? 4 : 2; }
+
+// Element types a variant takes.  fp32 variants: the reference Fp32Gemm's
+// rule, every port fp32 (fp32_gemm.cpp:28-37).  bf16 / fp16 variants: a and
+// b in that type, c and d both fp32 or both that type, alpha and beta fp32.
+Result typeChecks(const GemmProblem& p, FTrainNumericType input) {
     if (p.computeType() != FTRAIN_NUMERIC_TYPE_FP32) return Result(FTRAIN_STATUS_UNSUPPORTED, "compute type is not fp32");
-    for (int i = 0; i < 6; ++i)
-        if (p.port(i).numericType() != FTRAIN_NUMERIC_TYPE_FP32)
-            return Result(FTRAIN_STATUS_UNSUPPORTED, "an operand is not fp32");
+    if (input == FTRAIN_NUMERIC_TYPE_FP32) {
+        for (int i = 0; i < 6; ++i)
+            if (p.port(i).numericType() != FTRAIN_NUMERIC_TYPE_FP32)
+                return Result(FTRAIN_STATUS_UNSUPPORTED, "an operand is not fp32");
+        return Result{};
+    }
+    const bool bf16 = input == FTRAIN_NUMERIC_TYPE_BF16;
+    if (p.a().numericType() != input || p.b().numericType() != input)
+        return Result(FTRAIN_STATUS_UNSUPPORTED, bf16 ? "a or b is not bf16" : "a or b is not fp16");
+    const FTrainNumericType cd = p.d().numericType();
+    // A null c (no beta term) carries no data; its declared type is not checked.
+    if ((cd != FTRAIN_NUMERIC_TYPE_FP32 && cd != input) || (p.c().memory() != nullptr && p.c().numericType() != cd))
+        return Result(FTRAIN_STATUS_UNSUPPORTED, bf16 ? "c and d must both be fp32 or both bf16"
+                                                      : "c and d must both be fp32 or both fp16");
+    if (p.alpha().numericType() != FTRAIN_NUMERIC_TYPE_FP32 || p.beta().numericType() != FTRAIN_NUMERIC_TYPE_FP32)
+        return Result(FTRAIN_STATUS_UNSUPPORTED, "alpha or beta is not fp32");
+    return Result{};
+}
+
+// Rules every variant shares (reference fp32_gemm.cpp:27-62), for the
+// variant's input type.
+Result commonChecks(const GemmProblem& p, FTrainNumericType input) {
+    if (Result r = typeChecks(p, input); !r.isSuccess()) return r;
     // alpha and beta: continuous scalars.  a, b, c, d: continuous, or
     // explicit strides with one unit dimension (GemmProblem::launch).
     for (int i = 4; i < 6; ++i)
@@ -41,8 +67,10 @@ Result commonChecks(const GemmProblem& p) {
     GemmLaunch g;
     if (const char* why = p.launch(g)) return Result(FTRAIN_STATUS_UNSUPPORTED, why);
     for (int i = 0; i < 6; ++i)
-        if (!floatAligned(p.port(i).memory()))
-            return Result(FTRAIN_STATUS_UNSUPPORTED, "an operand address is not float-aligned");
+        if (!aligned(p.port(i).memory(), elementBytes(p.port(i).numericType())))
+            return Result(FTRAIN_STATUS_UNSUPPORTED, input == FTRAIN_NUMERIC_TYPE_FP32
+                                                         ? "an operand address is not float-aligned"
+                                                         : "an operand address is not aligned to its element size");
     if (p.emptyOutput()) return Result{};
     const GemmShape s = p.shape();
     if (p.d().memory() == nullptr || (s.k != 0 && (p.a().memory() == nullptr || p.b().memory() == nullptr)))
@@ -57,14 +85,15 @@ void check(hipError_t e, const char* what) {
 
 class GemmPrimitive final : public Primitive<GemmProblem> {
   public:
-    explicit GemmPrimitive(Variant v) : v_(v), info_(&gemm::info(v)) {}
+    explicit GemmPrimitive(Variant v)
+        : v_(v), info_(&gemm::info(v)), half_(gemm::info(v).input != FTRAIN_NUMERIC_TYPE_FP32) {}
 
     const char* name() const noexcept override { return info_->name; }
     std::unique_ptr<PrimitiveBase> clone() const override { return std::make_unique<GemmPrimitive>(*this); }
     uint64_t requiredWorkspaceBytes() const noexcept override { return 0; }
 
     Result isApplicable(const GemmProblem& p, const Constraints& constraints) const override {
-        Result r = commonChecks(p);
+        Result r = commonChecks(p, info_->input);
         if (!r.isSuccess() || p.emptyOutput()) return r;
         GemmLaunch g;
         (void)p.launch(g);  // succeeded in commonChecks
@@ -78,7 +107,18 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
             if (ceilDiv(s.m, info_->bm) * ceilDiv(s.n, info_->bn) > kMax)
                 return Result(FTRAIN_STATUS_UNSUPPORTED, "the tile count exceeds the grid limit");
         }
-        if (info_->vec) {
+        if (info_->vec && half_) {
+            // 16-byte accesses (8 elements) along a's and b's contiguous
+            // dimensions; c and d are accessed per element.
+            const uint64_t a_run = g.ta ? s.m : s.k, b_run = g.tb ? s.k : s.n;
+            if (a_run % 8 != 0 || b_run % 8 != 0)
+                return Result(FTRAIN_STATUS_UNSUPPORTED,
+                              "a contiguous extent of a or b is not a multiple of 8 (16-byte loads)");
+            if (g.lda % 8 != 0 || g.ldb % 8 != 0)
+                return Result(FTRAIN_STATUS_UNSUPPORTED, "a leading dimension of a or b is not a multiple of 8");
+            if (!vecAligned(g.a) || !vecAligned(g.b))
+                return Result(FTRAIN_STATUS_UNSUPPORTED, "a or b is not 16-byte aligned");
+        } else if (info_->vec) {
             // 128-bit accesses along each matrix's contiguous dimension:
             // that extent and every leading dimension a multiple of 4.
             const uint64_t a_run = g.ta ? s.m : s.k, b_run = g.tb ? s.k : s.n;
@@ -133,11 +173,16 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
         }
         params_ = GemmParams{a,      b,      c,     d,     alpha, beta,   int32_t(s.m), int32_t(s.n), int32_t(s.k),
                              int32_t(chunk), 0, 0, g.lda, g.ldb, g.ldc, g.ldd};
+        const bool cd_half = p.d().numericType() != FTRAIN_NUMERIC_TYPE_FP32;
+        half_params_       = HalfGemmParams{g.a,          g.b,          g.c,          g.d,   alpha, beta,
+                                      int32_t(s.m), int32_t(s.n), int32_t(s.k), int32_t(chunk),
+                                      0,            0,            g.lda,        g.ldb, g.ldc, g.ldd,
+                                      int32_t(cd_half)};
         if (info_->gemv) {
             grid_ = dim3(static_cast<uint32_t>(ceilDiv(s.n, gemm::kGemvCols)), 1, splits);
         } else {
-            params_.tiles_m = int32_t(ceilDiv(s.m, info_->bm));
-            params_.tiles_n = int32_t(ceilDiv(s.n, info_->bn));
+            params_.tiles_m = half_params_.tiles_m = int32_t(ceilDiv(s.m, info_->bm));
+            params_.tiles_n = half_params_.tiles_n = int32_t(ceilDiv(s.n, info_->bn));
             grid_           = dim3(uint32_t(params_.tiles_m) * uint32_t(params_.tiles_n), 1, splits);
         }
         const uint64_t count = s.m * s.n;
@@ -145,9 +190,13 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
             aux_grid_ = dim3(static_cast<uint32_t>(std::min<uint64_t>(ceilDiv(count, 256), 16384)));
         if (info_->split == SplitKind::kPartial) {
             partial_bytes_ = uint64_t(splits) * count * sizeof(float);
-            reduce_        = ReduceParams{nullptr, c, d, alpha, beta, count, s.n, g.ldc, g.ldd, int32_t(splits)};
-            // isApplicable guaranteed n, ldc, ldd % 4 == 0 and 16-byte bases for vec variants.
-            reduce_vec_    = info_->vec;
+            const int32_t cd_type = !cd_half ? gemm::kCdFp32
+                                    : p.d().numericType() == FTRAIN_NUMERIC_TYPE_BF16 ? gemm::kCdBf16
+                                                                                     : gemm::kCdFp16;
+            reduce_ = ReduceParams{nullptr, g.c, g.d, alpha, beta, count, s.n, g.ldc, g.ldd, int32_t(splits), cd_type};
+            // isApplicable guaranteed n, ldc, ldd % 4 == 0 and 16-byte bases
+            // for the fp32 vec variants; the half variants reduce per element.
+            reduce_vec_ = info_->vec && !half_;
             aux_grid_ = dim3(static_cast<uint32_t>(std::min<uint64_t>(ceilDiv(reduce_vec_ ? count / 4 : count, 256), 8192)));
         }
     }
@@ -160,8 +209,9 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
             check(hipLaunchKernel(kernel_, grid_, block_, args, 0, r.stream), info_->name);
             return;
         }
-        GemmParams params = params_;
-        void* args[]      = {&params};
+        GemmParams params          = params_;
+        HalfGemmParams half_params = half_params_;
+        void* args[]               = {half_ ? static_cast<void*>(&half_params) : static_cast<void*>(&params)};
         switch (info_->split) {
             case SplitKind::kNone:
                 check(hipLaunchKernel(kernel_, grid_, block_, args, 0, r.stream), info_->name);
@@ -179,6 +229,7 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
                                     reinterpret_cast<uintptr_t>(r.workspace) % 16 == 0;
                 void* ws           = caller ? r.workspace : acquireWorkspace(partial_bytes_, r.stream);
                 params.d           = static_cast<float*>(ws);
+                half_params.d      = ws;
                 ReduceParams red   = reduce_;
                 red.partials       = static_cast<const float*>(ws);
                 void* rargs[]      = {&red};
@@ -206,10 +257,12 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
 
     Variant v_;
     const VariantInfo* info_;
+    bool half_;  // bf16 / fp16 inputs (HalfGemmParams)
     bool empty_         = true;
     const void* kernel_ = nullptr;
     dim3 grid_, block_, aux_grid_;
     GemmParams params_{};
+    HalfGemmParams half_params_{};
     WideParams wide_{};
     ReduceParams reduce_{};
     bool reduce_vec_        = false;

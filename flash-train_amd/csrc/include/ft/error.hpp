@@ -16,7 +16,7 @@ namespace ftrain {
 
 class Result {
   public:
-    static constexpr std::size_t kCapacity = 2048;  // bytes including the terminator
+    static constexpr std::size_t kCapacity = 8192;  // bytes including the terminator (room for every variant's reason)
 
     Result() noexcept { text_[0] = '\0'; }
     Result(FTrainStatus status, const char* message) noexcept { set(status, message); }

@@ -13,6 +13,8 @@
 
 #include <cstdint>
 
+#include <flash_train/common.h>
+
 namespace ftrain::gemm {
 
 // Kernel parameters, passed by value.  Dimensions are 32-bit (Primitives
@@ -49,17 +51,37 @@ struct WideParams {
     int64_t a_rs, a_cs, b_rs, b_cs, ldc, ldd;
 };
 
+// Parameters of the bf16 / fp16 MFMA kernels (inputs a, b in the variant's
+// 16-bit type, fp32 accumulation; c and d in fp32 or the input type).
+struct HalfGemmParams {
+    const void* a;
+    const void* b;
+    const void* c;  // may be null
+    void* d;        // d, or the fp32 partial slices of a split-k variant
+    float alpha;
+    float beta;
+    int32_t m, n, k;
+    int32_t k_chunk;
+    int32_t tiles_m, tiles_n;
+    int64_t lda, ldb, ldc, ldd;  // as in GemmParams
+    int32_t cd_half;             // c and d hold the input type (else fp32)
+};
+
+// Element type of c and d in the split-k reduction.
+enum CdType : int32_t { kCdFp32 = 0, kCdBf16 = 1, kCdFp16 = 2 };
+
 // Parameters of the split-k reduction (d = alpha * sum_z partials[z] + beta*c).
 struct ReduceParams {
-    const float* partials;  // splits dense m x n slices of count floats
-    const float* c;         // may be null
-    float* d;
+    const float* partials;  // splits dense m x n fp32 slices of count elements
+    const void* c;          // may be null; element type cd_type
+    void* d;                // element type cd_type
     float alpha;
     float beta;
     uint64_t count;  // m * n
     uint64_t n;      // columns (the row length of a partial slice)
     int64_t ldc, ldd;
     int32_t splits;
+    int32_t cd_type;  // CdType
 };
 
 // Skinny-m kernel geometry: at most kGemvRows rows of a, kGemvCols output
@@ -91,8 +113,24 @@ enum class Variant : int {
     kGemvUS,
     // General SIMT kernel with 64-bit indexing.
     kSimt,
+    // bf16 and fp16 inputs, fp32 accumulation (v_mfma_f32_32x32x16_*):
+    // 16-byte loads (k, leading dimensions and contiguous extents multiples
+    // of 8), except the _Unaligned tile (per-element loads, any shape).
+    kBf16Mfma256x256,
+    kBf16Mfma128x128,
+    kBf16Mfma128x128S,
+    kBf16Mfma64x64U,
+    kFp16Mfma256x256,
+    kFp16Mfma128x128,
+    kFp16Mfma128x128S,
+    kFp16Mfma64x64U,
     kCount
 };
+
+// Tile index of a half-precision variant inside its type's group (the
+// order of the four variants above): 0 = 256x256, 1 = 128x128,
+// 2 = 128x128 split-k, 3 = 64x64 per-element.
+constexpr int kHalfTiles = 4;
 
 enum class SplitKind : int {
     kNone,     // one workgroup owns each output tile's whole reduction
@@ -110,7 +148,9 @@ struct VariantInfo {
     bool gemv;
     bool simt;
     bool layouts;       // instantiated for column-major a and b as well (else row-major a and b only)
-    double efficiency;  // fraction of the FP32 matrix peak the tile sustains (cost model)
+    double efficiency;
+    FTrainNumericType input;  // element type of a and b
+    double flop_per_clk;      // dense MFMA FLOP per clock per CU for that type  // fraction of the FP32 matrix peak the tile sustains (cost model)
 };
 
 // Largest split-k workspace (partial tiles) a Primitive will use.
@@ -128,6 +168,16 @@ const void* kernelFor(Variant v, bool ta = false, bool tb = false);
 const void* layoutKernelTN(Variant v);  // column-major a, row-major b
 const void* layoutKernelNT(Variant v);  // row-major a, column-major b
 const void* layoutKernelTT(Variant v);  // both column-major
+// Half-precision tiles (index 0..kHalfTiles-1) per input type and operand
+// orientation, one HIP TU each.
+const void* halfKernelBf16NN(int tile);
+const void* halfKernelBf16TN(int tile);
+const void* halfKernelBf16NT(int tile);
+const void* halfKernelBf16TT(int tile);
+const void* halfKernelFp16NN(int tile);
+const void* halfKernelFp16TN(int tile);
+const void* halfKernelFp16NT(int tile);
+const void* halfKernelFp16TT(int tile);
 const void* prologueKernel();            // d = c ? beta*c : 0 over m*n elements (WideParams)
 const void* reduceKernel(bool vec);      // split-k reduction (ReduceParams)
 

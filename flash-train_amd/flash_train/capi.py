@@ -31,6 +31,7 @@ FP64, INT64, UINT64, FP32, INT32, UINT32, FP16, BF16 = 1, 2, 3, 4, 5, 6, 7, 8
 NUMERIC_TYPE_COUNT = 24
 INDEX_INVALID, INDEX_CONTINUOUS, INDEX_SF_SWIZZLED, INDEX_GROUPED_CONTINUOUS = 0, 1, 2, 3
 INDEX_TYPE_COUNT = 4
+TORCH_NUMERIC_TYPES = {torch.float32: FP32, torch.bfloat16: BF16, torch.float16: FP16, torch.float64: FP64}
 
 EXPORTED_SYMBOLS = (
     "ftrainGetLastStatus", "ftrainGetLastMessage",
@@ -193,9 +194,12 @@ def matrix(t: Optional[torch.Tensor], shape: Optional[Sequence[int]] = None, **k
     """Device matrix view over a tensor (or a null-memory view of `shape`).
 
     A contiguous tensor gets FTRAIN_INDEX_TYPE_CONTINUOUS; a non-contiguous
-    one (a transpose, a column slice) its explicit element strides."""
+    one (a transpose, a column slice) its explicit element strides.  The
+    numeric type follows the tensor's dtype unless given."""
     if t is None:
         return View(None, list(shape), **kw)
+    if "numeric_type" not in kw:
+        kw["numeric_type"] = TORCH_NUMERIC_TYPES.get(t.dtype, FP32)
     if not t.is_contiguous() and shape is None and "index_type" not in kw and "strides" not in kw:
         return View(t.data_ptr(), list(t.shape), index_type=INDEX_INVALID, strides=list(t.stride()), **kw)
     return View(t.data_ptr(), list(shape) if shape is not None else list(t.shape), **kw)

@@ -16,6 +16,16 @@ Contents
                                    (/root/reference/tests/api/gemm_numerics_test.cpp:58-59,
                                    tests/support/numerics.hpp:72-101)
   seeded_inputs(config)            BASELINE inputs: one CPU torch.Generator seeded 2026, a, b, c in order
+  bf16_decode / bf16_encode        bfloat16 bit patterns <-> fp32 (exact widening; round to nearest
+  fp16_decode / fp16_encode        even when narrowing, NaN kept NaN); the same for IEEE binary16
+  gemm_f64_typed(...)              gemm_f64 on operands given as 16-bit patterns (decoded exactly)
+  tolerance_check(..., out_type)   for a bf16 / fp16 d, the bar widened by that type's rounding:
+                                   |d - ref| <= bound * (1 + u) + u * |ref|, u = 2^-8 (bf16) / 2^-11 (fp16)
+
+The 16-bit element types have no reference kernel (the reference's only kernel is
+fp32, fp32_gemm.hip:18-31, though its numeric-type enum names both types,
+include/flash_train/common.h:38-65); their products are exact in fp32, so the
+fp64 reference of the decoded values is the oracle for them too.
 """
 
 from __future__ import annotations
@@ -102,13 +112,16 @@ def threads() -> int:
     return lib().ft_oracle_threads()
 
 
-def tolerance_check(d, ref, k: int) -> dict:
+def tolerance_check(d, ref, k: int, out_type: str = "fp32") -> dict:
     """North-star parity bar.  Returns a report; report['ok'] is the verdict.
 
     bound = 1e-4 * sqrt(max(k, 1)) * max|ref| over finite ref entries; every
     entry where both are finite must satisfy |d - ref| <= bound, and the NaN,
-    +Inf and -Inf masks of d and ref must be identical.
+    +Inf and -Inf masks of d and ref must be identical.  For a d rounded to
+    bf16 / fp16 (`out_type`, d given as decoded values) each entry may
+    further differ by that rounding: |d - ref| <= bound * (1 + u) + u * |ref|.
     """
+    u = UNIT_ROUNDOFF[out_type]
     d = np.asarray(d, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     assert d.shape == ref.shape, (d.shape, ref.shape)
@@ -119,10 +132,60 @@ def tolerance_check(d, ref, k: int) -> dict:
     finite = np.isfinite(ref) & np.isfinite(d)
     scale = float(np.max(np.abs(ref[np.isfinite(ref)]))) if np.isfinite(ref).any() else 0.0
     bound = 1e-4 * math.sqrt(max(k, 1)) * scale
-    err = float(np.max(np.abs(d[finite] - ref[finite]))) if finite.any() else 0.0
-    ok = masks_equal and err <= bound
+    diff = np.abs(d[finite] - ref[finite])
+    err = float(np.max(diff)) if finite.any() else 0.0
+    if u > 0 and finite.any():
+        allowed = bound * (1 + u) + u * np.abs(ref[finite])
+        ok = masks_equal and bool(np.all(diff <= allowed))
+    else:
+        ok = masks_equal and err <= bound
     return {"ok": ok, "max_abs_err": err, "bound": bound, "ratio": (err / bound) if bound > 0 else (0.0 if err == 0 else math.inf),
             "masks_equal": masks_equal, "max_abs_ref": scale}
+
+
+# ---- 16-bit element types ----
+
+UNIT_ROUNDOFF = {"fp32": 0.0, "bf16": 2.0 ** -8, "fp16": 2.0 ** -11}
+
+
+def bf16_decode(bits) -> np.ndarray:
+    """bfloat16 patterns (uint16) -> fp32: the pattern is the high half of the fp32 word."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def bf16_encode(x) -> np.ndarray:
+    """fp32 -> bfloat16 patterns, round to nearest even; NaN stays a (quiet) NaN."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    # Adding 0x7FFF plus the lowest kept bit carries into the kept half exactly when the
+    # dropped half is above one half, or equal to it with an odd kept half.
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    out = np.where(nan, (u >> 16) | 0x0040, rounded)
+    return out.astype(np.uint16)
+
+
+def fp16_decode(bits) -> np.ndarray:
+    return np.asarray(bits, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def fp16_encode(x) -> np.ndarray:
+    """fp32 -> IEEE binary16 patterns (numpy's round-to-nearest-even conversion)."""
+    with np.errstate(over="ignore"):  # out-of-range values become +-inf, as IEEE narrowing does
+        return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+DECODE = {"bf16": bf16_decode, "fp16": fp16_decode}
+ENCODE = {"bf16": bf16_encode, "fp16": fp16_encode}
+
+
+def gemm_f64_typed(a_bits, b_bits, in_type: str, c=None, cd_type: str = "fp32", alpha: float = 1.0,
+                   beta: float = 0.0) -> np.ndarray:
+    """fp64 reference for a, b given as 16-bit patterns of `in_type`; c is fp32 values or
+    16-bit patterns of `cd_type`."""
+    a = DECODE[in_type](a_bits)
+    b = DECODE[in_type](b_bits)
+    cc = None if c is None else (DECODE[cd_type](c) if cd_type != "fp32" else np.asarray(c, np.float32))
+    return gemm_f64(a, b, cc, alpha, beta)
 
 
 def reference_grid_check(d, ref, rel: float = 2e-5, abs_: float = 2e-5) -> dict:

@@ -1,0 +1,196 @@
+"""GPU parity of the bf16 / fp16 GEMM variants, called through the C ABI.
+
+a and b in bf16 or fp16, fp32 accumulation, c and d in fp32 or the input
+type.  The reference names both element types in its numeric-type enum
+(include/flash_train/common.h:38-65) but ships only the fp32 kernel
+(src/primitive/hygon/gemm/fp32_gemm.hip:18-31), whose formula these variants
+follow.  Each result is compared with the fp64 oracle of the exactly decoded
+inputs (oracle.gemm_f64_typed) under the north-star bar
+max|d - ref| <= 1e-4 * sqrt(k) * max|ref|, widened for a bf16 / fp16 d by
+that type's rounding: |d - ref| <= bound * (1 + u) + u * |ref|,
+u = 2^-8 (bf16) or 2^-11 (fp16).  Operand storage is padded with NaN so an
+out-of-bounds read fails the comparison.
+"""
+
+import itertools
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+DT = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}
+
+
+@pytest.fixture(scope="module")
+def capi():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a visible device")
+    from flash_train import capi as c
+
+    return c
+
+
+@pytest.fixture(scope="module")
+def ops(capi):
+    return capi.GemmOps()
+
+
+def placed(x: np.ndarray, dtype, col_major: bool, pad: int, fill=float("nan")):
+    """Device tensor view with the values of x (already representable in dtype), row- or
+    column-major with `pad` spare elements per leading dimension, in a storage filled with `fill`."""
+    r, c = x.shape
+    t = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(dtype)
+    if col_major:
+        store = torch.full((c, r + pad), fill, dtype=dtype)
+        store[:, :r] = t.t()
+        store = store.cuda()
+        return store[:, :r].t(), store
+    store = torch.full((r, c + pad), fill, dtype=dtype)
+    store[:, :c] = t
+    store = store.cuda()
+    return store[:, :c], store
+
+
+def rounded(x: np.ndarray, kind: str) -> np.ndarray:
+    """x rounded to the 16-bit type and back to fp32 values."""
+    return torch.from_numpy(x).to(DT[kind]).float().numpy()
+
+
+def run_case(capi, ops, oracle, kind, cd, m, n, k, la, lb, lcd=False, pad=0, with_c=True, alpha=1.5, beta=-0.75,
+             seed=0, every=True):
+    g = np.random.default_rng(seed)
+    a = rounded(g.standard_normal((m, k)).astype(np.float32), kind)
+    b = rounded(g.standard_normal((k, n)).astype(np.float32), kind)
+    c = g.standard_normal((m, n)).astype(np.float32) if with_c else None
+    if c is not None and cd != "fp32":
+        c = rounded(c, cd)
+    ref = oracle.gemm_f64(a, b, c, alpha, beta)
+    av, _ = placed(a, DT[kind], la, pad)
+    bv, _ = placed(b, DT[kind], lb, pad)
+    cv = placed(c, DT[cd], lcd, pad)[0] if with_c else None
+    dv, dstore = placed(np.zeros((m, n), np.float32), DT[cd], lcd, pad, fill=7.0)
+    al, be = capi.HostScalar(alpha), capi.HostScalar(beta)
+    cview = capi.matrix(cv) if with_c else capi.View(None, [m, n], numeric_type=capi.TORCH_NUMERIC_TYPES[DT[cd]])
+    args = ops.args(capi.matrix(av), capi.matrix(bv), cview, capi.matrix(dv), al.view, be.view)
+    plan = args.plan()
+    args.close()
+    names = plan.names()
+    assert all(nm.startswith(kind.capitalize()) for nm in names), names
+    keep = torch.ones_like(dstore, dtype=torch.bool)
+    if lcd:
+        keep[:, :m] = False
+    else:
+        keep[:, :n] = False
+    for i, name in enumerate(names if every else names[:1]):
+        dv.fill_(float("nan"))
+        plan.execute(i, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        rep = oracle.tolerance_check(dv.float().cpu().numpy(), ref, k, cd)
+        assert rep["ok"], (name, kind, cd, m, n, k, la, lb, lcd, pad, rep)
+        assert torch.all(dstore[keep].float() == 7.0), (name, "wrote outside d")
+    return names
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+@pytest.mark.parametrize("cd", ["fp32", "same"])
+@pytest.mark.parametrize("la,lb", list(itertools.product((False, True), (False, True))))
+@pytest.mark.parametrize("m,n,k,pad", [(256, 192, 160, 8), (129, 67, 37, 3), (384, 256, 1024, 0)])
+def test_half_every_primitive(capi, ops, oracle, kind, cd, la, lb, m, n, k, pad):
+    run_case(capi, ops, oracle, kind, kind if cd == "same" else "fp32", m, n, k, la, lb, pad=pad)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+def test_half_column_major_d_and_no_c(capi, ops, oracle, kind):
+    run_case(capi, ops, oracle, kind, "fp32", 96, 160, 64, False, True, lcd=True, pad=8, with_c=False)
+    run_case(capi, ops, oracle, kind, kind, 96, 160, 64, True, False, lcd=True, pad=8, with_c=True)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+def test_half_deep_k_uses_split_k(capi, ops, oracle, kind):
+    names = run_case(capi, ops, oracle, kind, "fp32", 128, 128, 16384, False, True)
+    assert any("SplitK" in nm for nm in names), names
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+def test_half_exact_on_small_integers(capi, ops, kind):
+    # Integer inputs in [-8, 8]: every product and partial sum is exact in fp32 for k <= 2^16 / 64,
+    # so an fp32 d must equal the integer product bit for bit on every Primitive.
+    g = np.random.default_rng(11)
+    m, n, k = 160, 96, 256
+    a = g.integers(-8, 9, (m, k)).astype(np.float32)
+    b = g.integers(-8, 9, (k, n)).astype(np.float32)
+    exact = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+    at = torch.from_numpy(a).to(DT[kind]).cuda()
+    bt = torch.from_numpy(b).to(DT[kind]).cuda()
+    d = torch.empty(m, n, device="cuda")
+    plan = capi.plan_for(at, bt, None, d, 1.0, 0.0, ops)
+    for i in range(len(plan)):
+        d.fill_(float("nan"))
+        plan.execute(i, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(d.cpu().numpy(), exact, err_msg=plan.name(i))
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+def test_half_nan_inf_propagation(capi, ops, oracle, kind):
+    m, n, k = 64, 64, 64
+    g = np.random.default_rng(2)
+    a = rounded(g.standard_normal((m, k)).astype(np.float32), kind)
+    b = rounded(g.standard_normal((k, n)).astype(np.float32), kind)
+    c = g.standard_normal((m, n)).astype(np.float32)
+    a[3, 5] = np.nan
+    b[7, 9] = np.inf
+    c[10, 11] = -np.inf
+    ref = oracle.gemm_f64(a, b, c, 1.0, 0.0)  # beta = 0 with c: 0 * -inf = NaN propagates
+    at, bt = torch.from_numpy(a).to(DT[kind]).cuda(), torch.from_numpy(b).to(DT[kind]).cuda()
+    ct = torch.from_numpy(c).cuda()
+    d = torch.empty(m, n, device="cuda")
+    plan = capi.plan_for(at, bt, ct, d, 1.0, 0.0, ops)
+    for i in range(len(plan)):
+        plan.execute(i, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        rep = oracle.tolerance_check(d.cpu().numpy(), ref, k)
+        assert rep["ok"], (plan.name(i), rep)
+
+
+def test_half_type_rules(capi, ops):
+    x = torch.zeros(64, device="cuda")
+    p = x.data_ptr()
+    al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+    V = capi.View
+    # Mixed a / b types, and a half d with an fp32 c: nothing applies.
+    for a_t, b_t, c_t, d_t, why in ((capi.BF16, capi.FP16, capi.FP32, capi.FP32, "a or b is not bf16"),
+                                    (capi.BF16, capi.BF16, capi.FP32, capi.BF16, "c and d must both be")):
+        args = ops.args(V(p, [3, 2], numeric_type=a_t), V(p, [2, 4], numeric_type=b_t),
+                        V(p, [3, 4], numeric_type=c_t), V(p, [3, 4], numeric_type=d_t), al.view, be.view)
+        with pytest.raises(capi.FTrainError) as e:
+            args.plan()
+        assert e.value.status == capi.UNSUPPORTED and why in e.value.message
+    # fp16 a with fp32 b, c, d: the reference's own case, every fp32 Primitive says so.
+    args = ops.args(V(p, [3, 2], numeric_type=capi.FP16), V(p, [2, 4]), V(p, [3, 4]), V(p, [3, 4]), al.view, be.view)
+    with pytest.raises(capi.FTrainError) as e:
+        args.plan()
+    assert "Fp32Gemm" in e.value.message and "an operand is not fp32" in e.value.message
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+def test_half_large_sampled(capi, ops, oracle, kind):
+    # 4096^3 in the x @ W^T orientation (b column-major) on Primitive 0, sampled rows.
+    m = n = k = 4096
+    gen = torch.Generator().manual_seed(2026)
+    a = torch.randn(m, k, generator=gen).to(DT[kind])
+    w = torch.randn(n, k, generator=gen).to(DT[kind])  # b = w^T
+    ad, wd = a.cuda(), w.cuda()
+    d = torch.empty(m, n, device="cuda")
+    plan = capi.plan_for(ad, wd.t(), None, d, 1.0, 0.0, ops)
+    assert plan.name(0).startswith(kind.capitalize() + "MfmaGemm_256x256") or plan.name(0).startswith(
+        kind.capitalize() + "MfmaGemm_128x128"), plan.names()
+    plan.execute(0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    rows = np.random.default_rng(1).choice(m, 64, replace=False)
+    ref = oracle.gemm_f64(a.float().numpy()[rows], w.float().numpy().T, None, 1.0, 0.0)
+    rep = oracle.tolerance_check(d.cpu().numpy()[rows], ref, k)
+    assert rep["ok"], rep

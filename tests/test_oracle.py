@@ -136,3 +136,74 @@ def test_tolerance_checker(oracle):
     lost_nan = ref.copy()
     lost_nan[1, 0] = 0.0
     assert not oracle.tolerance_check(lost_nan, ref, k)["ok"]
+
+
+# ---------------------------------------------------------------- 16-bit element types
+
+
+def test_bf16_decode_every_pattern_matches_torch(oracle):
+    import torch
+
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    ours = oracle.bf16_decode(bits)
+    theirs = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).float().numpy()
+    nan = np.isnan(theirs)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert np.array_equal(ours[~nan].view(np.uint32), theirs[~nan].view(np.uint32))
+
+
+def test_fp16_decode_every_pattern_matches_torch(oracle):
+    import torch
+
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    ours = oracle.fp16_decode(bits)
+    theirs = torch.from_numpy(bits.view(np.int16)).view(torch.float16).float().numpy()
+    nan = np.isnan(theirs)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert np.array_equal(ours[~nan].view(np.uint32), theirs[~nan].view(np.uint32))
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+def test_encode_rounds_to_nearest_even_like_torch(oracle, kind):
+    import torch
+
+    g = np.random.default_rng(5)
+    x = np.concatenate([
+        g.standard_normal(200000).astype(np.float32) * np.float32(g.choice([1e-6, 1.0, 1e3], 200000)),
+        np.array([0.0, -0.0, np.inf, -np.inf, 1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, 1.0 + 2.0 ** -11,
+                  1.0 + 3 * 2.0 ** -11, 65504.0, 65520.0, 1e-8, -3.4e38], dtype=np.float32)])
+    ours = oracle.ENCODE[kind](x)
+    dt = torch.bfloat16 if kind == "bf16" else torch.float16
+    theirs = torch.from_numpy(x).to(dt).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, theirs)
+    # Ties go to even: 1 + half an ulp rounds down to 1, 1 + 1.5 ulp up to 1 + 2 ulp.
+    half_ulp = 2.0 ** -8 if kind == "bf16" else 2.0 ** -11
+    dec = oracle.DECODE[kind](oracle.ENCODE[kind](np.array([1 + half_ulp, 1 + 3 * half_ulp], np.float32)))
+    assert dec[0] == 1.0 and dec[1] == 1.0 + 4 * half_ulp
+    # NaN stays NaN.
+    assert np.isnan(oracle.DECODE[kind](oracle.ENCODE[kind](np.array([np.nan], np.float32))))[0]
+
+
+def test_typed_gemm_is_exact_on_small_integers(oracle):
+    # Integer-valued bf16 inputs: every product and partial sum is exact, so the fp64
+    # reference equals the integer matrix product.
+    g = np.random.default_rng(3)
+    a = g.integers(-8, 9, (5, 7)).astype(np.float32)
+    b = g.integers(-8, 9, (7, 3)).astype(np.float32)
+    ref = oracle.gemm_f64_typed(oracle.bf16_encode(a), oracle.bf16_encode(b), "bf16")
+    assert np.array_equal(ref, (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float64))
+    c = g.integers(-4, 5, (5, 3)).astype(np.float32)
+    ref = oracle.gemm_f64_typed(oracle.fp16_encode(a), oracle.fp16_encode(b), "fp16", oracle.fp16_encode(c), "fp16",
+                                2.0, -1.0)
+    assert np.array_equal(ref, 2.0 * (a.astype(np.float64) @ b) - c)
+
+
+def test_half_tolerance_allows_output_rounding_only(oracle):
+    ref = np.array([[1.0, 3.0]])
+    k = 1
+    bound = 1e-4 * 3.0
+    # One bf16 ulp at 3.0 is 2^-6: within bound*(1+u) + u*|ref| (u = 2^-8).
+    assert oracle.tolerance_check(np.array([[1.0, 3.0 + 2.0 ** -7]]), ref, k, "bf16")["ok"]
+    assert not oracle.tolerance_check(np.array([[1.0, 3.0 + 2.0 ** -5]]), ref, k, "bf16")["ok"]
+    assert not oracle.tolerance_check(np.array([[1.0, 3.0 + 2.0 ** -7]]), ref, k, "fp32")["ok"]
+    assert oracle.tolerance_check(np.array([[1.0, 3.0 + 0.5 * bound]]), ref, k, "fp32")["ok"]
