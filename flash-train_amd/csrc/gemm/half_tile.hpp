@@ -301,34 +301,99 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p)
 
         // All MFMAs of one stage; operands of step s+1 are read while step
         // s's MFMAs run (the compiler hoists the reads of the unrolled loop).
-        auto compute_stage = [&](int buf) {
+        // Operands of k-step s of LDS buffer `buf`.
+        auto read_ops = [&](int buf, int s, u32x4 (&av)[TM], u32x4 (&bv)[TN]) {
+            const int kk = h * (BK / 2) + 8 * s;
 #pragma unroll
-            for (int s = 0; s < STEPS; ++s) {
-                const int kk = h * (BK / 2) + 8 * s;
-                u32x4 av[TM], bv[TN];
+            for (int bi = 0; bi < TM; ++bi)
+                av[bi] = *reinterpret_cast<const u32x4*>(&As[buf][(wrow + bi * 32 + li) * SK + kk]);
 #pragma unroll
-                for (int bi = 0; bi < TM; ++bi)
-                    av[bi] = *reinterpret_cast<const u32x4*>(&As[buf][(wrow + bi * 32 + li) * SK + kk]);
+            for (int bj = 0; bj < TN; ++bj)
+                bv[bj] = *reinterpret_cast<const u32x4*>(&Bs[buf][(wcol + bj * 32 + li) * SK + kk]);
+        };
+        // MFMAs [first, last) of one k-step, blocks in row-major order.
+        auto mfmas = [&](const u32x4 (&av)[TM], const u32x4 (&bv)[TN], int first, int last) {
 #pragma unroll
-                for (int bj = 0; bj < TN; ++bj)
-                    bv[bj] = *reinterpret_cast<const u32x4*>(&Bs[buf][(wcol + bj * 32 + li) * SK + kk]);
-#pragma unroll
-                for (int bi = 0; bi < TM; ++bi)
-#pragma unroll
-                    for (int bj = 0; bj < TN; ++bj) acc[bi][bj] = mfma<BF16>(av[bi], bv[bj], acc[bi][bj]);
-            }
+            for (int i = 0; i < TM * TN; ++i)
+                if (i >= first && i < last) acc[i / TN][i % TN] = mfma<BF16>(av[i / TN], bv[i % TN], acc[i / TN][i % TN]);
         };
 
-        if (nst > 0) {
-            load_stage(kbeg);
-            store_stage(0);
-        }
-        __syncthreads();
-        for (int st = 0; st < nst; ++st) {
-            if (st + 1 < nst) load_stage(kbeg + (st + 1) * BK);
-            compute_stage(st & 1);
-            if (st + 1 < nst) store_stage((st + 1) & 1);
+        if constexpr (!VEC) {
+            // Per-element path: straightforward two-stage loop.
+            if (nst > 0) {
+                load_stage(kbeg);
+                store_stage(0);
+            }
             __syncthreads();
+            for (int st = 0; st < nst; ++st) {
+                if (st + 1 < nst) load_stage(kbeg + (st + 1) * BK);
+#pragma unroll
+                for (int s = 0; s < STEPS; ++s) {
+                    u32x4 av[TM], bv[TN];
+                    read_ops(st & 1, s, av, bv);
+                    mfmas(av, bv, 0, TM * TN);
+                }
+                if (st + 1 < nst) store_stage((st + 1) & 1);
+                __syncthreads();
+            }
+        } else {
+            // Software pipeline.  Stage st computes from LDS buffer st&1
+            // while registers hold the global data of stage st+1:
+            //   steps 0..STEPS-2: each step's MFMAs run while the operands
+            //     of the next step are read (two operand register sets);
+            //   last step: its first MFMAs run while stage st+1 is written
+            //     to the other buffer and the global loads of stage st+2 are
+            //     issued; then the barrier (stage st+1 visible, and every
+            //     read of buffer st&1 done before stage st+1 overwrites it
+            //     with stage st+2); then the operands of stage st+1's first
+            //     step are read under the last few MFMAs.
+            // Past the last stage the loads re-read the final stage (no
+            // branch in the loop body) and the extra LDS writes land in a
+            // buffer nobody reads again.
+            static_assert(STEPS % 2 == 0, "operand register sets alternate by step");
+            constexpr int NB   = TM * TN;
+            constexpr int TAIL = NB >= 8 ? 4 : NB / 2;  // MFMAs left after the barrier
+            u32x4 opa[2][TM], opb[2][TN];
+            auto clamp_k0 = [&](int stage) { return kbeg + min(stage, nst - 1) * BK; };
+            if (nst > 0) {
+                load_stage(kbeg);
+                store_stage(0);
+                load_stage(clamp_k0(1));
+            }
+            __syncthreads();
+            if (nst > 0) read_ops(0, 0, opa[0], opb[0]);
+            for (int st = 0; st < nst; ++st) {
+                const int cur = st & 1;
+                // sched_barrier(0) fences keep each phase where it is
+                // written: the compiler would otherwise sink every operand
+                // read next to its MFMA and wait for it there.
+#pragma unroll
+                for (int s = 0; s + 1 < STEPS; ++s) {
+                    read_ops(cur, s + 1, opa[(s + 1) & 1], opb[(s + 1) & 1]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    mfmas(opa[s & 1], opb[s & 1], 0, NB);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                constexpr int L = (STEPS - 1) & 1;
+                store_stage(cur ^ 1);
+                load_stage(clamp_k0(st + 2));
+                mfmas(opa[L], opb[L], 0, NB - TAIL);
+                // Spread the LDS writes and global loads over these MFMAs.
+                constexpr int WR = (VEC ? (TA ? 8 * A_PER : A_PER) + (TB ? B_PER : 8 * B_PER) : 0);
+                constexpr int PER = (WR + NB - TAIL - 1) / (NB - TAIL);
+#pragma unroll
+                for (int i = 0; i < NB - TAIL; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x200, PER, 0);  // DS write
+                    __builtin_amdgcn_sched_group_barrier(0x020, PER, 0);  // VMEM read
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                __syncthreads();
+                read_ops(cur ^ 1, 0, opa[0], opb[0]);
+                __builtin_amdgcn_sched_barrier(0);
+                mfmas(opa[L], opb[L], NB - TAIL, NB);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     };
 
