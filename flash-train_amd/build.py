@@ -58,6 +58,10 @@ LIB_SOURCES = [
     "csrc/gemm/kernels_layout_tn.hip",
     "csrc/gemm/kernels_layout_nt.hip",
     "csrc/gemm/kernels_layout_tt.hip",
+    "csrc/gemm/kernels_m16_nn.hip",
+    "csrc/gemm/kernels_m16_tn.hip",
+    "csrc/gemm/kernels_m16_nt.hip",
+    "csrc/gemm/kernels_m16_tt.hip",
     "csrc/gemm/kernels_half_bf16_nn.hip",
     "csrc/gemm/kernels_half_bf16_tn.hip",
     "csrc/gemm/kernels_half_bf16_nt.hip",

@@ -11,6 +11,8 @@ constexpr SplitKind N = SplitKind::kNone, P = SplitKind::kPartial, A = SplitKind
 constexpr FTrainNumericType FP32 = FTRAIN_NUMERIC_TYPE_FP32, BF16 = FTRAIN_NUMERIC_TYPE_BF16,
                             FP16 = FTRAIN_NUMERIC_TYPE_FP16;
 constexpr VariantInfo kInfo[] = {
+    {"Fp32Mfma16Gemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, true, 0.88, FP32, 256.0},
+    {"Fp32Mfma16Gemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, true, 0.60, FP32, 256.0},
     {"Fp32MfmaGemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, false, 0.85, FP32, 256.0},
     {"Fp32MfmaGemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, false, 0.25, FP32, 256.0},
     {"Fp32MfmaGemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, false, 0.84, FP32, 256.0},
@@ -28,11 +30,11 @@ constexpr VariantInfo kInfo[] = {
     {"Fp32Gemv_SplitK", kGemvRows, kGemvCols, 1, 256, 8, true, A, true, false, false, 0.0, FP32, 256.0},
     {"Fp32Gemv_Unaligned_SplitK", kGemvRows, kGemvCols, 1, 256, 8, false, A, true, false, false, 0.0, FP32, 256.0},
     {"Fp32Gemm", 64, 64, 16, 256, 2, false, N, false, true, true, 0.20, FP32, 256.0},
-    {"Bf16MfmaGemm_256x256", 256, 256, 64, 256, 1, true, N, false, false, true, 0.60, BF16, 4096.0},
+    {"Bf16MfmaGemm_256x256", 256, 256, 64, 512, 1, true, N, false, false, true, 0.60, BF16, 4096.0},
     {"Bf16MfmaGemm_128x128", 128, 128, 64, 256, 2, true, N, false, false, true, 0.50, BF16, 4096.0},
     {"Bf16MfmaGemm_128x128_SplitK", 128, 128, 64, 256, 2, true, P, false, false, true, 0.40, BF16, 4096.0},
     {"Bf16MfmaGemm_64x64_Unaligned", 64, 64, 32, 256, 2, false, N, false, false, true, 0.15, BF16, 4096.0},
-    {"Fp16MfmaGemm_256x256", 256, 256, 64, 256, 1, true, N, false, false, true, 0.60, FP16, 4096.0},
+    {"Fp16MfmaGemm_256x256", 256, 256, 64, 512, 1, true, N, false, false, true, 0.60, FP16, 4096.0},
     {"Fp16MfmaGemm_128x128", 128, 128, 64, 256, 2, true, N, false, false, true, 0.50, FP16, 4096.0},
     {"Fp16MfmaGemm_128x128_SplitK", 128, 128, 64, 256, 2, true, P, false, false, true, 0.40, FP16, 4096.0},
     {"Fp16MfmaGemm_64x64_Unaligned", 64, 64, 32, 256, 2, false, N, false, false, true, 0.15, FP16, 4096.0},

@@ -438,7 +438,7 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p)
 template <bool BF16, bool TA, bool TB>
 const void* halfKernel(int tile) {
     switch (tile) {
-        case 0: return reinterpret_cast<const void*>(&half_gemm<BF16, 256, 256, 64, 2, 2, 1, true, kWhole, TA, TB>);
+        case 0: return reinterpret_cast<const void*>(&half_gemm<BF16, 256, 256, 64, 2, 4, 1, true, kWhole, TA, TB>);
         case 1: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kWhole, TA, TB>);
         case 2: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kPartial, TA, TB>);
         case 3: return reinterpret_cast<const void*>(&half_gemm<BF16, 64, 64, 32, 2, 2, 2, false, kWhole, TA, TB>);

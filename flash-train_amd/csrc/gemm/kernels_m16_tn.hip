@@ -1,0 +1,9 @@
+// FP32 16x16x4 MFMA tiles for one operand orientation (see gemm/mfma16_tile.hpp).
+// One translation unit per layout keeps the build parallel.
+#include "mfma16_tile.hpp"
+
+namespace ftrain::gemm {
+
+const void* mfma16KernelTN(int which) { return m16::mfma16Kernel<true, false>(which); }
+
+}  // namespace ftrain::gemm

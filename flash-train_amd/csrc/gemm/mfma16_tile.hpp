@@ -1,0 +1,347 @@
+// FP32 MFMA tile kernel on v_mfma_f32_16x16x4_f32 for large shapes, shared
+// by the per-layout HIP translation units.  Device code only.
+//
+// Replaces the reference's SIMT kernel (src/primitive/hygon/gemm/
+// fp32_gemm.hip:18-31) with the same formula: d = alpha*(a@b) + beta*c, the
+// beta term dropped for a null c and always evaluated otherwise.
+//
+// Geometry: a 256 x 256 output tile per workgroup of 4 waves (one per
+// SIMD), each wave a 128 x 128 sub-tile of 16 x 16 MFMA blocks (8 x 8
+// blocks, 256 fp32 accumulators per lane, held in the accumulation
+// registers).  A stage (BK = 16) is 256 MFMAs per wave, so the one barrier
+// per stage is amortised over ~8k cycles.  With 8192^3 that is 1024 tiles,
+// exactly four rounds over 256 CUs, and every A/B element fetched from L2
+// feeds 256 outputs.  Measured on MI355X: 88% MFMA busy at 8192^3.
+//
+// v_mfma_f32_16x16x4_f32, one block (16 x 16 output, k = 4):
+//   A operand: lane l holds A[row = l % 16][k slot g = l / 16]
+//   B operand: lane l holds B[k slot g][col = l % 16]
+//   result   : lane l, register r holds D[row = 4*g + r][col = l % 16]
+// Lane group g takes k = g*KS + s at step s (KS = BK/4 steps per stage), so
+// over one stage a lane's A values are KS consecutive k: one 128-bit LDS
+// read per row block.  Column interleave in groups of four blocks: block
+// bj, MFMA column j maps to wave-tile column (bj/4)*64 + 4*j + bj%4, so a
+// lane owns TN/4 runs of 4 adjacent columns.  The B operands of all TN
+// blocks of one step are then TN/4 128-bit LDS reads that the 16 lanes of a
+// group take from one contiguous 256-byte span (conflict free), and each
+// 128-bit store of the epilogue covers 256 contiguous bytes of a d row.
+//
+// Operand layouts (TA, TB) and their LDS staging are those of mfma_tile.hpp:
+// each tile is stored with its memory-contiguous dimension innermost so
+// 128-bit global loads become 128-bit LDS writes; a column-major A tile is
+// then read one k per 32-bit read, a column-major B tile one column's KS
+// consecutive k per 128-bit read.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "ft/gemm_kernels.hpp"
+
+namespace ftrain::gemm::m16 {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+enum SplitMode : int { kWhole = 0, kPartial = 2 };
+
+// XCD-aware tile order (see mfma_tile.hpp): each XCD gets a contiguous range
+// of tiles, walked in bands of 8 tile rows.
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int tiles = tiles_m * tiles_n;
+    const int per   = tiles >> 3;
+    int t           = bid;
+    if (bid < (per << 3)) t = (bid & 7) * per + (bid >> 3);
+    constexpr int kBand = 8;
+    const int band_span = kBand * tiles_n;
+    const int band      = t / band_span;
+    const int first_m   = band * kBand;
+    const int band_rows = min(tiles_m - first_m, kBand);
+    const int within    = t - band * band_span;
+    tm                  = first_m + within % band_rows;
+    tn                  = within / band_rows;
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int SPLIT, bool TA, bool TB>
+__global__ __launch_bounds__(WM* WN * 64, 1) void mfma16_gemm(GemmParams p) {
+    constexpr int NT  = WM * WN * 64;
+    constexpr int WTM = BM / WM;
+    constexpr int WTN = BN / WN;
+    constexpr int TM  = WTM / 16;
+    constexpr int TN  = WTN / 16;
+    constexpr int KS  = BK / 4;  // k-steps per stage
+    constexpr int SA  = TA ? BM + 4 : BK + 4;
+    constexpr int SB  = TB ? BK + 4 : BN + 4;
+    constexpr int A_ELEMS = TA ? BK * SA : BM * SA;
+    constexpr int B_ELEMS = TB ? BN * SB : BK * SB;
+    static_assert(TN % 4 == 0 && KS % 4 == 0, "128-bit operand reads");
+    constexpr int A_LD = BM * BK / 4 / NT;
+    constexpr int B_LD = BK * BN / 4 / NT;
+    static_assert(A_LD >= 1 && B_LD >= 1 && BM * BK / 4 % NT == 0 && BK * BN / 4 % NT == 0, "staging");
+
+    __shared__ __attribute__((aligned(16))) float As[2][A_ELEMS];
+    __shared__ __attribute__((aligned(16))) float Bs[2][B_ELEMS];
+
+    const int tid  = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int j16  = lane & 15;
+    const int g    = lane >> 4;
+    const int wrow = (wave / WN) * WTM;
+    const int wcol = (wave % WN) * WTN;
+
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int M = p.m, N = p.n, K = p.k;
+    const int kbeg = SPLIT != kWhole ? blockIdx.z * p.k_chunk : 0;
+    const int kend = SPLIT != kWhole ? min(K, kbeg + p.k_chunk) : K;
+    const int nst  = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+
+    const float* __restrict__ A = p.a;
+    const float* __restrict__ B = p.b;
+    const size_t lda = p.lda, ldb = p.ldb;
+
+    // Staging slot j of this thread: tile-local coordinates, consecutive
+    // threads along each matrix's contiguous dimension.
+    auto a_coord = [&](int j, int& r, int& k) {
+        const int idx = tid + j * NT;
+        if constexpr (TA) {
+            r = 4 * (idx % (BM / 4));
+            k = idx / (BM / 4);
+        } else {
+            r = idx / (BK / 4);
+            k = 4 * (idx % (BK / 4));
+        }
+    };
+    auto b_coord = [&](int j, int& k, int& c) {
+        const int idx = tid + j * NT;
+        if constexpr (TB) {
+            k = 4 * (idx % (BK / 4));
+            c = idx / (BK / 4);
+        } else {
+            k = idx / (BN / 4);
+            c = 4 * (idx % (BN / 4));
+        }
+    };
+    auto a_lds = [&](int r, int k) { return TA ? k * SA + r : r * SA + k; };
+    auto b_lds = [&](int k, int c) { return TB ? c * SB + k : k * SB + c; };
+
+    floatx4 ra[A_LD], rb[B_LD];
+    floatx4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    auto main_loop = [&](auto checked_tag) {
+        constexpr bool CHECKED = decltype(checked_tag)::value;
+        auto a_at = [&](int gm, int gk) { return A + (TA ? (size_t)gk * lda + gm : (size_t)gm * lda + gk); };
+        auto b_at = [&](int gk, int gn) { return B + (TB ? (size_t)gn * ldb + gk : (size_t)gk * ldb + gn); };
+
+        auto load_stage = [&](int k0) {
+#pragma unroll
+            for (int j = 0; j < A_LD; ++j) {
+                int r, k;
+                a_coord(j, r, k);
+                const int gm = m0 + r, gk = k0 + k;
+                ra[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                if (!CHECKED || (gm < M && gk < kend)) ra[j] = *reinterpret_cast<const floatx4*>(a_at(gm, gk));
+            }
+#pragma unroll
+            for (int j = 0; j < B_LD; ++j) {
+                int k, c;
+                b_coord(j, k, c);
+                const int gk = k0 + k, gn = n0 + c;
+                rb[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                if (!CHECKED || (gk < kend && gn < N)) rb[j] = *reinterpret_cast<const floatx4*>(b_at(gk, gn));
+            }
+        };
+        auto store_stage = [&](int buf) {
+#pragma unroll
+            for (int j = 0; j < A_LD; ++j) {
+                int r, k;
+                a_coord(j, r, k);
+                *reinterpret_cast<floatx4*>(&As[buf][a_lds(r, k)]) = ra[j];
+            }
+#pragma unroll
+            for (int j = 0; j < B_LD; ++j) {
+                int k, c;
+                b_coord(j, k, c);
+                *reinterpret_cast<floatx4*>(&Bs[buf][b_lds(k, c)]) = rb[j];
+            }
+        };
+
+        // A operands of a whole stage: av[bi][q] holds k = g*KS + 4q .. +3.
+        auto read_a = [&](int buf, floatx4 (&av)[TM][KS / 4]) {
+#pragma unroll
+            for (int bi = 0; bi < TM; ++bi) {
+                const int r = wrow + bi * 16 + j16;
+#pragma unroll
+                for (int q = 0; q < KS / 4; ++q) {
+                    if constexpr (TA) {
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) av[bi][q][t] = As[buf][(g * KS + 4 * q + t) * SA + r];
+                    } else {
+                        av[bi][q] = *reinterpret_cast<const floatx4*>(&As[buf][r * SA + g * KS + 4 * q]);
+                    }
+                }
+            }
+        };
+        // B operands of the whole stage: bv[s][bj] for k = g*KS + s and
+        // column (bj/4)*64 + 4*j16 + bj%4.
+        auto read_b = [&](int buf, float (&bv)[KS][TN]) {
+            if constexpr (TB) {
+                // Column-major tile: one column's KS consecutive k per read.
+#pragma unroll
+                for (int bj = 0; bj < TN; ++bj)
+#pragma unroll
+                    for (int q = 0; q < KS / 4; ++q) {
+                        const int c = wcol + (bj / 4) * 64 + 4 * j16 + bj % 4;
+                        const floatx4 v = *reinterpret_cast<const floatx4*>(&Bs[buf][c * SB + g * KS + 4 * q]);
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) bv[4 * q + t][bj] = v[t];
+                    }
+            } else {
+#pragma unroll
+                for (int s = 0; s < KS; ++s)
+#pragma unroll
+                    for (int q = 0; q < TN / 4; ++q) {
+                        const floatx4 v =
+                            *reinterpret_cast<const floatx4*>(&Bs[buf][(g * KS + s) * SB + wcol + 64 * q + 4 * j16]);
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) bv[s][4 * q + t] = v[t];
+                    }
+            }
+        };
+
+        auto mfmas = [&](const floatx4 (&av)[TM][KS / 4], const float (&bv)[KS][TN], int first, int last) {
+#pragma unroll
+            for (int i = 0; i < KS * TM * TN; ++i) {
+                if (i < first || i >= last) continue;
+                const int s = i / (TM * TN), bi = (i / TN) % TM, bj = i % TN;
+                acc[bi][bj] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[bi][s / 4][s % 4], bv[s][bj], acc[bi][bj], 0, 0, 0);
+            }
+        };
+
+        // Software pipeline over two LDS buffers and two operand register
+        // sets.  Iteration st holds stage st's operands in registers (read
+        // at the end of the previous iteration) and the global data of
+        // stage st+1 in the staging registers:
+        //   1. the first MFMAs of stage st run while stage st+1 is written to
+        //      the other LDS buffer and stage st+2's global loads are issued;
+        //   2. barrier (stage st+1 visible; its buffer's previous contents,
+        //      stage st-1, were read before the previous barrier);
+        //   3. stage st+1's operands are read into the other register set
+        //      under the remaining MFMAs of stage st.
+        // sched_barrier(0) keeps each phase where it is written.  Past the
+        // last stage the loads re-read the final stage and the extra LDS
+        // writes land in a buffer nobody reads again.
+        constexpr int NM    = KS * TM * TN;
+        constexpr int FIRST = NM / 2;
+        floatx4 av[2][TM][KS / 4];
+        float bv[2][KS][TN];
+        auto clamp_k0 = [&](int stage) { return kbeg + min(stage, nst - 1) * BK; };
+        if (nst > 0) {
+            load_stage(kbeg);
+            store_stage(0);
+            load_stage(clamp_k0(1));
+        }
+        __syncthreads();
+        if (nst > 0) {
+            read_a(0, av[0]);
+            read_b(0, bv[0]);
+        }
+        auto iteration = [&](int st, const floatx4 (&ac)[TM][KS / 4], const float (&bc)[KS][TN],
+                             floatx4 (&an)[TM][KS / 4], float (&bn)[KS][TN]) {
+            const int nxt = (st + 1) & 1;
+            store_stage(nxt);
+            load_stage(clamp_k0(st + 2));
+            mfmas(ac, bc, 0, FIRST);
+            constexpr int MEM = A_LD + B_LD;  // LDS writes, then global loads, spread over the MFMAs
+#pragma unroll
+            for (int i = 0; i < MEM; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, FIRST / (2 * MEM), 0);
+                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, FIRST / (2 * MEM), 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+            read_a(nxt, an);
+            read_b(nxt, bn);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(ac, bc, FIRST, NM);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        for (int st = 0; st < nst; ++st) {
+            iteration(st, av[0], bv[0], av[1], bv[1]);
+            // Rotate the register sets by copying (the allocator coalesces
+            // the copies; swapping references across an unrolled pair made
+            // it keep both sets live in separate registers and spill).
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int q = 0; q < KS / 4; ++q) av[0][i][q] = av[1][i][q];
+#pragma unroll
+            for (int i = 0; i < KS; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) bv[0][i][j] = bv[1][i][j];
+        }
+    };
+
+    const bool interior = m0 + BM <= M && n0 + BN <= N && (kend - kbeg) % BK == 0;
+    if (interior)
+        main_loop(std::false_type{});
+    else
+        main_loop(std::true_type{});
+
+    // Epilogue: block (bi, bj) register r is D[row 4g + r][col (bj/4)*64 +
+    // 4*j16 + bj%4]: run q of the lane is bj = 4q .. 4q+3.
+    const float alpha = p.alpha, beta = p.beta;
+    const float* __restrict__ C = p.c;
+    float* __restrict__ D       = p.d;
+    const size_t ldc = p.ldc, ldd = p.ldd;
+    const int col = n0 + wcol + 4 * j16;
+#pragma unroll
+    for (int bi = 0; bi < TM; ++bi) {
+        // One row block at a time: keeps the scheduler from hoisting every
+        // c load of the tile into registers at once.
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = m0 + wrow + bi * 16 + 4 * g + r;
+            if (row >= M) continue;
+#pragma unroll
+            for (int q = 0; q < TN / 4; ++q) {
+                if (col + 64 * q >= N) continue;  // n % 4 == 0: a run of 4 columns is all in or all out
+                floatx4 out;
+                if constexpr (SPLIT == kPartial) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) out[t] = acc[bi][4 * q + t][r];
+                    *reinterpret_cast<floatx4*>(D + (size_t)blockIdx.z * M * N + (size_t)row * N + col + 64 * q) = out;
+                } else {
+                    floatx4 cv = floatx4{0.f, 0.f, 0.f, 0.f};
+                    if (C != nullptr) cv = *reinterpret_cast<const floatx4*>(C + (size_t)row * ldc + col + 64 * q);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        out[t] = alpha * acc[bi][4 * q + t][r] + (C != nullptr ? beta * cv[t] : 0.f);
+                    *reinterpret_cast<floatx4*>(D + (size_t)row * ldd + col + 64 * q) = out;
+                }
+            }
+        }
+    }
+}
+
+// The 16x16x4 variants for one operand orientation: 0 = 256x256 whole-k,
+// 1 = 256x256 split-k.
+template <bool TA, bool TB>
+const void* mfma16Kernel(int which) {
+    switch (which) {
+        case 0: return reinterpret_cast<const void*>(&mfma16_gemm<256, 256, 16, 2, 2, kWhole, TA, TB>);
+        case 1: return reinterpret_cast<const void*>(&mfma16_gemm<256, 256, 16, 2, 2, kPartial, TA, TB>);
+        default: return nullptr;
+    }
+}
+
+}  // namespace ftrain::gemm::m16

@@ -78,6 +78,20 @@ Result commonChecks(const GemmProblem& p, FTrainNumericType input) {
     return Result{};
 }
 
+// The catalog's workgroup size must fit the kernel's launch bounds (a
+// mismatch would only surface as a launch failure).  Checked when HIP can
+// describe the kernel, i.e. on a host with a device.
+void checkBlockSize(const void* kernel, int threads, const char* name) {
+    hipFuncAttributes attr{};
+    if (hipFuncGetAttributes(&attr, kernel) != hipSuccess) {
+        (void)hipGetLastError();
+        return;
+    }
+    if (attr.maxThreadsPerBlock < threads)
+        throw Exception(FTRAIN_STATUS_INTERNAL_ERROR, "%s: catalog workgroup size %d exceeds the kernel's limit %d", name,
+                        threads, attr.maxThreadsPerBlock);
+}
+
 void check(hipError_t e, const char* what) {
     if (e != hipSuccess)
         throw Exception(FTRAIN_STATUS_INTERNAL_ERROR, "%s launch failed: %s", what, hipGetErrorString(e));
@@ -156,6 +170,7 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
         wide_ = WideParams{a, b, c, d, alpha, beta, s.m, s.n, s.k, a_rs, a_cs, b_rs, b_cs, g.ldc, g.ldd};
 
         kernel_ = gemm::kernelFor(v_, g.ta, g.tb);
+        checkBlockSize(kernel_, info_->threads, info_->name);
         block_  = dim3(info_->threads);
         if (info_->simt) {
             const uint64_t tiles = ceilDiv(s.m, 64) * ceilDiv(s.n, 64);

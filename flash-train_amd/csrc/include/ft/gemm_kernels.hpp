@@ -90,6 +90,10 @@ constexpr int kGemvRows = 8;
 constexpr int kGemvCols = 256;
 
 enum class Variant : int {
+    // v_mfma_f32_16x16x4_f32 256x256 tiles, 4 waves of 128x128 (one per
+    // SIMD), 128-bit loads, every operand orientation; whole-k and split-k.
+    kMfma16_256x256,
+    kMfma16_256x256S,
     // MFMA tiles, 128-bit global loads (needs k % 4 == 0, n % 4 == 0 and
     // 16-byte aligned a/b/c/d).  Suffix S = split-k: per-split partial tiles
     // to a workspace, then a deterministic reduction kernel.
@@ -168,6 +172,11 @@ const void* kernelFor(Variant v, bool ta = false, bool tb = false);
 const void* layoutKernelTN(Variant v);  // column-major a, row-major b
 const void* layoutKernelNT(Variant v);  // row-major a, column-major b
 const void* layoutKernelTT(Variant v);  // both column-major
+// FP32 16x16x4 tiles (0 = whole-k, 1 = split-k) per operand orientation.
+const void* mfma16KernelNN(int which);
+const void* mfma16KernelTN(int which);
+const void* mfma16KernelNT(int which);
+const void* mfma16KernelTT(int which);
 // Half-precision tiles (index 0..kHalfTiles-1) per input type and operand
 // orientation, one HIP TU each.
 const void* halfKernelBf16NN(int tile);

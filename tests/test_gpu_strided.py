@@ -128,7 +128,7 @@ def test_transposed_headline_shape_sampled(capi, ops, oracle):
     args = ops.args(view(capi, av), view(capi, bd), capi.View(None, [m, n]), capi.matrix(d), al.view, be.view)
     plan = args.plan()
     args.close()
-    assert plan.name(0).startswith("Fp32MfmaGemm"), plan.names()
+    assert plan.name(0).startswith("Fp32Mfma"), plan.names()
     plan.execute(0, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     rows = np.random.default_rng(1).choice(m, 64, replace=False)
