@@ -188,11 +188,14 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p)
         constexpr bool CHECKED = decltype(checked_tag)::value;
 
         // Global loads of one stage (k range [k0, k0 + BK)) into registers.
-        auto load_stage = [&](int k0) {
+        // Entries: A staging slots 0 .. A_PER-1, then B slots; [first, last)
+        // selects a part (the whole stage by default).
+        auto load_stage = [&](int k0, int first = 0, int last = 1 << 20) {
             if constexpr (VEC) {
 #pragma unroll
                 for (int j = 0; j < A_PER; ++j) {
                     const int idx = tid + j * NT;
+                    if (j < first || j >= last) continue;
                     if (A_VECS % NT != 0 && idx >= A_VECS) continue;
                     if constexpr (!TA) {  // (r, 8 k) vectors, 8 threads per row of BK = 64
                         const int r = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
@@ -214,6 +217,7 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p)
 #pragma unroll
                 for (int j = 0; j < B_PER; ++j) {
                     const int idx = tid + j * NT;
+                    if (A_PER + j < first || A_PER + j >= last) continue;
                     if (B_VECS % NT != 0 && idx >= B_VECS) continue;
                     if constexpr (TB) {  // (c, 8 k) vectors
                         const int c = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
@@ -251,11 +255,12 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p)
         };
 
         // Registers -> LDS buffer `buf` (k-contiguous rows).
-        auto store_stage = [&](int buf) {
+        auto store_stage = [&](int buf, int first = 0, int last = 1 << 20) {
             if constexpr (VEC) {
 #pragma unroll
                 for (int j = 0; j < A_PER; ++j) {
                     const int idx = tid + j * NT;
+                    if (j < first || j >= last) continue;
                     if (A_VECS % NT != 0 && idx >= A_VECS) continue;
                     if constexpr (!TA) {
                         const int r = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
@@ -271,6 +276,7 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p)
 #pragma unroll
                 for (int j = 0; j < B_PER; ++j) {
                     const int idx = tid + j * NT;
+                    if (A_PER + j < first || A_PER + j >= last) continue;
                     if (B_VECS % NT != 0 && idx >= B_VECS) continue;
                     if constexpr (TB) {
                         const int c = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
@@ -337,62 +343,140 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p)
                 __syncthreads();
             }
         } else {
-            // Software pipeline.  Stage st computes from LDS buffer st&1
-            // while registers hold the global data of stage st+1:
-            //   steps 0..STEPS-2: each step's MFMAs run while the operands
-            //     of the next step are read (two operand register sets);
-            //   last step: its first MFMAs run while stage st+1 is written
-            //     to the other buffer and the global loads of stage st+2 are
-            //     issued; then the barrier (stage st+1 visible, and every
-            //     read of buffer st&1 done before stage st+1 overwrites it
-            //     with stage st+2); then the operands of stage st+1's first
-            //     step are read under the last few MFMAs.
-            // Past the last stage the loads re-read the final stage (no
-            // branch in the loop body) and the extra LDS writes land in a
-            // buffer nobody reads again.
-            static_assert(STEPS % 2 == 0, "operand register sets alternate by step");
-            constexpr int NB   = TM * TN;
-            constexpr int TAIL = NB >= 8 ? 4 : NB / 2;  // MFMAs left after the barrier
-            u32x4 opa[2][TM], opb[2][TN];
-            auto clamp_k0 = [&](int stage) { return kbeg + min(stage, nst - 1) * BK; };
-            if (nst > 0) {
-                load_stage(kbeg);
-                store_stage(0);
-                load_stage(clamp_k0(1));
-            }
-            __syncthreads();
-            if (nst > 0) read_ops(0, 0, opa[0], opb[0]);
-            for (int st = 0; st < nst; ++st) {
-                const int cur = st & 1;
-                // sched_barrier(0) fences keep each phase where it is
-                // written: the compiler would otherwise sink every operand
-                // read next to its MFMA and wait for it there.
-#pragma unroll
-                for (int s = 0; s + 1 < STEPS; ++s) {
-                    read_ops(cur, s + 1, opa[(s + 1) & 1], opb[(s + 1) & 1]);
-                    __builtin_amdgcn_sched_barrier(0);
-                    mfmas(opa[s & 1], opb[s & 1], 0, NB);
-                    __builtin_amdgcn_sched_barrier(0);
+            // Two schedules.  When both operands are copied straight into LDS
+            // (row-major a, column-major b) the staging is spread over all
+            // k-steps; the in-register transposes of the other orientations
+            // do not fit beside it in the register budget, so those keep every
+            // LDS write and load in the last k-step.
+            constexpr bool SPREAD = !TA && TB;
+            if constexpr (SPREAD) {
+                // Software pipeline.  Stage st computes from LDS buffer st&1
+                // while registers hold the global data of stage st+1.  The
+                // staging entries (A slots, then B slots) are split into STEPS
+                // parts; during k-step s, part s of stage st+1 is written to the
+                // other LDS buffer and part s of stage st+2 is loaded into the
+                // registers it frees, interleaved with that step's MFMAs and the
+                // operand reads of step s+1 (the other buffer is free from the
+                // barrier of stage st-1 on: every read of it precedes that
+                // barrier).  In the last step the barrier (stage st+1 complete
+                // and visible) comes before the final TAIL MFMAs, so stage
+                // st+1's first operands are read under them.  sched_barrier(0)
+                // keeps each phase where it is written.  Past the last stage
+                // the loads re-read the final stage and the extra LDS writes land
+                // in a buffer nobody reads again.
+                static_assert(STEPS % 2 == 0, "operand register sets alternate by step");
+                constexpr int NB    = TM * TN;
+                constexpr int TAIL  = NB >= 8 ? 4 : NB / 2;  // MFMAs left after the barrier
+                constexpr int ENT   = A_PER + B_PER;
+                constexpr int PART  = (ENT + STEPS - 1) / STEPS;
+                // Instructions per entry: 16-byte global loads and LDS writes.
+                constexpr int A_INS = TA ? 8 : 1;
+                constexpr int B_INS = TB ? 1 : 8;
+                // Upper bound of one part's loads (or writes) per tail MFMA.
+                constexpr int PER_MFMA = (PART * (A_INS > B_INS ? A_INS : B_INS) + NB - TAIL - 1) / (NB - TAIL);
+                u32x4 opa[2][TM], opb[2][TN];
+                auto clamp_k0 = [&](int stage) { return kbeg + min(stage, nst - 1) * BK; };
+                if (nst > 0) {
+                    load_stage(kbeg);
+                    store_stage(0);
+                    load_stage(clamp_k0(1));
                 }
-                constexpr int L = (STEPS - 1) & 1;
-                store_stage(cur ^ 1);
-                load_stage(clamp_k0(st + 2));
-                mfmas(opa[L], opb[L], 0, NB - TAIL);
-                // Spread the LDS writes and global loads over these MFMAs.
-                constexpr int WR = (VEC ? (TA ? 8 * A_PER : A_PER) + (TB ? B_PER : 8 * B_PER) : 0);
-                constexpr int PER = (WR + NB - TAIL - 1) / (NB - TAIL);
-#pragma unroll
-                for (int i = 0; i < NB - TAIL; ++i) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x200, PER, 0);  // DS write
-                    __builtin_amdgcn_sched_group_barrier(0x020, PER, 0);  // VMEM read
-                }
-                __builtin_amdgcn_sched_barrier(0);
                 __syncthreads();
-                read_ops(cur ^ 1, 0, opa[0], opb[0]);
-                __builtin_amdgcn_sched_barrier(0);
-                mfmas(opa[L], opb[L], NB - TAIL, NB);
-                __builtin_amdgcn_sched_barrier(0);
+                if (nst > 0) read_ops(0, 0, opa[0], opb[0]);
+                for (int st = 0; st < nst; ++st) {
+                    const int cur = st & 1;
+    #pragma unroll
+                    for (int s = 0; s < STEPS; ++s) {
+                        const int e0 = s * PART, e1 = min(ENT, (s + 1) * PART);
+                        if (s + 1 < STEPS) read_ops(cur, s + 1, opa[(s + 1) & 1], opb[(s + 1) & 1]);
+                        store_stage(cur ^ 1, e0, e1);
+                        load_stage(clamp_k0(st + 2), e0, e1);
+                        if (s + 1 < STEPS) {
+                            mfmas(opa[s & 1], opb[s & 1], 0, NB);
+                            // Per MFMA: one operand read, then LDS writes and loads.
+    #pragma unroll
+                            for (int i = 0; i < NB; ++i) {
+                                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+                                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
+                        } else {
+                            mfmas(opa[s & 1], opb[s & 1], 0, NB - TAIL);
+    #pragma unroll
+                            for (int i = 0; i < NB - TAIL; ++i) {
+                                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                                __builtin_amdgcn_sched_group_barrier(0x200, PER_MFMA, 0);  // DS write
+                                __builtin_amdgcn_sched_group_barrier(0x020, PER_MFMA, 0);  // VMEM read
+                            }
+                            __builtin_amdgcn_sched_barrier(0);
+                            __syncthreads();
+                            read_ops(cur ^ 1, 0, opa[0], opb[0]);
+                            __builtin_amdgcn_sched_barrier(0);
+                            mfmas(opa[s & 1], opb[s & 1], NB - TAIL, NB);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                    }
+                }
+            } else {
+                // Software pipeline.  Stage st computes from LDS buffer st&1
+                // while registers hold the global data of stage st+1:
+                //   steps 0..STEPS-2: each step's MFMAs run while the operands
+                //     of the next step are read (two operand register sets);
+                //   last step: its first MFMAs run while stage st+1 is written
+                //     to the other buffer and the global loads of stage st+2 are
+                //     issued; then the barrier (stage st+1 visible, and every
+                //     read of buffer st&1 done before stage st+1 overwrites it
+                //     with stage st+2); then the operands of stage st+1's first
+                //     step are read under the last few MFMAs.
+                // Past the last stage the loads re-read the final stage (no
+                // branch in the loop body) and the extra LDS writes land in a
+                // buffer nobody reads again.
+                static_assert(STEPS % 2 == 0, "operand register sets alternate by step");
+                constexpr int NB   = TM * TN;
+                constexpr int TAIL = NB >= 8 ? 4 : NB / 2;  // MFMAs left after the barrier
+                u32x4 opa[2][TM], opb[2][TN];
+                auto clamp_k0 = [&](int stage) { return kbeg + min(stage, nst - 1) * BK; };
+                if (nst > 0) {
+                    load_stage(kbeg);
+                    store_stage(0);
+                    load_stage(clamp_k0(1));
+                }
+                __syncthreads();
+                if (nst > 0) read_ops(0, 0, opa[0], opb[0]);
+                for (int st = 0; st < nst; ++st) {
+                    const int cur = st & 1;
+                    // sched_barrier(0) fences keep each phase where it is
+                    // written: the compiler would otherwise sink every operand
+                    // read next to its MFMA and wait for it there.
+    #pragma unroll
+                    for (int s = 0; s + 1 < STEPS; ++s) {
+                        read_ops(cur, s + 1, opa[(s + 1) & 1], opb[(s + 1) & 1]);
+                        __builtin_amdgcn_sched_barrier(0);
+                        mfmas(opa[s & 1], opb[s & 1], 0, NB);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    constexpr int L = (STEPS - 1) & 1;
+                    store_stage(cur ^ 1);
+                    load_stage(clamp_k0(st + 2));
+                    mfmas(opa[L], opb[L], 0, NB - TAIL);
+                    // Spread the LDS writes and global loads over these MFMAs.
+                    constexpr int WR = (VEC ? (TA ? 8 * A_PER : A_PER) + (TB ? B_PER : 8 * B_PER) : 0);
+                    constexpr int PER = (WR + NB - TAIL - 1) / (NB - TAIL);
+    #pragma unroll
+                    for (int i = 0; i < NB - TAIL; ++i) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x200, PER, 0);  // DS write
+                        __builtin_amdgcn_sched_group_barrier(0x020, PER, 0);  // VMEM read
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    __syncthreads();
+                    read_ops(cur ^ 1, 0, opa[0], opb[0]);
+                    __builtin_amdgcn_sched_barrier(0);
+                    mfmas(opa[L], opb[L], NB - TAIL, NB);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
         }
     };
