@@ -112,11 +112,11 @@ __global__ __launch_bounds__(256) void prologue(WideParams p) {
 }
 
 // ----------------------------------------------------------------------------
-// Split-k reduction: d = alpha * sum_{z < splits} W[z] + (c ? beta*c : 0),
-// summing the partial slices in increasing z (deterministic).  The slices
-// are dense m x n; c and d are row-major with row strides ldc and ldd.  VEC:
-// four adjacent elements per thread (n, ldc, ldd multiples of 4 and 16-byte
-// aligned c, d, W).
+// Split-k reduction: d = alpha * sum_{z < splits} W[z] + (c ? beta*c : 0) in a
+// fixed summation order (deterministic).  The slices are dense m x n fp32; c
+// and d are row-major with row strides ldc and ldd, in fp32 or a 16-bit type
+// (cd_type).  VEC: units of four adjacent elements (fp32 c and d; n, ldc, ldd
+// multiples of 4; 16-byte aligned c, d, W).
 // ----------------------------------------------------------------------------
 __device__ __forceinline__ float load_cd(const void* p, uint64_t i, int32_t type) {
     if (type == kCdFp32) return static_cast<const float*>(p)[i];
@@ -137,38 +137,56 @@ __device__ __forceinline__ void store_cd(void* p, uint64_t i, int32_t type, floa
 
 template <bool VEC>
 __global__ __launch_bounds__(256) void splitk_reduce(ReduceParams p) {
-    const uint64_t total  = p.count;
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    if constexpr (VEC) {
-        // fp32 c and d only.
-        const floatx4* __restrict__ W = reinterpret_cast<const floatx4*>(p.partials);
-        const float* C                = static_cast<const float*>(p.c);
-        float* D                      = static_cast<float*>(p.d);
-        const uint64_t vecs           = total / 4;
-        const uint64_t row_vecs       = p.n / 4;
-        for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < vecs; i += stride) {
-            const uint64_t r = i / row_vecs, c = 4 * (i - r * row_vecs);
-            floatx4 s = W[i];
-            for (int z = 1; z < p.splits; ++z) s += W[(uint64_t)z * vecs + i];
-            floatx4 out;
-            if (C != nullptr) {
-                const floatx4 cv = *reinterpret_cast<const floatx4*>(C + r * p.ldc + c);
+    // Each block reduces E output units (VEC: 4 adjacent elements) over the
+    // splits with G threads per unit: thread group g sums slices z = g, g+G,
+    // ... in increasing z, then one thread adds the G group sums in
+    // increasing g.  The order is fixed, so results are deterministic, and
+    // the G independent load streams per unit keep enough bytes in flight
+    // for deep splits.
+    constexpr int G = 16;
+    constexpr int E = 256 / G;
+    using V         = std::conditional_t<VEC, floatx4, float>;
+    __shared__ V part[G][E];
+    const int e          = threadIdx.x % E;
+    const int g          = threadIdx.x / E;
+    const uint64_t units = VEC ? p.count / 4 : p.count;
+    const V* __restrict__ W = reinterpret_cast<const V*>(p.partials);
+    const int groups        = min(G, p.splits);
+    for (uint64_t base = (uint64_t)blockIdx.x * E; base < units; base += (uint64_t)gridDim.x * E) {
+        const uint64_t i = base + e;
+        if (i < units && g < groups) {
+            V s = W[(uint64_t)g * units + i];
+#pragma unroll 4
+            for (int z = g + G; z < p.splits; z += G) s += W[(uint64_t)z * units + i];
+            part[g][e] = s;
+        }
+        __syncthreads();
+        if (g == 0 && i < units) {
+            V s = part[0][e];
+            for (int q = 1; q < groups; ++q) s += part[q][e];
+            if constexpr (VEC) {
+                // fp32 c and d, n % 4 == 0.
+                const uint64_t row_vecs = p.n / 4;
+                const uint64_t r = i / row_vecs, c = 4 * (i - r * row_vecs);
+                const float* C = static_cast<const float*>(p.c);
+                float* D       = static_cast<float*>(p.d);
+                floatx4 out;
+                if (C != nullptr) {
+                    const floatx4 cv = *reinterpret_cast<const floatx4*>(C + r * p.ldc + c);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) out[j] = p.alpha * s[j] + p.beta * cv[j];
+                    for (int j = 0; j < 4; ++j) out[j] = p.alpha * s[j] + p.beta * cv[j];
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) out[j] = p.alpha * s[j] + 0.f;
+                }
+                *reinterpret_cast<floatx4*>(D + r * p.ldd + c) = out;
             } else {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) out[j] = p.alpha * s[j] + 0.f;
+                const uint64_t r = i / p.n, c = i - r * p.n;
+                const float out = p.alpha * s + (p.c != nullptr ? p.beta * load_cd(p.c, r * p.ldc + c, p.cd_type) : 0.f);
+                store_cd(p.d, r * p.ldd + c, p.cd_type, out);
             }
-            *reinterpret_cast<floatx4*>(D + r * p.ldd + c) = out;
         }
-    } else {
-        for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-            const uint64_t r = i / p.n, c = i - r * p.n;
-            float s = p.partials[i];
-            for (int z = 1; z < p.splits; ++z) s += p.partials[(uint64_t)z * total + i];
-            const float out = p.alpha * s + (p.c != nullptr ? p.beta * load_cd(p.c, r * p.ldc + c, p.cd_type) : 0.f);
-            store_cd(p.d, r * p.ldd + c, p.cd_type, out);
-        }
+        __syncthreads();
     }
 }
 

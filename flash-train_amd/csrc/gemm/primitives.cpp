@@ -212,7 +212,8 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
             // isApplicable guaranteed n, ldc, ldd % 4 == 0 and 16-byte bases
             // for the fp32 vec variants; the half variants reduce per element.
             reduce_vec_ = info_->vec && !half_;
-            aux_grid_ = dim3(static_cast<uint32_t>(std::min<uint64_t>(ceilDiv(reduce_vec_ ? count / 4 : count, 256), 8192)));
+            // splitk_reduce: 16 output units per block (16 threads each).
+            aux_grid_ = dim3(static_cast<uint32_t>(std::min<uint64_t>(ceilDiv(reduce_vec_ ? count / 4 : count, 16), 65535)));
         }
     }
 
