@@ -257,10 +257,10 @@ __global__ __launch_bounds__(256) void simt_gemm(WideParams p) {
 }  // namespace
 
 const void* kernelFor(Variant v, bool ta, bool tb) {
-    if (v == Variant::kMfma16_256x256 || v == Variant::kMfma16_256x256S) {
+    if (v >= Variant::kMfma16_256x256 && v <= Variant::kMfma16_256x128S) {
         using Fn                     = const void* (*)(int);
         static constexpr Fn table[4] = {mfma16KernelNN, mfma16KernelTN, mfma16KernelNT, mfma16KernelTT};
-        return table[(ta ? 1 : 0) + (tb ? 2 : 0)](v == Variant::kMfma16_256x256 ? 0 : 1);
+        return table[(ta ? 1 : 0) + (tb ? 2 : 0)](static_cast<int>(v) - static_cast<int>(Variant::kMfma16_256x256));
     }
     if (v >= Variant::kBf16Mfma256x256 && v < Variant::kCount) {
         const int i    = static_cast<int>(v) - static_cast<int>(Variant::kBf16Mfma256x256);

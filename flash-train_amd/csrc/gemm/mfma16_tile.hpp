@@ -62,8 +62,13 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
     tn                  = within / band_rows;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int SPLIT, bool TA, bool TB>
-__global__ __launch_bounds__(WM* WN * 64, 1) void mfma16_gemm(GemmParams p) {
+// MINB workgroups per CU bound the registers; SIMPLE selects the plain
+// stage loop (operands read after the barrier, then the stage's MFMAs, then
+// the next stage's LDS writes and global loads), for tiles that run two
+// workgroups per CU: the other workgroup's MFMAs cover this one's reads and
+// barrier, and the single operand set fits the halved register budget.
+template <int BM, int BN, int BK, int WM, int WN, int SPLIT, bool TA, bool TB, int MINB = 1, bool SIMPLE = false>
+__global__ __launch_bounds__(WM* WN * 64, MINB) void mfma16_gemm(GemmParams p) {
     constexpr int NT  = WM * WN * 64;
     constexpr int WTM = BM / WM;
     constexpr int WTN = BN / WN;
@@ -274,19 +279,30 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void mfma16_gemm(GemmParams p) {
             mfmas(ac, bc, FIRST, NM);
             __builtin_amdgcn_sched_barrier(0);
         };
-        for (int st = 0; st < nst; ++st) {
-            iteration(st, av[0], bv[0], av[1], bv[1]);
-            // Rotate the register sets by copying (the allocator coalesces
-            // the copies; swapping references across an unrolled pair made
-            // it keep both sets live in separate registers and spill).
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int q = 0; q < KS / 4; ++q) av[0][i][q] = av[1][i][q];
-#pragma unroll
-            for (int i = 0; i < KS; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j) bv[0][i][j] = bv[1][i][j];
+        if constexpr (SIMPLE) {
+            for (int st = 0; st < nst; ++st) {
+                read_a(st & 1, av[0]);
+                read_b(st & 1, bv[0]);
+                mfmas(av[0], bv[0], 0, NM);
+                store_stage((st + 1) & 1);
+                load_stage(clamp_k0(st + 2));
+                __syncthreads();
+            }
+        } else {
+            for (int st = 0; st < nst; ++st) {
+                iteration(st, av[0], bv[0], av[1], bv[1]);
+                // Rotate the register sets by copying (the allocator coalesces
+                // the copies; swapping references across an unrolled pair made
+                // it keep both sets live in separate registers and spill).
+    #pragma unroll
+                for (int i = 0; i < TM; ++i)
+    #pragma unroll
+                    for (int q = 0; q < KS / 4; ++q) av[0][i][q] = av[1][i][q];
+    #pragma unroll
+                for (int i = 0; i < KS; ++i)
+    #pragma unroll
+                    for (int j = 0; j < TN; ++j) bv[0][i][j] = bv[1][i][j];
+            }
         }
     };
 
@@ -334,12 +350,15 @@ __global__ __launch_bounds__(WM* WN * 64, 1) void mfma16_gemm(GemmParams p) {
 }
 
 // The 16x16x4 variants for one operand orientation: 0 = 256x256 whole-k,
-// 1 = 256x256 split-k.
+// 1 = 256x256 split-k, 2 = 256x128 whole-k (two workgroups per CU),
+// 3 = 256x128 split-k.
 template <bool TA, bool TB>
 const void* mfma16Kernel(int which) {
     switch (which) {
         case 0: return reinterpret_cast<const void*>(&mfma16_gemm<256, 256, 16, 2, 2, kWhole, TA, TB>);
         case 1: return reinterpret_cast<const void*>(&mfma16_gemm<256, 256, 16, 2, 2, kPartial, TA, TB>);
+        case 2: return reinterpret_cast<const void*>(&mfma16_gemm<256, 128, 16, 2, 2, kWhole, TA, TB, 2, true>);
+        case 3: return reinterpret_cast<const void*>(&mfma16_gemm<256, 128, 16, 2, 2, kPartial, TA, TB, 2, true>);
         default: return nullptr;
     }
 }

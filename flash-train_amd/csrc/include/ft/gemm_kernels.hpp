@@ -94,6 +94,10 @@ enum class Variant : int {
     // SIMD), 128-bit loads, every operand orientation; whole-k and split-k.
     kMfma16_256x256,
     kMfma16_256x256S,
+    // Same instruction, 256x128 tiles of 4 waves of 128x64, two workgroups
+    // per CU, plain stage loop.
+    kMfma16_256x128,
+    kMfma16_256x128S,
     // MFMA tiles, 128-bit global loads (needs k % 4 == 0, n % 4 == 0 and
     // 16-byte aligned a/b/c/d).  Suffix S = split-k: per-split partial tiles
     // to a workspace, then a deterministic reduction kernel.
