@@ -46,13 +46,16 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 enum SplitMode : int { kWhole = 0, kPartial = 2 };
 
 // XCD-aware tile order (see mfma_tile.hpp): each XCD gets a contiguous range
-// of tiles, walked in bands of 8 tile rows.
+// of tiles, walked in column sweeps over bands of kBand tile rows.  Measured
+// at 8192^3 (FETCH_SIZE per launch): bands of 4 rows fetch 5.3 GB for the
+// 256x128 tile and 3.2 GB for the 256x256 tile, against 12.3 GB and 3.5 GB
+// with bands of 8, at the same speed.
+template <int kBand>
 __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
     const int tiles = tiles_m * tiles_n;
     const int per   = tiles >> 3;
     int t           = bid;
     if (bid < (per << 3)) t = (bid & 7) * per + (bid >> 3);
-    constexpr int kBand = 8;
     const int band_span = kBand * tiles_n;
     const int band      = t / band_span;
     const int first_m   = band * kBand;
@@ -67,7 +70,8 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 // the next stage's LDS writes and global loads), for tiles that run two
 // workgroups per CU: the other workgroup's MFMAs cover this one's reads and
 // barrier, and the single operand set fits the halved register budget.
-template <int BM, int BN, int BK, int WM, int WN, int SPLIT, bool TA, bool TB, int MINB = 1, bool SIMPLE = false>
+template <int BM, int BN, int BK, int WM, int WN, int SPLIT, bool TA, bool TB, int MINB = 1, bool SIMPLE = false,
+          int BAND = 4>
 __global__ __launch_bounds__(WM* WN * 64, MINB) void mfma16_gemm(GemmParams p) {
     constexpr int NT  = WM * WN * 64;
     constexpr int WTM = BM / WM;
@@ -96,7 +100,7 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void mfma16_gemm(GemmParams p) {
     const int wcol = (wave % WN) * WTN;
 
     int tm, tn;
-    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    tile_of<BAND>(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int M = p.m, N = p.n, K = p.k;
     const int kbeg = SPLIT != kWhole ? blockIdx.z * p.k_chunk : 0;
