@@ -54,6 +54,7 @@ LIB_SOURCES = [
     "csrc/gemm/problem.cpp",
     "csrc/gemm/finder.cpp",
     "csrc/gemm/primitives.cpp",
+    "csrc/gemm/grouped.cpp",
     "csrc/gemm/kernels.hip",
     "csrc/gemm/kernels_layout_tn.hip",
     "csrc/gemm/kernels_layout_nt.hip",

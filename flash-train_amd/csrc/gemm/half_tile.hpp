@@ -120,8 +120,9 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 // SPLIT: kWhole writes d; kPartial writes the raw fp32 partial tile to slice
 // z of the workspace (dense m x n) for splitk_reduce.
 // ----------------------------------------------------------------------------
+// The tile body (see mfma_tile.hpp): tile `bid` of p's grid, split `z`.
 template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, int SPLIT, bool TA, bool TB>
-__global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p) {
+__device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid, int z) {
     using u16           = unsigned short;
     constexpr int NT    = WM * WN * 64;
     constexpr int WTM   = BM / WM;
@@ -144,10 +145,10 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p)
     const int wcol = (wave % WN) * WTN;
 
     int tm, tn;
-    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    tile_of(bid, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int M = p.m, N = p.n, K = p.k;
-    const int kbeg = SPLIT != kWhole ? blockIdx.z * p.k_chunk : 0;
+    const int kbeg = SPLIT != kWhole ? z * p.k_chunk : 0;
     const int kend = SPLIT != kWhole ? min(K, kbeg + p.k_chunk) : K;
     const int nst  = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 
@@ -501,7 +502,7 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p)
                 const int row = m0 + wrow + bi * 32 + 8 * (r / 4) + 4 * h + (r % 4);
                 if (row >= M) continue;
                 if constexpr (SPLIT == kPartial) {
-                    static_cast<float*>(p.d)[(size_t)blockIdx.z * M * N + (size_t)row * N + col] = acc[bi][bj][r];
+                    static_cast<float*>(p.d)[(size_t)z * M * N + (size_t)row * N + col] = acc[bi][bj][r];
                 } else {
                     const size_t ci = (size_t)row * p.ldc + col, di = (size_t)row * p.ldd + col;
                     float cv = 0.f;
@@ -517,6 +518,33 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p)
         }
 }
 
+template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, int SPLIT, bool TA, bool TB>
+__global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p) {
+    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, SPLIT, TA, TB>(p, blockIdx.x, blockIdx.z);
+}
+
+// Grouped GEMM over a device table of per-group parameters (see
+// grouped_mfma_gemm in mfma_tile.hpp).
+__device__ __forceinline__ int find_group(const int32_t* __restrict__ start, int groups, int bid) {
+    int lo = 0, hi = groups - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (start[mid] <= bid)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    return lo;
+}
+
+template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, bool TA, bool TB>
+__global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_half_gemm(GroupedHalfArgs g) {
+    const int bid = blockIdx.x;
+    const int grp = find_group(g.tile_start, g.groups, bid);
+    const HalfGemmParams p = g.params[grp];
+    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, kWhole, TA, TB>(p, bid - g.tile_start[grp], 0);
+}
+
 // The half-precision tiles (index as in kHalfTiles) for one input type and
 // one operand orientation.
 template <bool BF16, bool TA, bool TB>
@@ -526,6 +554,16 @@ const void* halfKernel(int tile) {
         case 1: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kWhole, TA, TB>);
         case 2: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kPartial, TA, TB>);
         case 3: return reinterpret_cast<const void*>(&half_gemm<BF16, 64, 64, 32, 2, 2, 2, false, kWhole, TA, TB>);
+        default: return nullptr;
+    }
+}
+
+// Grouped variants: 0 = 128x128 (16-byte loads), 1 = 64x64 per-element.
+template <bool BF16, bool TA, bool TB>
+const void* groupedHalfKernel(int which) {
+    switch (which) {
+        case 0: return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, TA, TB>);
+        case 1: return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 64, 64, 32, 2, 2, 2, false, TA, TB>);
         default: return nullptr;
     }
 }

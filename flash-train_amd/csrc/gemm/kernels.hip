@@ -293,6 +293,18 @@ const void* kernelFor(Variant v, bool ta, bool tb) {
     }
 }
 
+const void* groupedKernelNN(int which) { return groupedLayoutKernel<false, false>(which); }
+
+const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool tb) {
+    using Fn                        = const void* (*)(int);
+    static constexpr Fn table[3][4] = {
+        {groupedKernelNN, groupedKernelTN, groupedKernelNT, groupedKernelTT},
+        {groupedHalfKernelBf16NN, groupedHalfKernelBf16TN, groupedHalfKernelBf16NT, groupedHalfKernelBf16TT},
+        {groupedHalfKernelFp16NN, groupedHalfKernelFp16TN, groupedHalfKernelFp16NT, groupedHalfKernelFp16TT}};
+    const int t = input == FTRAIN_NUMERIC_TYPE_FP32 ? 0 : input == FTRAIN_NUMERIC_TYPE_BF16 ? 1 : 2;
+    return table[t][(ta ? 1 : 0) + (tb ? 2 : 0)](which);
+}
+
 const void* prologueKernel() { return reinterpret_cast<const void*>(&prologue); }
 
 const void* reduceKernel(bool vec) {

@@ -6,4 +6,6 @@ namespace ftrain::gemm {
 
 const void* halfKernelBf16NN(int tile) { return hdev::halfKernel<true, false, false>(tile); }
 
+const void* groupedHalfKernelBf16NN(int which) { return hdev::groupedHalfKernel<true, false, false>(which); }
+
 }  // namespace ftrain::gemm

@@ -6,4 +6,6 @@ namespace ftrain::gemm {
 
 const void* halfKernelBf16NT(int tile) { return hdev::halfKernel<true, false, true>(tile); }
 
+const void* groupedHalfKernelBf16NT(int which) { return hdev::groupedHalfKernel<true, false, true>(which); }
+
 }  // namespace ftrain::gemm

@@ -6,4 +6,6 @@ namespace ftrain::gemm {
 
 const void* halfKernelBf16TN(int tile) { return hdev::halfKernel<true, true, false>(tile); }
 
+const void* groupedHalfKernelBf16TN(int which) { return hdev::groupedHalfKernel<true, true, false>(which); }
+
 }  // namespace ftrain::gemm

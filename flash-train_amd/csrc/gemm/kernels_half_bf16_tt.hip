@@ -6,4 +6,6 @@ namespace ftrain::gemm {
 
 const void* halfKernelBf16TT(int tile) { return hdev::halfKernel<true, true, true>(tile); }
 
+const void* groupedHalfKernelBf16TT(int which) { return hdev::groupedHalfKernel<true, true, true>(which); }
+
 }  // namespace ftrain::gemm

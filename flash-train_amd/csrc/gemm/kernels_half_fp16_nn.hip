@@ -6,4 +6,6 @@ namespace ftrain::gemm {
 
 const void* halfKernelFp16NN(int tile) { return hdev::halfKernel<false, false, false>(tile); }
 
+const void* groupedHalfKernelFp16NN(int which) { return hdev::groupedHalfKernel<false, false, false>(which); }
+
 }  // namespace ftrain::gemm

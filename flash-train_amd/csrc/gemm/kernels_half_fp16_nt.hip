@@ -6,4 +6,6 @@ namespace ftrain::gemm {
 
 const void* halfKernelFp16NT(int tile) { return hdev::halfKernel<false, false, true>(tile); }
 
+const void* groupedHalfKernelFp16NT(int which) { return hdev::groupedHalfKernel<false, false, true>(which); }
+
 }  // namespace ftrain::gemm

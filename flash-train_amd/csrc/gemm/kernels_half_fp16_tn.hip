@@ -6,4 +6,6 @@ namespace ftrain::gemm {
 
 const void* halfKernelFp16TN(int tile) { return hdev::halfKernel<false, true, false>(tile); }
 
+const void* groupedHalfKernelFp16TN(int which) { return hdev::groupedHalfKernel<false, true, false>(which); }
+
 }  // namespace ftrain::gemm

@@ -6,4 +6,6 @@ namespace ftrain::gemm {
 
 const void* halfKernelFp16TT(int tile) { return hdev::halfKernel<false, true, true>(tile); }
 
+const void* groupedHalfKernelFp16TT(int which) { return hdev::groupedHalfKernel<false, true, true>(which); }
+
 }  // namespace ftrain::gemm

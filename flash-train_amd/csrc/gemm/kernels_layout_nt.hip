@@ -6,4 +6,6 @@ namespace ftrain::gemm {
 
 const void* layoutKernelNT(Variant v) { return dev::layoutKernel<false, true>(v); }
 
+const void* groupedKernelNT(int which) { return dev::groupedLayoutKernel<false, true>(which); }
+
 }  // namespace ftrain::gemm

@@ -6,4 +6,6 @@ namespace ftrain::gemm {
 
 const void* layoutKernelTN(Variant v) { return dev::layoutKernel<true, false>(v); }
 
+const void* groupedKernelTN(int which) { return dev::groupedLayoutKernel<true, false>(which); }
+
 }  // namespace ftrain::gemm

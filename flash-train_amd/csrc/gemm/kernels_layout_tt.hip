@@ -6,4 +6,6 @@ namespace ftrain::gemm {
 
 const void* layoutKernelTT(Variant v) { return dev::layoutKernel<true, true>(v); }
 
+const void* groupedKernelTT(int which) { return dev::groupedLayoutKernel<true, true>(which); }
+
 }  // namespace ftrain::gemm

@@ -126,8 +126,12 @@ enum SplitMode : int { kWhole = 0, kAtomic = 1, kPartial = 2 };
 // last read.  Interior tiles (no m/n edge, whole stages) take a copy of the
 // loop without bounds checks.
 // ----------------------------------------------------------------------------
+// The tile body: output tile number `bid` of p's tile grid, split `z` of
+// the reduction (0 when not split).  Wrapped below by the plain kernel (one
+// problem: the workgroup's x and z grid indices) and the grouped kernel
+// (many problems in one launch).
 template <int BM, int BN, int BK, int WM, int WN, int NBUF, int MINB, bool VEC, int SPLIT, bool TA, bool TB>
-__global__ __launch_bounds__(WM* WN * 64, MINB) void mfma_gemm(GemmParams p) {
+__device__ __forceinline__ void mfma_gemm_tile(const GemmParams& p, int bid, int z) {
     constexpr int NT  = WM * WN * 64;
     constexpr int WTM = BM / WM;
     constexpr int WTN = BN / WN;
@@ -157,11 +161,11 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void mfma_gemm(GemmParams p) {
     const int wcol = (wave % WN) * WTN;
 
     int tm, tn;
-    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    tile_of(bid, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM;
     const int n0 = tn * BN;
     const int M = p.m, N = p.n, K = p.k;
-    const int kbeg = SPLIT != kWhole ? blockIdx.z * p.k_chunk : 0;
+    const int kbeg = SPLIT != kWhole ? z * p.k_chunk : 0;
     const int kend = SPLIT != kWhole ? min(K, kbeg + p.k_chunk) : K;
     const int nst  = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 
@@ -410,7 +414,7 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void mfma_gemm(GemmParams p) {
                 for (int bj = 0; bj < TN; ++bj)
                     if (col + bj < N) unsafeAtomicAdd(D + dbase + bj, alpha * acc[bi][bj][r]);
             } else if constexpr (SPLIT == kPartial) {
-                float* W           = D + (size_t)blockIdx.z * M * N;
+                float* W           = D + (size_t)z * M * N;
                 const size_t pbase = (size_t)row * N + col;
                 if constexpr (VEC && TN > 1) {
                     if (col >= N) continue;
@@ -448,6 +452,36 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void mfma_gemm(GemmParams p) {
     }
 }
 
+template <int BM, int BN, int BK, int WM, int WN, int NBUF, int MINB, bool VEC, int SPLIT, bool TA, bool TB>
+__global__ __launch_bounds__(WM* WN * 64, MINB) void mfma_gemm(GemmParams p) {
+    mfma_gemm_tile<BM, BN, BK, WM, WN, NBUF, MINB, VEC, SPLIT, TA, TB>(p, blockIdx.x, blockIdx.z);
+}
+
+// Index of the group that owns workgroup `bid`: the last g with
+// start[g] <= bid (groups are listed with ascending, distinct starts).
+__device__ __forceinline__ int find_group(const int32_t* __restrict__ start, int groups, int bid) {
+    int lo = 0, hi = groups - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (start[mid] <= bid)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    return lo;
+}
+
+// Grouped GEMM: the tiles of every group in one launch.  Workgroup bid runs
+// tile bid - start[g] of group g, whose parameters (pointers, shape, leading
+// dimensions, tile grid) sit in a device table.
+template <int BM, int BN, int BK, int WM, int WN, int NBUF, int MINB, bool VEC, bool TA, bool TB>
+__global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_mfma_gemm(GroupedGemmArgs g) {
+    const int bid = blockIdx.x;
+    const int grp = find_group(g.tile_start, g.groups, bid);
+    const GemmParams p = g.params[grp];
+    mfma_gemm_tile<BM, BN, BK, WM, WN, NBUF, MINB, VEC, kWhole, TA, TB>(p, bid - g.tile_start[grp], 0);
+}
+
 // The variants with all four operand layouts instantiated, keyed by the
 // Variant they implement.  Used by each layout translation unit.
 template <bool TA, bool TB>
@@ -460,6 +494,17 @@ const void* layoutKernel(Variant v) {
         case Variant::kMfma128x128U: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, 3, 1, false, kWhole, TA, TB>);
         case Variant::kMfma128x128US: return reinterpret_cast<const void*>(&mfma_gemm<128, 128, 16, 2, 2, 3, 1, false, kPartial, TA, TB>);
         case Variant::kMfma64x64U: return reinterpret_cast<const void*>(&mfma_gemm<64, 64, 16, 2, 2, 3, 1, false, kWhole, TA, TB>);
+        default: return nullptr;
+    }
+}
+
+// Grouped variants for one orientation: 0 = 128x128 (128-bit loads),
+// 1 = 64x64 per-element.
+template <bool TA, bool TB>
+const void* groupedLayoutKernel(int which) {
+    switch (which) {
+        case 0: return reinterpret_cast<const void*>(&grouped_mfma_gemm<128, 128, 16, 2, 2, 2, 3, true, TA, TB>);
+        case 1: return reinterpret_cast<const void*>(&grouped_mfma_gemm<64, 64, 16, 2, 2, 3, 1, false, TA, TB>);
         default: return nullptr;
     }
 }

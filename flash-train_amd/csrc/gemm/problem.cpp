@@ -4,6 +4,7 @@
 #include <limits>
 
 #include "ft/gemm.hpp"
+#include "ft/grouped.hpp"
 
 namespace ftrain {
 
@@ -139,6 +140,10 @@ GemmProblem GemmFamily::makeProblem(const Args& args) {
                        args.operation(r.gemm)->compute_type);
 }
 
-std::vector<std::shared_ptr<OpsEngineBase>> builtinEngines() { return {std::make_shared<GemmEngine>()}; }
+std::vector<std::shared_ptr<OpsEngineBase>> builtinEngines() {
+    std::vector<std::shared_ptr<OpsEngineBase>> engines{std::make_shared<GemmEngine>()};
+    for (auto& e : groupedEngines()) engines.push_back(std::move(e));
+    return engines;
+}
 
 }  // namespace ftrain

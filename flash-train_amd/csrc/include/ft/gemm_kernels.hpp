@@ -67,6 +67,19 @@ struct HalfGemmParams {
     int32_t cd_half;             // c and d hold the input type (else fp32)
 };
 
+// Grouped GEMM launch arguments: a device table of per-group parameters
+// (non-empty groups only) and each group's first workgroup, ascending.
+struct GroupedGemmArgs {
+    const GemmParams* params;
+    const int32_t* tile_start;
+    int32_t groups;
+};
+struct GroupedHalfArgs {
+    const HalfGemmParams* params;
+    const int32_t* tile_start;
+    int32_t groups;
+};
+
 // Element type of c and d in the split-k reduction.
 enum CdType : int32_t { kCdFp32 = 0, kCdBf16 = 1, kCdFp16 = 2 };
 
@@ -191,6 +204,22 @@ const void* halfKernelFp16NN(int tile);
 const void* halfKernelFp16TN(int tile);
 const void* halfKernelFp16NT(int tile);
 const void* halfKernelFp16TT(int tile);
+// Grouped kernels: element type (FTRAIN_NUMERIC_TYPE_FP32 / BF16 / FP16),
+// tile (0 = 128x128 with 16-byte loads, 1 = 64x64 per-element) and operand
+// orientation.
+const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool tb);
+const void* groupedKernelNN(int which);
+const void* groupedKernelTN(int which);
+const void* groupedKernelNT(int which);
+const void* groupedKernelTT(int which);
+const void* groupedHalfKernelBf16NN(int which);
+const void* groupedHalfKernelBf16TN(int which);
+const void* groupedHalfKernelBf16NT(int which);
+const void* groupedHalfKernelBf16TT(int which);
+const void* groupedHalfKernelFp16NN(int which);
+const void* groupedHalfKernelFp16TN(int which);
+const void* groupedHalfKernelFp16NT(int which);
+const void* groupedHalfKernelFp16TT(int which);
 const void* prologueKernel();            // d = c ? beta*c : 0 over m*n elements (WideParams)
 const void* reduceKernel(bool vec);      // split-k reduction (ReduceParams)
 

@@ -61,6 +61,9 @@ class GroupedTensor {
 
     uint32_t numGroups() const noexcept { return num_groups_; }
     const StorageView& data() const noexcept { return data_; }
+    const std::optional<StorageView>& offsets() const noexcept { return offsets_; }
+    const std::vector<StorageView>& dimSizes() const noexcept { return dim_sizes_; }
+    const std::vector<StorageView>& strides() const noexcept { return strides_; }
 
   private:
     uint32_t num_groups_;

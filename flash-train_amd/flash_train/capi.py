@@ -342,3 +342,134 @@ def plan_for(a: torch.Tensor, b: torch.Tensor, c: Optional[torch.Tensor], d: tor
         return args.plan()
     finally:
         args.close()
+
+
+# ---- grouped Gemm families (GroupedABCDGemm, GroupedBCDGemm, GroupedABGemm) ----
+
+class GroupedSpec:
+    """One GroupedTensor argument: a rank-two data view and per-group host int64
+    descriptors (reference common.h:397-425).  `dims` and `strides` are lists of
+    (rows, cols) and (row stride, column stride) per group; `offsets` lists each
+    group's first element.  Any of them may be None (absent)."""
+
+    def __init__(self, data: View, num_groups: int, dims=None, strides=None, offsets=None):
+        self.data, self.num_groups = data, num_groups
+        g = num_groups
+
+        def arr(values):
+            a = (c_int64 * max(g, 1))(*values)
+            return a, View(ctypes.addressof(a), [g], numeric_type=INT64, host=True)
+
+        self._keep = []
+        self.dim_views = self.stride_views = self.offset_view = None
+        if dims is not None:
+            cols = [arr([d[i] for d in dims]) for i in range(2)]
+            self._keep += cols
+            self.dim_views = (StorageView * 2)(cols[0][1].sv, cols[1][1].sv)
+        if strides is not None:
+            cols = [arr([s[i] for s in strides]) for i in range(2)]
+            self._keep += cols
+            self.stride_views = (StorageView * 2)(cols[0][1].sv, cols[1][1].sv)
+        if offsets is not None:
+            o = arr(list(offsets))
+            self._keep.append(o)
+            self.offset_view = o[1]
+
+
+class GroupedOps:
+    """Pattern -> Ops for one grouped Gemm: kind "abcd", "bcd" (a is a TensorList) or
+    "ab" (c and d are TensorLists)."""
+
+    def __init__(self, kind: str, l: Optional[ctypes.CDLL] = None):
+        self.lib = l or lib()
+        self.kind = kind
+        lists = {"abcd": (), "bcd": ("a",), "ab": ("c", "d")}[kind]
+        self.ids, self.kinds = {}, {}
+        pat = _H()
+        check(self.lib.ftrainPatternCreate(ctypes.byref(pat)), "ftrainPatternCreate", self.lib)
+        try:
+            for role in ("a", "b", "c", "d", "alpha", "beta"):
+                rid = RoleId()
+                if role in ("alpha", "beta"):
+                    fn, k = self.lib.ftrainPatternAddTensor, "tensor"
+                elif role in lists:
+                    fn, k = self.lib.ftrainPatternAddTensorList, "list"
+                else:
+                    fn, k = self.lib.ftrainPatternAddGroupedTensor, "grouped"
+                check(fn(pat, ctypes.byref(rid)), "ftrainPatternAdd", self.lib)
+                self.ids[role], self.kinds[role] = rid, k
+            self.op_id = RoleId()
+            add = {"abcd": self.lib.ftrainPatternAddGroupedABCDGemm, "bcd": self.lib.ftrainPatternAddGroupedBCDGemm,
+                   "ab": self.lib.ftrainPatternAddGroupedABGemm}[kind]
+            i = self.ids
+            check(add(pat, ctypes.byref(self.op_id), i["a"], i["b"], i["c"], i["d"], i["alpha"], i["beta"]),
+                  "ftrainPatternAddGrouped*Gemm", self.lib)
+            self.ops = _H()
+            check(self.lib.ftrainOpsCreate(ctypes.byref(self.ops), pat), "ftrainOpsCreate", self.lib)
+        finally:
+            self.lib.ftrainPatternDestroy(pat)
+
+    def args(self, compute_type: int = FP32, **values) -> "GroupedArgs":
+        return GroupedArgs(self, values, compute_type)
+
+    def close(self) -> None:
+        if self.ops:
+            self.lib.ftrainOpsDestroy(self.ops)
+            self.ops = _H()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class GroupedArgs:
+    """Args of a GroupedOps: a View for alpha/beta, a GroupedSpec for grouped roles and
+    a list of Views for TensorList roles."""
+
+    def __init__(self, ops: GroupedOps, values: dict, compute_type: int):
+        self.lib = ops.lib
+        self.values = values  # keep alive until the Plan binds them
+        self.handle = _H()
+        check(self.lib.ftrainArgsCreate(ctypes.byref(self.handle), ops.ops), "ftrainArgsCreate", self.lib)
+        self._lists = []
+        for role, v in values.items():
+            rid, kind = ops.ids[role], ops.kinds[role]
+            if kind == "tensor":
+                st = self.lib.ftrainArgsSetTensor(self.handle, rid, v.sv)
+            elif kind == "list":
+                arr = (StorageView * max(len(v), 1))(*[x.sv for x in v])
+                self._lists.append(arr)
+                st = self.lib.ftrainArgsSetTensorList(self.handle, rid, arr, len(v))
+            else:
+                st = self.lib.ftrainArgsSetGroupedTensor(
+                    self.handle, rid, v.num_groups, v.data.sv,
+                    ctypes.byref(v.offset_view.sv) if v.offset_view is not None else None,
+                    v.dim_views, v.stride_views)
+            check(st, f"ftrainArgsSet({role})", self.lib)
+        set_op = {"abcd": self.lib.ftrainArgsSetGroupedABCDGemm, "bcd": self.lib.ftrainArgsSetGroupedBCDGemm,
+                  "ab": self.lib.ftrainArgsSetGroupedABGemm}[ops.kind]
+        check(set_op(self.handle, ops.op_id, compute_type), "ftrainArgsSetGrouped*Gemm", self.lib)
+
+    def plan(self) -> Plan:
+        h = _H()
+        check(self.lib.ftrainPlanCreate(ctypes.byref(h), self.handle), "ftrainPlanCreate", self.lib)
+        return Plan(h, self.lib)
+
+    def plan_status_on_device(self, device: int = 0):
+        """Plan creation for an explicit device id through the testing library (CPU hosts)."""
+        h = _H()
+        st = self.lib.ftrainTestingPlanCreateOnDevice(ctypes.byref(h), self.handle, device)
+        return st, last_message(self.lib), (Plan(h, self.lib) if st == SUCCESS else None)
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.ftrainArgsDestroy(self.handle)
+            self.handle = _H()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
