@@ -130,6 +130,89 @@ def torch_cpu_matmul(a, b, budget_s: float) -> dict:
             "cores": torch.get_num_threads(), "sample": f"{rows}x{b.shape[1]}x{a.shape[1]}, median of 3"}
 
 
+def expert_rows(m: int, experts: int) -> list:
+    """Uneven token counts per expert (deterministic), summing to m; none a multiple of the tile."""
+    w = [1.0 + 0.6 * math.sin(1.7 * e + 0.3) for e in range(experts)]
+    rows = [int(m * x / sum(w)) for x in w]
+    rows[-1] += m - sum(rows)
+    return rows
+
+
+def run_grouped(args, a_h, b_h, c_h, cfg) -> None:
+    """One step = one GroupedABCDGemm launch sequence over all experts (Primitive 0 of its Plan)."""
+    import numpy as np
+    import torch
+
+    import flash_train.capi as capi
+    from oracle import oracle
+
+    m, n, k, E = cfg["m"], cfg["n"], cfg["k"], args.grouped
+    rows = expert_rows(m, E)
+    dt = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[args.dtype]
+    # Expert e's weight: the workload's b with its columns rotated by 97·e (distinct memory, same distribution).
+    b_all = torch.stack([torch.roll(b_h, 97 * e, dims=1) for e in range(E)]).to(dt)
+    a_h = a_h.to(dt)
+    a, b = a_h.cuda(), b_all.cuda()
+    c = c_h.cuda() if c_h is not None else None
+    d = torch.empty(m, n, device="cuda")
+    ops = capi.GroupedOps("abcd")
+    al, be = capi.HostScalar(cfg["alpha"]), capi.HostScalar(cfg["beta"])
+    dims_mn = [(r, n) for r in rows]
+    cspec = capi.GroupedSpec(capi.matrix(c) if c is not None else capi.View(None, [m, n]), E, dims=dims_mn)
+    gargs = ops.args(a=capi.GroupedSpec(capi.matrix(a), E, dims=[(r, k) for r in rows]),
+                     b=capi.GroupedSpec(capi.matrix(b[0]), E), c=cspec,
+                     d=capi.GroupedSpec(capi.matrix(d), E, dims=dims_mn), alpha=al.view, beta=be.view)
+    plan = gargs.plan()
+    gargs.close()
+    name = plan.name(0)
+    log(f"grouped {args.workload} ({m}x{n}x{k}) over {E} experts, rows {rows}; primitive 0 = {name}")
+    stream = torch.cuda.Stream()
+    h = stream.cuda_stream
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            plan.execute(0, h)
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(args.steps):
+            plan.execute(0, h)
+        stop.record(stream)
+        torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / args.steps
+
+    # Parity spot check: 8 sampled rows of every expert against fp64.
+    rng = np.random.default_rng(1)
+    ok, worst, row0 = True, 0.0, 0
+    for e, r in enumerate(rows):
+        pick = np.sort(rng.choice(r, size=min(8, r), replace=False)) + row0
+        ref = oracle.sampled_rows_f64(a_h.float(), b_all[e].float(), c_h, cfg["alpha"], cfg["beta"], pick)
+        rep = oracle.tolerance_check(d[torch.as_tensor(pick).cuda()].cpu().numpy(), ref, k)
+        ok, worst = ok and rep["ok"], max(worst, rep["max_abs_err"] / max(rep["bound"], 1e-30))
+        row0 += r
+
+    half = args.dtype != "fp32"
+    flops = 2.0 * m * n * k
+    tflops = flops / (ms * 1e-3) / 1e12
+    peak = HALF_MATRIX_PEAK_TFLOPS if half else FP32_MATRIX_PEAK_TFLOPS
+    eb = 2.0 if half else 4.0
+    alg_bytes = eb * (m * k + E * k * n) + 4.0 * m * n * (2 if c is not None else 1)
+    workload = f"grouped_{args.workload}_e{E}"
+    print(json.dumps({
+        "metric": METRIC, "value": round(tflops, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": args.dtype,
+        "data": "synthetic (seeded CPU torch.Generator 2026; expert weights are column rotations of b)",
+        "config": {"workload": workload, "m": m, "n": n, "k": k, "experts": E, "rows": rows,
+                   "c": c is not None, "primitive": name, "parallelism": "single GPU"},
+        "pct_of_matrix_peak": round(100.0 * tflops / peak, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(tflops / peak, 4), "traffic": traffic_from_profiles(workload),
+                     "algorithmic_bytes": alg_bytes, "algorithmic_flops": flops, "kernel_ms": round(ms, 4),
+                     "kernel": name},
+        "parity": {"rows_checked": 8 * E, "worst_err_over_bound": worst, "ok": ok},
+    }), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -144,6 +227,9 @@ def main() -> None:
                     help="element type of a and b (c and d stay fp32; accumulation is fp32)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-overhead", action="store_true", help="skip the cached-Plan host-overhead probe")
+    ap.add_argument("--grouped", type=int, default=0, metavar="E",
+                    help="grouped GEMM (GroupedABCDGemm): the workload's m rows split unevenly over E experts, "
+                         "each with its own k x n weight (mixture-of-experts forward)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 device copies of 256 MiB (the known-size kernel that scales the PMC "
                          "FETCH_SIZE / WRITE_SIZE counters into bytes)")
@@ -172,6 +258,9 @@ def main() -> None:
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     a_h, b_h, c_h, cfg = oracle.seeded_inputs(args.workload)
+    if args.grouped:
+        run_grouped(args, a_h, b_h, c_h, cfg)
+        return
     m, n, k = cfg["m"], cfg["n"], cfg["k"]
     half = args.dtype != "fp32"
     if half:

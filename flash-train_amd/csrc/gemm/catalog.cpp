@@ -15,6 +15,7 @@ constexpr VariantInfo kInfo[] = {
     {"Fp32Mfma16Gemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, true, 0.45, FP32, 256.0},
     {"Fp32Mfma16Gemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, true, 0.895, FP32, 256.0},
     {"Fp32Mfma16Gemm_256x128_SplitK", 256, 128, 16, 256, 2, true, P, false, false, true, 0.50, FP32, 256.0},
+    {"Fp32Mfma16Gemm_128x256", 128, 256, 16, 256, 2, true, N, false, false, true, 0.885, FP32, 256.0},
     {"Fp32MfmaGemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, false, 0.85, FP32, 256.0},
     {"Fp32MfmaGemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, false, 0.25, FP32, 256.0},
     {"Fp32MfmaGemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, false, 0.84, FP32, 256.0},

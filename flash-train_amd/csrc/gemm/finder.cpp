@@ -141,6 +141,27 @@ double estimateMicros(Variant v, const GemmShape& s, bool has_c, int cus) {
     return modelMicros(vi, s, has_c, cus, splits);
 }
 
+double groupedMicros(Variant v, const std::vector<GemmShape>& shapes, bool has_c, int cus) {
+    // The groups' tiles share one grid: a CU's load is its share of all
+    // tiles, each costing its own group's depth; bytes add over the groups.
+    const VariantInfo& vi = info(v);
+    const double eb = vi.input == FTRAIN_NUMERIC_TYPE_FP32 ? 4.0 : 2.0;
+    double flops = 0.0, bytes = 0.0;
+    uint64_t tiles = 0;
+    for (const GemmShape& s : shapes) {
+        const uint64_t t = ceilDiv(s.m, vi.bm) * ceilDiv(s.n, vi.bn);
+        tiles += t;
+        flops += double(t) * 2.0 * vi.bm * vi.bn * double(std::max<uint64_t>(s.k, vi.bk));
+        bytes += eb * (double(s.m) * s.k + double(s.k) * s.n + double(s.m) * s.n * (has_c ? 2.0 : 1.0));
+    }
+    if (tiles == 0) return kLaunchMicros;
+    const uint64_t per_cu = ceilDiv(tiles, cus);
+    const double fill     = std::sqrt(std::min(1.0, double(per_cu) / double(vi.occupancy)));
+    const double cu_rate  = vi.flop_per_clk * kClockPerMicro * vi.efficiency * (vi.occupancy > 1 ? fill : 1.0);
+    const double compute  = double(per_cu) * (flops / double(tiles)) / cu_rate;
+    return std::max(compute, bytes / kHbmBytesPerMicro) + kLaunchMicros;
+}
+
 }  // namespace gemm
 
 std::vector<std::string> ShapeCostFinder::candidates(const GemmProblem& problem, const Constraints& constraints) {

@@ -261,18 +261,28 @@ namespace {
 struct GroupedVariant {
     const char* name;
     FTrainNumericType input;
-    int which;  // 0: 128x128 tile with 16-byte loads; 1: 64x64 per-element
-    int bm, bn;
+    int which;             // kernel index for groupedKernelFor
+    gemm::Variant tile;    // the plain variant with the same tile: geometry and cost-model figures
 };
 
+// Registration order is also the fallback order when the GroupedCost Finder
+// is disabled: largest tiles first.
 constexpr GroupedVariant kGroupedVariants[] = {
-    {"GroupedFp32MfmaGemm_128x128", FTRAIN_NUMERIC_TYPE_FP32, 0, 128, 128},
-    {"GroupedFp32MfmaGemm_64x64_Unaligned", FTRAIN_NUMERIC_TYPE_FP32, 1, 64, 64},
-    {"GroupedBf16MfmaGemm_128x128", FTRAIN_NUMERIC_TYPE_BF16, 0, 128, 128},
-    {"GroupedBf16MfmaGemm_64x64_Unaligned", FTRAIN_NUMERIC_TYPE_BF16, 1, 64, 64},
-    {"GroupedFp16MfmaGemm_128x128", FTRAIN_NUMERIC_TYPE_FP16, 0, 128, 128},
-    {"GroupedFp16MfmaGemm_64x64_Unaligned", FTRAIN_NUMERIC_TYPE_FP16, 1, 64, 64},
+    {"GroupedFp32Mfma16Gemm_256x128", FTRAIN_NUMERIC_TYPE_FP32, 2, gemm::Variant::kMfma16_256x128},
+    {"GroupedFp32Mfma16Gemm_128x256", FTRAIN_NUMERIC_TYPE_FP32, 3, gemm::Variant::kMfma16_128x256},
+    {"GroupedFp32MfmaGemm_128x128", FTRAIN_NUMERIC_TYPE_FP32, 0, gemm::Variant::kMfma128x128},
+    {"GroupedFp32MfmaGemm_64x64_Unaligned", FTRAIN_NUMERIC_TYPE_FP32, 1, gemm::Variant::kMfma64x64U},
+    {"GroupedBf16MfmaGemm_256x256", FTRAIN_NUMERIC_TYPE_BF16, 2, gemm::Variant::kBf16Mfma256x256},
+    {"GroupedBf16MfmaGemm_128x128", FTRAIN_NUMERIC_TYPE_BF16, 0, gemm::Variant::kBf16Mfma128x128},
+    {"GroupedBf16MfmaGemm_64x64_Unaligned", FTRAIN_NUMERIC_TYPE_BF16, 1, gemm::Variant::kBf16Mfma64x64U},
+    {"GroupedFp16MfmaGemm_256x256", FTRAIN_NUMERIC_TYPE_FP16, 2, gemm::Variant::kFp16Mfma256x256},
+    {"GroupedFp16MfmaGemm_128x128", FTRAIN_NUMERIC_TYPE_FP16, 0, gemm::Variant::kFp16Mfma128x128},
+    {"GroupedFp16MfmaGemm_64x64_Unaligned", FTRAIN_NUMERIC_TYPE_FP16, 1, gemm::Variant::kFp16Mfma64x64U},
 };
+
+// Workgroup slots of a group: its tiles rounded up to a multiple of 8, so
+// that every group starts on an XCD boundary of the workgroup ids.
+uint64_t groupSlots(uint64_t tiles) { return (tiles + 7) / 8 * 8; }
 
 bool aligned(const void* p, uintptr_t n) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % n == 0; }
 uint64_t ceilDiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
@@ -325,7 +335,7 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
                 return Result(FTRAIN_STATUS_UNSUPPORTED, "an operand address is not aligned to its element size");
             if (l.shape.m > kMax || l.shape.n > kMax || l.shape.k > kMax)
                 return Result(FTRAIN_STATUS_UNSUPPORTED, "a dimension exceeds the 32-bit kernel limit");
-            if (v_->which == 0) {
+            if (gemm::info(v_->tile).vec) {
                 // 16-byte accesses along each matrix's contiguous dimension.
                 const uint64_t w = half ? 8 : 4;
                 const uint64_t a_run = l.ta ? l.shape.m : l.shape.k, b_run = l.tb ? l.shape.k : l.shape.n;
@@ -338,7 +348,8 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
                               !aligned(l.c, 16) || !aligned(l.d, 16)))
                     return Result(FTRAIN_STATUS_UNSUPPORTED, "a group's c or d does not fit 128-bit stores");
             }
-            tiles += ceilDiv(l.shape.m, v_->bm) * ceilDiv(l.shape.n, v_->bn);
+            const gemm::VariantInfo& vi = gemm::info(v_->tile);
+            tiles += groupSlots(ceilDiv(l.shape.m, vi.bm) * ceilDiv(l.shape.n, vi.bn));
             if (tiles > kMax) return Result(FTRAIN_STATUS_UNSUPPORTED, "the tile count exceeds the grid limit");
         }
         return Result{};
@@ -357,9 +368,10 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
             // Groups are launched per operand orientation (one kernel
             // instantiation each); a degenerate matrix may read as either.
             Bucket& bk       = buckets_[(l.ta ? 1 : 0) + (l.tb ? 2 : 0)];
-            const int32_t tm = int32_t(ceilDiv(l.shape.m, v_->bm)), tn = int32_t(ceilDiv(l.shape.n, v_->bn));
+            const gemm::VariantInfo& vi = gemm::info(v_->tile);
+            const int32_t tm = int32_t(ceilDiv(l.shape.m, vi.bm)), tn = int32_t(ceilDiv(l.shape.n, vi.bn));
             bk.tile_start.push_back(bk.tiles);
-            bk.tiles += tm * tn;
+            bk.tiles += int32_t(groupSlots(uint64_t(tm) * uint64_t(tn)));
             const int32_t m = int32_t(l.shape.m), n = int32_t(l.shape.n), k = int32_t(l.shape.k);
             if (half)
                 bk.half_params.push_back(HalfGemmParams{l.a, l.b, l.c, l.d, alpha, beta, m, n, k, k, tm, tn, l.lda,
@@ -417,11 +429,11 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
             if (!half) {
                 GroupedGemmArgs args{reinterpret_cast<const GemmParams*>(base + bk.param_off), start, groups};
                 void* kargs[] = {&args};
-                check(hipLaunchKernel(bk.kernel, dim3(uint32_t(bk.tiles)), dim3(256), kargs, 0, r.stream), v_->name);
+                check(hipLaunchKernel(bk.kernel, dim3(uint32_t(bk.tiles)), dim3(uint32_t(gemm::info(v_->tile).threads)), kargs, 0, r.stream), v_->name);
             } else {
                 GroupedHalfArgs args{reinterpret_cast<const HalfGemmParams*>(base + bk.param_off), start, groups};
                 void* kargs[] = {&args};
-                check(hipLaunchKernel(bk.kernel, dim3(uint32_t(bk.tiles)), dim3(256), kargs, 0, r.stream), v_->name);
+                check(hipLaunchKernel(bk.kernel, dim3(uint32_t(bk.tiles)), dim3(uint32_t(gemm::info(v_->tile).threads)), kargs, 0, r.stream), v_->name);
             }
         }
     }
@@ -489,10 +501,31 @@ template struct GroupedGemmFamily<GroupedKind::kABCD>;
 template struct GroupedGemmFamily<GroupedKind::kBCD>;
 template struct GroupedGemmFamily<GroupedKind::kAB>;
 
+std::vector<std::string> GroupedCostFinder::candidates(const GroupedGemmProblem& problem,
+                                                       const Constraints& constraints) {
+    std::vector<GemmShape> shapes;
+    bool has_c = false;
+    for (uint32_t g = 0; g < problem.groups(); ++g) {
+        if (problem.emptyOutput(g)) continue;
+        GemmLaunch l;
+        if (problem.launch(g, l) != nullptr) continue;
+        shapes.push_back(l.shape);
+        has_c = has_c || l.c != nullptr;
+    }
+    const int cus = gemm::computeUnits(constraints.device());
+    std::vector<std::pair<double, const char*>> ranked;
+    for (const GroupedVariant& v : kGroupedVariants)
+        if (v.input == problem.a().type) ranked.emplace_back(gemm::groupedMicros(v.tile, shapes, has_c, cus), v.name);
+    std::stable_sort(ranked.begin(), ranked.end(), [](const auto& x, const auto& y) { return x.first < y.first; });
+    std::vector<std::string> names;
+    for (const auto& r : ranked) names.emplace_back(r.second);
+    return names;
+}
+
 std::vector<std::shared_ptr<OpsEngineBase>> groupedEngines() {
-    return {std::make_shared<OpsEngine<GroupedGemmFamily<GroupedKind::kABCD>>>(),
-            std::make_shared<OpsEngine<GroupedGemmFamily<GroupedKind::kBCD>>>(),
-            std::make_shared<OpsEngine<GroupedGemmFamily<GroupedKind::kAB>>>()};
+    return {std::make_shared<OpsEngine<GroupedGemmFamily<GroupedKind::kABCD>, GroupedCostFinder>>(),
+            std::make_shared<OpsEngine<GroupedGemmFamily<GroupedKind::kBCD>, GroupedCostFinder>>(),
+            std::make_shared<OpsEngine<GroupedGemmFamily<GroupedKind::kAB>, GroupedCostFinder>>()};
 }
 
 }  // namespace ftrain

@@ -542,7 +542,11 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_half_gemm(GroupedHa
     const int bid = blockIdx.x;
     const int grp = find_group(g.tile_start, g.groups, bid);
     const HalfGemmParams p = g.params[grp];
-    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, kWhole, TA, TB>(p, bid - g.tile_start[grp], 0);
+    // Group starts are multiples of 8, so the group-local id keeps the
+    // hardware id's XCD (id mod 8); ids past the group's tiles are padding.
+    const int local = bid - g.tile_start[grp];
+    if (local >= p.tiles_m * p.tiles_n) return;
+    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, kWhole, TA, TB>(p, local, 0);
 }
 
 // The half-precision tiles (index as in kHalfTiles) for one input type and
@@ -558,12 +562,14 @@ const void* halfKernel(int tile) {
     }
 }
 
-// Grouped variants: 0 = 128x128 (16-byte loads), 1 = 64x64 per-element.
+// Grouped variants: 0 = 128x128 (16-byte loads), 1 = 64x64 per-element,
+// 2 = 256x256 (16-byte loads, 512 threads).
 template <bool BF16, bool TA, bool TB>
 const void* groupedHalfKernel(int which) {
     switch (which) {
         case 0: return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, TA, TB>);
         case 1: return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 64, 64, 32, 2, 2, 2, false, TA, TB>);
+        case 2: return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 256, 256, 64, 2, 4, 1, true, TA, TB>);
         default: return nullptr;
     }
 }

@@ -257,7 +257,7 @@ __global__ __launch_bounds__(256) void simt_gemm(WideParams p) {
 }  // namespace
 
 const void* kernelFor(Variant v, bool ta, bool tb) {
-    if (v >= Variant::kMfma16_256x256 && v <= Variant::kMfma16_256x128S) {
+    if (v >= Variant::kMfma16_256x256 && v <= Variant::kMfma16_128x256) {
         using Fn                     = const void* (*)(int);
         static constexpr Fn table[4] = {mfma16KernelNN, mfma16KernelTN, mfma16KernelNT, mfma16KernelTT};
         return table[(ta ? 1 : 0) + (tb ? 2 : 0)](static_cast<int>(v) - static_cast<int>(Variant::kMfma16_256x256));
@@ -302,7 +302,13 @@ const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool t
         {groupedHalfKernelBf16NN, groupedHalfKernelBf16TN, groupedHalfKernelBf16NT, groupedHalfKernelBf16TT},
         {groupedHalfKernelFp16NN, groupedHalfKernelFp16TN, groupedHalfKernelFp16NT, groupedHalfKernelFp16TT}};
     const int t = input == FTRAIN_NUMERIC_TYPE_FP32 ? 0 : input == FTRAIN_NUMERIC_TYPE_BF16 ? 1 : 2;
-    return table[t][(ta ? 1 : 0) + (tb ? 2 : 0)](which);
+    const int o = (ta ? 1 : 0) + (tb ? 2 : 0);
+    if (t == 0 && (which == 2 || which == 3)) {
+        // The fp32 256x128 / 128x256 tiles of the 16x16x4 family (grouped entries 5 and 6).
+        static constexpr Fn m16[4] = {mfma16KernelNN, mfma16KernelTN, mfma16KernelNT, mfma16KernelTT};
+        return m16[o](which + 3);
+    }
+    return table[t][o](which);
 }
 
 const void* prologueKernel() { return reinterpret_cast<const void*>(&prologue); }

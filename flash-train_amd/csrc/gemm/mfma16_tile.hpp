@@ -72,7 +72,7 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 // barrier, and the single operand set fits the halved register budget.
 template <int BM, int BN, int BK, int WM, int WN, int SPLIT, bool TA, bool TB, int MINB = 1, bool SIMPLE = false,
           int BAND = 4>
-__global__ __launch_bounds__(WM* WN * 64, MINB) void mfma16_gemm(GemmParams p) {
+__device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, int z) {
     constexpr int NT  = WM * WN * 64;
     constexpr int WTM = BM / WM;
     constexpr int WTN = BN / WN;
@@ -100,10 +100,10 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void mfma16_gemm(GemmParams p) {
     const int wcol = (wave % WN) * WTN;
 
     int tm, tn;
-    tile_of<BAND>(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    tile_of<BAND>(bid, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int M = p.m, N = p.n, K = p.k;
-    const int kbeg = SPLIT != kWhole ? blockIdx.z * p.k_chunk : 0;
+    const int kbeg = SPLIT != kWhole ? z * p.k_chunk : 0;
     const int kend = SPLIT != kWhole ? min(K, kbeg + p.k_chunk) : K;
     const int nst  = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void mfma16_gemm(GemmParams p) {
                 if constexpr (SPLIT == kPartial) {
 #pragma unroll
                     for (int t = 0; t < 4; ++t) out[t] = acc[bi][4 * q + t][r];
-                    *reinterpret_cast<floatx4*>(D + (size_t)blockIdx.z * M * N + (size_t)row * N + col + 64 * q) = out;
+                    *reinterpret_cast<floatx4*>(D + (size_t)z * M * N + (size_t)row * N + col + 64 * q) = out;
                 } else {
                     floatx4 cv = floatx4{0.f, 0.f, 0.f, 0.f};
                     if (C != nullptr) cv = *reinterpret_cast<const floatx4*>(C + (size_t)row * ldc + col + 64 * q);
@@ -353,9 +353,44 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void mfma16_gemm(GemmParams p) {
     }
 }
 
+template <int BM, int BN, int BK, int WM, int WN, int SPLIT, bool TA, bool TB, int MINB = 1, bool SIMPLE = false,
+          int BAND = 4>
+__global__ __launch_bounds__(WM* WN * 64, MINB) void mfma16_gemm(GemmParams p) {
+    mfma16_gemm_tile<BM, BN, BK, WM, WN, SPLIT, TA, TB, MINB, SIMPLE, BAND>(p, blockIdx.x, blockIdx.z);
+}
+
+// Index of the group that owns workgroup `bid`: the last g with
+// start[g] <= bid (groups are listed with ascending, distinct starts).
+__device__ __forceinline__ int find_group(const int32_t* __restrict__ start, int groups, int bid) {
+    int lo = 0, hi = groups - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (start[mid] <= bid)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    return lo;
+}
+
+// Grouped GEMM: workgroup bid runs tile bid - start[g] of group g, whose
+// parameters sit in a device table.
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, int MINB, bool SIMPLE>
+__global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_mfma16_gemm(GroupedGemmArgs g) {
+    const int bid = blockIdx.x;
+    const int grp = find_group(g.tile_start, g.groups, bid);
+    const GemmParams p = g.params[grp];
+    // Group starts are multiples of 8, so the group-local id keeps the
+    // hardware id's XCD (id mod 8); ids past the group's tiles are padding.
+    const int local = bid - g.tile_start[grp];
+    if (local >= p.tiles_m * p.tiles_n) return;
+    mfma16_gemm_tile<BM, BN, BK, WM, WN, kWhole, TA, TB, MINB, SIMPLE>(p, local, 0);
+}
+
 // The 16x16x4 variants for one operand orientation: 0 = 256x256 whole-k,
 // 1 = 256x256 split-k, 2 = 256x128 whole-k (two workgroups per CU),
-// 3 = 256x128 split-k.
+// 3 = 256x128 split-k, 4 = 128x256 whole-k (two workgroups per CU),
+// 5 = grouped 256x128, 6 = grouped 128x256.
 template <bool TA, bool TB>
 const void* mfma16Kernel(int which) {
     switch (which) {
@@ -363,6 +398,9 @@ const void* mfma16Kernel(int which) {
         case 1: return reinterpret_cast<const void*>(&mfma16_gemm<256, 256, 16, 2, 2, kPartial, TA, TB>);
         case 2: return reinterpret_cast<const void*>(&mfma16_gemm<256, 128, 16, 2, 2, kWhole, TA, TB, 2, true>);
         case 3: return reinterpret_cast<const void*>(&mfma16_gemm<256, 128, 16, 2, 2, kPartial, TA, TB, 2, true>);
+        case 4: return reinterpret_cast<const void*>(&mfma16_gemm<128, 256, 16, 2, 2, kWhole, TA, TB, 2, true>);
+        case 5: return reinterpret_cast<const void*>(&grouped_mfma16_gemm<256, 128, 16, 2, 2, TA, TB, 2, true>);
+        case 6: return reinterpret_cast<const void*>(&grouped_mfma16_gemm<128, 256, 16, 2, 2, TA, TB, 2, true>);
         default: return nullptr;
     }
 }

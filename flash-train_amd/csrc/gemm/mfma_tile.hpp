@@ -479,7 +479,11 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_mfma_gemm(GroupedGe
     const int bid = blockIdx.x;
     const int grp = find_group(g.tile_start, g.groups, bid);
     const GemmParams p = g.params[grp];
-    mfma_gemm_tile<BM, BN, BK, WM, WN, NBUF, MINB, VEC, kWhole, TA, TB>(p, bid - g.tile_start[grp], 0);
+    // Group starts are multiples of 8, so the group-local id keeps the
+    // hardware id's XCD (id mod 8); ids past the group's tiles are padding.
+    const int local = bid - g.tile_start[grp];
+    if (local >= p.tiles_m * p.tiles_n) return;
+    mfma_gemm_tile<BM, BN, BK, WM, WN, NBUF, MINB, VEC, kWhole, TA, TB>(p, local, 0);
 }
 
 // The variants with all four operand layouts instantiated, keyed by the

@@ -127,6 +127,10 @@ double estimateMicros(Variant v, const GemmShape& s, bool has_c, int cus);
 // Compute units of `device` (cached; 256 when HIP cannot be queried).
 int computeUnits(FTrainDeviceId device);
 
+// Modelled microseconds of one grouped launch over the groups' (kernel-
+// orientation) shapes with tile variant v.
+double groupedMicros(Variant v, const std::vector<GemmShape>& shapes, bool has_c, int cus);
+
 }  // namespace gemm
 
 using GemmEngine = OpsEngine<GemmFamily, ShapeCostFinder>;

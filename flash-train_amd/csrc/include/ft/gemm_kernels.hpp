@@ -111,6 +111,8 @@ enum class Variant : int {
     // per CU, plain stage loop.
     kMfma16_256x128,
     kMfma16_256x128S,
+    // 128x256 tiles of 4 waves of 64x128 (m padded to 128 rows only).
+    kMfma16_128x256,
     // MFMA tiles, 128-bit global loads (needs k % 4 == 0, n % 4 == 0 and
     // 16-byte aligned a/b/c/d).  Suffix S = split-k: per-split partial tiles
     // to a workspace, then a deterministic reduction kernel.
@@ -205,7 +207,9 @@ const void* halfKernelFp16TN(int tile);
 const void* halfKernelFp16NT(int tile);
 const void* halfKernelFp16TT(int tile);
 // Grouped kernels: element type (FTRAIN_NUMERIC_TYPE_FP32 / BF16 / FP16),
-// tile (0 = 128x128 with 16-byte loads, 1 = 64x64 per-element) and operand
+// tile (0 = 128x128 with 16-byte loads, 1 = 64x64 per-element, 2 = the
+// family's large tile: fp32 16x16x4 256x128, bf16/fp16 256x256; 3 = fp32
+// 16x16x4 128x256) and operand
 // orientation.
 const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool tb);
 const void* groupedKernelNN(int which);

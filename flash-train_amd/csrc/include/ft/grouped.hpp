@@ -103,6 +103,13 @@ struct GroupedGemmFamily {
     static GroupedGemmProblem makeProblem(const Args& args);
 };
 
+// Ranks the grouped variants of a's element type by the roofline model of
+// one launch over all groups (gemm::groupedMicros).  Name: "GroupedCost".
+struct GroupedCostFinder {
+    static const char* name() { return "GroupedCost"; }
+    static std::vector<std::string> candidates(const GroupedGemmProblem& problem, const Constraints& constraints);
+};
+
 // The three grouped engines (registered beside the Gemm engine).
 std::vector<std::shared_ptr<OpsEngineBase>> groupedEngines();
 

@@ -59,11 +59,45 @@ def test_every_grouped_kind_gets_an_ops(tlib):
         ops.close()
 
 
+FP32_GROUPED = ["GroupedFp32Mfma16Gemm_256x128", "GroupedFp32Mfma16Gemm_128x256",
+                "GroupedFp32MfmaGemm_128x128", "GroupedFp32MfmaGemm_64x64_Unaligned"]
+
+
 def test_abcd_plan_and_primitive_order(tlib):
+    # Few, small groups: every fp32 tile applies; the cost model puts the
+    # smallest tile first (most workgroups for 256 CUs).
     st, msg, plan = moe_abcd(tlib, [128, 0, 37, 256])
     assert st == c.SUCCESS, msg
-    assert plan.names() == ["GroupedFp32MfmaGemm_128x128", "GroupedFp32MfmaGemm_64x64_Unaligned"]
+    assert sorted(plan.names()) == sorted(FP32_GROUPED)
+    assert plan.names()[0] == "GroupedFp32MfmaGemm_64x64_Unaligned"
     assert all(plan.workspace_bytes(i) == 0 for i in range(len(plan)))
+
+
+def test_large_groups_take_the_large_tiles(tlib):
+    # Mixture-of-experts forward: 8 experts over 16384 tokens, k 4096, n 14336.
+    rows = [2100, 1900, 2300, 1700, 2048, 2200, 1800, 2336]
+    st, msg, plan = moe_abcd(tlib, rows, k=4096, n=14336)
+    assert st == c.SUCCESS, msg
+    assert plan.names()[0] == "GroupedFp32Mfma16Gemm_128x256"
+    st, msg, plan = moe_abcd(tlib, rows, k=4096, n=14336, a_type=c.BF16)
+    assert st == c.SUCCESS, msg
+    assert plan.names()[0] == "GroupedBf16MfmaGemm_256x256"
+
+
+def test_disabled_grouped_finder_falls_back_to_registration_order():
+    import os
+    import subprocess
+    import sys
+
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    prog = ("import sys; sys.path[:0]=[%r, %r, %r]\n" % (os.path.join(repo, "flash-train_amd"), repo,
+                                                        os.path.join(repo, "tests")) +
+            "from test_grouped_host import moe_abcd\nfrom flash_train import capi as c\n"
+            "st, msg, plan = moe_abcd(c.testing_lib(), [128, 0, 37, 256])\nprint(','.join(plan.names()))")
+    out = subprocess.run([sys.executable, "-c", prog], env=dict(os.environ, FTRAIN_DISABLED_FINDERS="GroupedCost"),
+                         capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip().split(",") == FP32_GROUPED
 
 
 def test_unaligned_groups_take_the_per_element_tile(tlib):
@@ -75,10 +109,11 @@ def test_unaligned_groups_take_the_per_element_tile(tlib):
 def test_half_types_select_their_variants(tlib):
     st, msg, plan = moe_abcd(tlib, [64, 32], a_type=c.BF16)
     assert st == c.SUCCESS, msg
-    assert plan.names() == ["GroupedBf16MfmaGemm_128x128", "GroupedBf16MfmaGemm_64x64_Unaligned"]
+    assert sorted(plan.names()) == sorted(["GroupedBf16MfmaGemm_256x256", "GroupedBf16MfmaGemm_128x128",
+                                           "GroupedBf16MfmaGemm_64x64_Unaligned"])
     st, msg, plan = moe_abcd(tlib, [64, 32], a_type=c.FP16, d_type=c.FP16)
     assert st == c.SUCCESS, msg
-    assert plan.names()[0] == "GroupedFp16MfmaGemm_128x128"
+    assert all(n.startswith("GroupedFp16") for n in plan.names()) and len(plan) == 3
 
 
 def test_group_shape_mismatch_is_invalid(tlib):
@@ -95,7 +130,7 @@ def test_mixed_orientations_are_accepted(tlib):
     # Group 0 row-major, group 1 column-major a: one launch per orientation.
     st, msg, plan = moe_abcd(tlib, [64, 32], a_strides=[(64, 1), (1, 32)])
     assert st == c.SUCCESS, msg
-    assert plan.names()[0] == "GroupedFp32MfmaGemm_128x128"
+    assert sorted(plan.names()) == sorted(FP32_GROUPED)
 
 
 def test_group_count_mismatch_is_invalid(tlib):
@@ -146,4 +181,4 @@ def test_ab_with_c_and_d_lists_and_a_column_major(tlib):
     cl = [D([M, N]) for _ in tokens]
     st, msg, plan = ops.args(a=a, b=b, c=cl, d=cl, alpha=al.view, beta=be.view).plan_status_on_device(0)
     assert st == c.SUCCESS, msg
-    assert plan.names()[0] == "GroupedFp32MfmaGemm_128x128"
+    assert sorted(plan.names()) == sorted(FP32_GROUPED)
