@@ -206,7 +206,8 @@ def run_grouped(args, a_h, b_h, c_h, cfg) -> None:
                    "c": c is not None, "primitive": name, "parallelism": "single GPU"},
         "pct_of_matrix_peak": round(100.0 * tflops / peak, 2),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(tflops / peak, 4), "traffic": traffic_from_profiles(workload),
+                     "frac": round(tflops / peak, 4),
+                     "traffic": traffic_from_profiles(workload + ("" if args.dtype == "fp32" else f"_{args.dtype}_nn")),
                      "algorithmic_bytes": alg_bytes, "algorithmic_flops": flops, "kernel_ms": round(ms, 4),
                      "kernel": name},
         "parity": {"rows_checked": 8 * E, "worst_err_over_bound": worst, "ok": ok},

@@ -203,8 +203,14 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                         const int gm = m0 + r, gk = k0 + kq;
                         ra[j][0] = zero4;
                         if (!CHECKED || (gm < M && gk < kend)) ra[j][0] = *reinterpret_cast<const u32x4*>(a_at(gm, gk));
-                    } else {  // 8 x 8 blocks: 8 consecutive m at k = kb..kb+7
-                        const int r = 8 * (idx % (BM / 8)), kb = 8 * (idx / (BM / 8));
+                    } else {
+                        // 8 x 8 blocks: 8 consecutive m at k = kb..kb+7.  Consecutive
+                        // threads take consecutive k blocks of the same 8 rows, so
+                        // each group of 8 lanes writes one contiguous 128-byte run
+                        // of LDS (32 distinct banks) after the transpose; taking
+                        // consecutive row blocks instead put the 8 lanes' rows 288
+                        // dwords apart, an 8-way bank conflict on every write.
+                        const int kb = 8 * (idx % (BK / 8)), r = 8 * (idx / (BK / 8));
                         const int gm = m0 + r;
 #pragma unroll
                         for (int i = 0; i < 8; ++i) {
@@ -225,8 +231,8 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                         const int gn = n0 + c, gk = k0 + kq;
                         rb[j][0] = zero4;
                         if (!CHECKED || (gn < N && gk < kend)) rb[j][0] = *reinterpret_cast<const u32x4*>(b_at(gk, gn));
-                    } else {  // 8 x 8 blocks: 8 consecutive n at k = kb..kb+7
-                        const int c = 8 * (idx % (BN / 8)), kb = 8 * (idx / (BN / 8));
+                    } else {  // 8 x 8 blocks: 8 consecutive n at k = kb..kb+7 (thread order as for a)
+                        const int kb = 8 * (idx % (BK / 8)), c = 8 * (idx / (BK / 8));
                         const int gn = n0 + c;
 #pragma unroll
                         for (int i = 0; i < 8; ++i) {
@@ -267,7 +273,7 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                         const int r = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
                         *reinterpret_cast<u32x4*>(&As[buf][r * SK + kq]) = ra[j][0];
                     } else {
-                        const int r = 8 * (idx % (BM / 8)), kb = 8 * (idx / (BM / 8));
+                        const int kb = 8 * (idx % (BK / 8)), r = 8 * (idx / (BK / 8));
                         u32x4 w[8];
                         transpose8x8(ra[j], w);
 #pragma unroll
@@ -283,7 +289,7 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                         const int c = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
                         *reinterpret_cast<u32x4*>(&Bs[buf][c * SK + kq]) = rb[j][0];
                     } else {
-                        const int c = 8 * (idx % (BN / 8)), kb = 8 * (idx / (BN / 8));
+                        const int kb = 8 * (idx % (BK / 8)), c = 8 * (idx / (BK / 8));
                         u32x4 w[8];
                         transpose8x8(rb[j], w);
 #pragma unroll

@@ -79,8 +79,14 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
     constexpr int TM  = WTM / 16;
     constexpr int TN  = WTN / 16;
     constexpr int KS  = BK / 4;  // k-steps per stage
-    constexpr int SA  = TA ? BM + 4 : BK + 4;
-    constexpr int SB  = TB ? BK + 4 : BN + 4;
+    // LDS row strides (floats).  A 128-bit LDS read is conflict-free when each
+    // half-wave's 32 lanes cover 128 distinct banks; a 128-bit write when each
+    // 8 consecutive lanes cover 32 (measured on MI355X with SQ_LDS_BANK_CONFLICT).
+    // Row-major A: a half-wave reads 16 rows at two 4-float k offsets, so
+    // rows 24 floats apart land on 16 distinct 8-bank slots.  Row-major B: a
+    // half-wave reads two k rows 4 apart, which BN + 16 places 64 banks apart.
+    constexpr int SA  = TA ? BM + 4 : BK + 8;
+    constexpr int SB  = TB ? BK + 4 : BN + 16;
     constexpr int A_ELEMS = TA ? BK * SA : BM * SA;
     constexpr int B_ELEMS = TB ? BN * SB : BK * SB;
     static_assert(TN % 4 == 0 && KS % 4 == 0, "128-bit operand reads");
@@ -119,8 +125,14 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
             r = 4 * (idx % (BM / 4));
             k = idx / (BM / 4);
         } else {
-            r = idx / (BK / 4);
-            k = 4 * (idx % (BK / 4));
+            // Four threads per row of BK = 16.  Within each group of 16 rows
+            // the even rows go to the first half-wave and the odd rows to the
+            // second, so the 8 lanes of one write group cover rows 2 apart
+            // (48 floats: disjoint 32-bank sets at stride 24).
+            static_assert(BK == 16 && NT % 64 == 0, "row permutation assumes BK = 16");
+            const int q = idx >> 2;  // consecutive row slot
+            r = (q & ~15) | ((q & 7) << 1) | ((q >> 3) & 1);
+            k = 4 * (idx & 3);
         }
     };
     auto b_coord = [&](int j, int& k, int& c) {
