@@ -6,41 +6,48 @@ namespace ftrain::gemm {
 namespace {
 
 // name, bm, bn, bk, threads, occupancy, vec, split, gemv, simt, layouts, efficiency, input type,
-// MFMA FLOP/clk/CU (fp32 256; bf16/fp16 4096, the 2.5 PFLOP/s dense peak over 256 CUs at 2.4 GHz)
+// MFMA FLOP/clk/CU (fp32 256; bf16/fp16 4096, the 2.5 PFLOP/s dense peak over 256 CUs at 2.4 GHz),
+// efficiency with one resident workgroup.  The fp32 efficiencies are fitted to Primitive timings
+// on MI355X (every applicable Primitive over 14 shapes from 64x4096x4096 to 16384x14336x4096,
+// random N(0,1) inputs, best of 3 interleaved passes), minimising the time lost by the top pick.
 constexpr SplitKind N = SplitKind::kNone, P = SplitKind::kPartial, A = SplitKind::kAtomic;
 constexpr FTrainNumericType FP32 = FTRAIN_NUMERIC_TYPE_FP32, BF16 = FTRAIN_NUMERIC_TYPE_BF16,
                             FP16 = FTRAIN_NUMERIC_TYPE_FP16;
 constexpr VariantInfo kInfo[] = {
-    {"Fp32Mfma16Gemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, true, 0.88, FP32, 256.0},
-    {"Fp32Mfma16Gemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, true, 0.45, FP32, 256.0},
-    {"Fp32Mfma16Gemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, true, 0.895, FP32, 256.0},
-    {"Fp32Mfma16Gemm_256x128_SplitK", 256, 128, 16, 256, 2, true, P, false, false, true, 0.50, FP32, 256.0},
-    {"Fp32Mfma16Gemm_128x256", 128, 256, 16, 256, 2, true, N, false, false, true, 0.885, FP32, 256.0},
-    {"Fp32MfmaGemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, false, 0.85, FP32, 256.0},
-    {"Fp32MfmaGemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, false, 0.25, FP32, 256.0},
-    {"Fp32MfmaGemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, false, 0.84, FP32, 256.0},
-    {"Fp32MfmaGemm_128x128", 128, 128, 16, 256, 3, true, N, false, false, true, 0.865, FP32, 256.0},
-    {"Fp32MfmaGemm_128x128_SplitK", 128, 128, 16, 256, 3, true, P, false, false, true, 0.55, FP32, 256.0},
-    {"Fp32MfmaGemm_64x256", 64, 256, 16, 256, 2, true, N, false, false, false, 0.76, FP32, 256.0},
-    {"Fp32MfmaGemm_64x256_SplitK", 64, 256, 16, 256, 2, true, P, false, false, false, 0.55, FP32, 256.0},
-    {"Fp32MfmaGemm_256x64", 256, 64, 16, 256, 2, true, N, false, false, false, 0.76, FP32, 256.0},
-    {"Fp32MfmaGemm_256x64_SplitK", 256, 64, 16, 256, 2, true, P, false, false, false, 0.55, FP32, 256.0},
-    {"Fp32MfmaGemm_64x64", 64, 64, 16, 256, 4, true, N, false, false, true, 0.50, FP32, 256.0},
-    {"Fp32MfmaGemm_64x64_SplitK", 64, 64, 16, 256, 4, true, P, false, false, true, 0.50, FP32, 256.0},
-    {"Fp32MfmaGemm_128x128_Unaligned", 128, 128, 16, 256, 2, false, N, false, false, true, 0.70, FP32, 256.0},
-    {"Fp32MfmaGemm_128x128_Unaligned_SplitK", 128, 128, 16, 256, 2, false, P, false, false, true, 0.45, FP32, 256.0},
-    {"Fp32MfmaGemm_64x64_Unaligned", 64, 64, 16, 256, 4, false, N, false, false, true, 0.45, FP32, 256.0},
-    {"Fp32Gemv_SplitK", kGemvRows, kGemvCols, 1, 256, 8, true, A, true, false, false, 0.0, FP32, 256.0},
-    {"Fp32Gemv_Unaligned_SplitK", kGemvRows, kGemvCols, 1, 256, 8, false, A, true, false, false, 0.0, FP32, 256.0},
-    {"Fp32Gemm", 64, 64, 16, 256, 2, false, N, false, true, true, 0.20, FP32, 256.0},
-    {"Bf16MfmaGemm_256x256", 256, 256, 64, 512, 1, true, N, false, false, true, 0.60, BF16, 4096.0},
-    {"Bf16MfmaGemm_128x128", 128, 128, 64, 256, 2, true, N, false, false, true, 0.50, BF16, 4096.0},
-    {"Bf16MfmaGemm_128x128_SplitK", 128, 128, 64, 256, 2, true, P, false, false, true, 0.40, BF16, 4096.0},
-    {"Bf16MfmaGemm_64x64_Unaligned", 64, 64, 32, 256, 2, false, N, false, false, true, 0.15, BF16, 4096.0},
-    {"Fp16MfmaGemm_256x256", 256, 256, 64, 512, 1, true, N, false, false, true, 0.60, FP16, 4096.0},
-    {"Fp16MfmaGemm_128x128", 128, 128, 64, 256, 2, true, N, false, false, true, 0.50, FP16, 4096.0},
-    {"Fp16MfmaGemm_128x128_SplitK", 128, 128, 64, 256, 2, true, P, false, false, true, 0.40, FP16, 4096.0},
-    {"Fp16MfmaGemm_64x64_Unaligned", 64, 64, 32, 256, 2, false, N, false, false, true, 0.15, FP16, 4096.0},
+    {"Fp32Mfma16Gemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, true, 0.905, FP32, 256.0, 0.905},
+    {"Fp32Mfma16Gemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, true, 0.73, FP32, 256.0, 0.73},
+    {"Fp32Mfma16Gemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, true, 0.895, FP32, 256.0, 0.855},
+    {"Fp32Mfma16Gemm_256x128_SplitK", 256, 128, 16, 256, 2, true, P, false, false, true, 0.855, FP32, 256.0, 0.82},
+    {"Fp32Mfma16Gemm_128x256", 128, 256, 16, 256, 2, true, N, false, false, true, 0.895, FP32, 256.0, 0.855},
+    {"Fp32Mfma16Gemm_64x256", 64, 256, 16, 256, 2, true, N, false, false, true, 0.865, FP32, 256.0, 0.915},
+    {"Fp32Mfma16Gemm_64x256_SplitK", 64, 256, 16, 256, 2, true, P, false, false, true, 0.77, FP32, 256.0, 0.82},
+    {"Fp32Mfma16Gemm_256x64", 256, 64, 16, 256, 2, true, N, false, false, true, 0.87, FP32, 256.0, 0.915},
+    {"Fp32Mfma16Gemm_256x64_SplitK", 256, 64, 16, 256, 2, true, P, false, false, true, 0.86, FP32, 256.0, 0.82},
+    {"Fp32MfmaGemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, false, 0.86, FP32, 256.0, 0.86},
+    {"Fp32MfmaGemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, false, 0.74, FP32, 256.0, 0.74},
+    {"Fp32MfmaGemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, false, 0.855, FP32, 256.0, 0.805},
+    {"Fp32MfmaGemm_128x128", 128, 128, 16, 256, 3, true, N, false, false, true, 0.87, FP32, 256.0, 0.78},
+    {"Fp32MfmaGemm_128x128_SplitK", 128, 128, 16, 256, 3, true, P, false, false, true, 0.83, FP32, 256.0, 0.825},
+    {"Fp32MfmaGemm_64x256", 64, 256, 16, 256, 2, true, N, false, false, false, 0.805, FP32, 256.0, 0.67},
+    {"Fp32MfmaGemm_64x256_SplitK", 64, 256, 16, 256, 2, true, P, false, false, false, 0.78, FP32, 256.0, 0.755},
+    {"Fp32MfmaGemm_256x64", 256, 64, 16, 256, 2, true, N, false, false, false, 0.83, FP32, 256.0, 0.775},
+    {"Fp32MfmaGemm_256x64_SplitK", 256, 64, 16, 256, 2, true, P, false, false, false, 0.755, FP32, 256.0, 0.805},
+    {"Fp32MfmaGemm_64x64", 64, 64, 16, 256, 4, true, N, false, false, true, 0.75, FP32, 256.0, 0.77},
+    {"Fp32MfmaGemm_64x64_SplitK", 64, 64, 16, 256, 4, true, P, false, false, true, 0.68, FP32, 256.0, 0.665},
+    {"Fp32MfmaGemm_128x128_Unaligned", 128, 128, 16, 256, 2, false, N, false, false, true, 0.66, FP32, 256.0, 0.675},
+    {"Fp32MfmaGemm_128x128_Unaligned_SplitK", 128, 128, 16, 256, 2, false, P, false, false, true, 0.55, FP32, 256.0, 0.4},
+    {"Fp32MfmaGemm_64x64_Unaligned", 64, 64, 16, 256, 4, false, N, false, false, true, 0.585, FP32, 256.0, 0.45},
+    {"Fp32Gemv_SplitK", kGemvRows, kGemvCols, 1, 256, 8, true, A, true, false, false, 0, FP32, 256.0, 0},
+    {"Fp32Gemv_Unaligned_SplitK", kGemvRows, kGemvCols, 1, 256, 8, false, A, true, false, false, 0, FP32, 256.0, 0},
+    {"Fp32Gemm", 64, 64, 16, 256, 2, false, N, false, true, true, 0.2, FP32, 256.0, 0.2},
+    {"Bf16MfmaGemm_256x256", 256, 256, 64, 512, 1, true, N, false, false, true, 0.6, BF16, 4096.0, 0.6},
+    {"Bf16MfmaGemm_128x128", 128, 128, 64, 256, 2, true, N, false, false, true, 0.5, BF16, 4096.0, 0.5},
+    {"Bf16MfmaGemm_128x128_SplitK", 128, 128, 64, 256, 2, true, P, false, false, true, 0.4, BF16, 4096.0, 0.4},
+    {"Bf16MfmaGemm_64x64_Unaligned", 64, 64, 32, 256, 2, false, N, false, false, true, 0.15, BF16, 4096.0, 0.15},
+    {"Fp16MfmaGemm_256x256", 256, 256, 64, 512, 1, true, N, false, false, true, 0.6, FP16, 4096.0, 0.6},
+    {"Fp16MfmaGemm_128x128", 128, 128, 64, 256, 2, true, N, false, false, true, 0.5, FP16, 4096.0, 0.5},
+    {"Fp16MfmaGemm_128x128_SplitK", 128, 128, 64, 256, 2, true, P, false, false, true, 0.4, FP16, 4096.0, 0.4},
+    {"Fp16MfmaGemm_64x64_Unaligned", 64, 64, 32, 256, 2, false, N, false, false, true, 0.15, FP16, 4096.0, 0.15},
 };
 static_assert(sizeof(kInfo) / sizeof(kInfo[0]) == static_cast<int>(Variant::kCount), "catalog");
 

@@ -9,9 +9,11 @@
 //
 // Model, per variant (microseconds):
 //   compute: workgroups = tiles * splits; each CU runs ceil(wgs / CUs) of
-//            them back to back at the variant's sustained fraction of 256
-//            FP32 matrix FLOP/clk/CU at 2.4 GHz (lower while fewer than its
-//            resident-workgroup count are available).
+//            them back to back at the variant's sustained fraction of its
+//            MFMA FLOP/clk/CU at 2.4 GHz (interpolated down to the variant's
+//            single-workgroup fraction while fewer than its resident count
+//            are available), plus a fixed cost per round of resident
+//            workgroups.
 //   memory : algorithmic bytes (a, b, d, optional c) at 80% of 8 TB/s, plus
 //            the partial tiles (written and read once) for split-k with a
 //            reduction, or the beta*c prologue pass for atomic split-k.
@@ -38,6 +40,9 @@ constexpr double kHbmBytesPerMicro = 8.0e6 * 0.8;  // sustained HBM bytes per mi
 constexpr double kLaunchMicros = 4.0;
 constexpr double kAtomicsPerMicro = 6.0e4;
 constexpr double kPoolMicros      = 2.0;  // stream-ordered workspace acquire + release
+// Fixed cost per round of resident workgroups (operand prologue, epilogue
+// stores, the ramp of the first stages); fitted with the catalog efficiencies.
+constexpr double kRoundMicros     = 8.2;
 constexpr uint64_t kMinSplitDepth = 256;  // reduction depth worth one split-k workgroup
 constexpr uint64_t kMinGemvDepth  = 64;
 
@@ -61,6 +66,15 @@ int computeUnits(FTrainDeviceId device) {
 }
 
 namespace {
+
+// Sustained fraction of the MFMA rate when a CU holds `per_cu` of the
+// launch's workgroups: interpolated between one resident workgroup and the
+// variant's full occupancy.
+double residentEfficiency(const VariantInfo& vi, uint64_t per_cu) {
+    if (vi.occupancy <= 1) return vi.efficiency;
+    const double resident = double(std::min<uint64_t>(std::max<uint64_t>(per_cu, 1), uint64_t(vi.occupancy)));
+    return vi.solo_efficiency + (vi.efficiency - vi.solo_efficiency) * (resident - 1.0) / double(vi.occupancy - 1);
+}
 
 // Modelled time of variant `v` with a given split count (1 = no split).
 double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cus, uint64_t splits) {
@@ -100,12 +114,11 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
     const uint64_t tiles   = ceilDiv(s.m, vi.bm) * ceilDiv(s.n, vi.bn);
     const uint64_t wgs     = tiles * used;
     const uint64_t per_cu  = ceilDiv(wgs, cus);
-    const double fill      = std::sqrt(std::min(1.0, double(per_cu) / double(vi.occupancy)));
     const double depth     = double(std::max<uint64_t>(chunk, vi.bk));
     // SIMT FMAs run at half the matrix rate without packed FP32.
-    const double cu_rate   = vi.flop_per_clk * kClockPerMicro * vi.efficiency * (vi.simt ? 0.5 : 1.0) *
-                           (vi.occupancy > 1 ? fill : 1.0);
-    const double compute   = double(per_cu) * 2.0 * vi.bm * vi.bn * depth / cu_rate;
+    const double cu_rate   = vi.flop_per_clk * kClockPerMicro * residentEfficiency(vi, per_cu) * (vi.simt ? 0.5 : 1.0);
+    const double rounds    = double(ceilDiv(per_cu, uint64_t(vi.occupancy)));
+    const double compute   = double(per_cu) * 2.0 * vi.bm * vi.bn * depth / cu_rate + rounds * kRoundMicros;
     return std::max({compute, bytes / kHbmBytesPerMicro, atomics_us}) + serial_us + launch;
 }
 
@@ -156,9 +169,9 @@ double groupedMicros(Variant v, const std::vector<GemmShape>& shapes, bool has_c
     }
     if (tiles == 0) return kLaunchMicros;
     const uint64_t per_cu = ceilDiv(tiles, cus);
-    const double fill     = std::sqrt(std::min(1.0, double(per_cu) / double(vi.occupancy)));
-    const double cu_rate  = vi.flop_per_clk * kClockPerMicro * vi.efficiency * (vi.occupancy > 1 ? fill : 1.0);
-    const double compute  = double(per_cu) * (flops / double(tiles)) / cu_rate;
+    const double cu_rate  = vi.flop_per_clk * kClockPerMicro * residentEfficiency(vi, per_cu);
+    const double rounds   = double(ceilDiv(per_cu, uint64_t(vi.occupancy)));
+    const double compute  = double(per_cu) * (flops / double(tiles)) / cu_rate + rounds * kRoundMicros;
     return std::max(compute, bytes / kHbmBytesPerMicro) + kLaunchMicros;
 }
 

@@ -257,7 +257,7 @@ __global__ __launch_bounds__(256) void simt_gemm(WideParams p) {
 }  // namespace
 
 const void* kernelFor(Variant v, bool ta, bool tb) {
-    if (v >= Variant::kMfma16_256x256 && v <= Variant::kMfma16_128x256) {
+    if (v >= Variant::kMfma16_256x256 && v <= Variant::kMfma16_256x64S) {
         using Fn                     = const void* (*)(int);
         static constexpr Fn table[4] = {mfma16KernelNN, mfma16KernelTN, mfma16KernelNT, mfma16KernelTT};
         return table[(ta ? 1 : 0) + (tb ? 2 : 0)](static_cast<int>(v) - static_cast<int>(Variant::kMfma16_256x256));
@@ -304,9 +304,9 @@ const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool t
     const int t = input == FTRAIN_NUMERIC_TYPE_FP32 ? 0 : input == FTRAIN_NUMERIC_TYPE_BF16 ? 1 : 2;
     const int o = (ta ? 1 : 0) + (tb ? 2 : 0);
     if (t == 0 && (which == 2 || which == 3)) {
-        // The fp32 256x128 / 128x256 tiles of the 16x16x4 family (grouped entries 5 and 6).
+        // The fp32 256x128 / 128x256 tiles of the 16x16x4 family (grouped entries 16 and 17).
         static constexpr Fn m16[4] = {mfma16KernelNN, mfma16KernelTN, mfma16KernelNT, mfma16KernelTT};
-        return m16[o](which + 3);
+        return m16[o](which + 14);
     }
     return table[t][o](which);
 }

@@ -402,7 +402,9 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_mfma16_gemm(Grouped
 // The 16x16x4 variants for one operand orientation: 0 = 256x256 whole-k,
 // 1 = 256x256 split-k, 2 = 256x128 whole-k (two workgroups per CU),
 // 3 = 256x128 split-k, 4 = 128x256 whole-k (two workgroups per CU),
-// 5 = grouped 256x128, 6 = grouped 128x256.
+// 5 / 6 = 64x256 whole-k / split-k, 7 / 8 = 256x64 whole-k / split-k (4 waves
+// of 64x64, two workgroups per CU, pipelined loop); grouped: 16 = 256x128,
+// 17 = 128x256.
 template <bool TA, bool TB>
 const void* mfma16Kernel(int which) {
     switch (which) {
@@ -411,8 +413,12 @@ const void* mfma16Kernel(int which) {
         case 2: return reinterpret_cast<const void*>(&mfma16_gemm<256, 128, 16, 2, 2, kWhole, TA, TB, 2, true>);
         case 3: return reinterpret_cast<const void*>(&mfma16_gemm<256, 128, 16, 2, 2, kPartial, TA, TB, 2, true>);
         case 4: return reinterpret_cast<const void*>(&mfma16_gemm<128, 256, 16, 2, 2, kWhole, TA, TB, 2, true>);
-        case 5: return reinterpret_cast<const void*>(&grouped_mfma16_gemm<256, 128, 16, 2, 2, TA, TB, 2, true>);
-        case 6: return reinterpret_cast<const void*>(&grouped_mfma16_gemm<128, 256, 16, 2, 2, TA, TB, 2, true>);
+        case 5: return reinterpret_cast<const void*>(&mfma16_gemm<64, 256, 16, 1, 4, kWhole, TA, TB, 2>);
+        case 6: return reinterpret_cast<const void*>(&mfma16_gemm<64, 256, 16, 1, 4, kPartial, TA, TB, 2>);
+        case 7: return reinterpret_cast<const void*>(&mfma16_gemm<256, 64, 16, 4, 1, kWhole, TA, TB, 2>);
+        case 8: return reinterpret_cast<const void*>(&mfma16_gemm<256, 64, 16, 4, 1, kPartial, TA, TB, 2>);
+        case 16: return reinterpret_cast<const void*>(&grouped_mfma16_gemm<256, 128, 16, 2, 2, TA, TB, 2, true>);
+        case 17: return reinterpret_cast<const void*>(&grouped_mfma16_gemm<128, 256, 16, 2, 2, TA, TB, 2, true>);
         default: return nullptr;
     }
 }

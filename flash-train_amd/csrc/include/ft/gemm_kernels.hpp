@@ -113,6 +113,12 @@ enum class Variant : int {
     kMfma16_256x128S,
     // 128x256 tiles of 4 waves of 64x128 (m padded to 128 rows only).
     kMfma16_128x256,
+    // Skinny 64x256 / 256x64 tiles (4 waves of 64x64, two workgroups per CU),
+    // whole-k and split-k.
+    kMfma16_64x256,
+    kMfma16_64x256S,
+    kMfma16_256x64,
+    kMfma16_256x64S,
     // MFMA tiles, 128-bit global loads (needs k % 4 == 0, n % 4 == 0 and
     // 16-byte aligned a/b/c/d).  Suffix S = split-k: per-split partial tiles
     // to a workspace, then a deterministic reduction kernel.
@@ -171,9 +177,10 @@ struct VariantInfo {
     bool gemv;
     bool simt;
     bool layouts;       // instantiated for column-major a and b as well (else row-major a and b only)
-    double efficiency;
+    double efficiency;        // sustained fraction of the MFMA rate with `occupancy` workgroups resident per CU
     FTrainNumericType input;  // element type of a and b
-    double flop_per_clk;      // dense MFMA FLOP per clock per CU for that type  // fraction of the FP32 matrix peak the tile sustains (cost model)
+    double flop_per_clk;      // dense MFMA FLOP per clock per CU for that type
+    double solo_efficiency;   // the same with a single resident workgroup (equal to efficiency when occupancy is 1)
 };
 
 // Largest split-k workspace (partial tiles) a Primitive will use.

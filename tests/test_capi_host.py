@@ -495,19 +495,25 @@ def rank(tlib, m, n, k, addr=FAKE, with_c=False, device=0):
 
 
 def test_finder_choices_for_the_baseline_configs(tlib):
-    # Measured on MI355X: the 16x16x4 256x128 tile at two workgroups per CU beats the 256x256
-    # tile (one per CU) and the 32x32x2 128x128 tile at 8192^3 (140.7 / 139.4 / 136.7 TFLOP/s),
-    # MLP fwd (141.6 / 137.1 / 136.4) and MLP dgrad (140.9 / 138.4 / 135.6).
-    assert rank(tlib, 8192, 8192, 8192)[0] == "Fp32Mfma16Gemm_256x128"
-    assert rank(tlib, 16384, 14336, 4096)[0] == "Fp32Mfma16Gemm_256x128"
-    assert rank(tlib, 16384, 4096, 14336)[0] == "Fp32Mfma16Gemm_256x128"
-    # 6144^3: 256x256 tiles would leave 2.25 tiles per CU; the 128x128 tile divides evenly.
+    # Best of 3 interleaved passes over every applicable Primitive, MI355X, N(0,1) inputs (us):
+    # 8192^3: Fp32Mfma16Gemm_256x256 7771, _128x256 7811, _256x128 7834, Fp32MfmaGemm_128x128 7921.
+    # MLP fwd: _128x256 13620, _256x128 13655, _256x256 13673 (all within 0.4%).
+    assert rank(tlib, 8192, 8192, 8192)[0] == "Fp32Mfma16Gemm_256x256"
+    assert rank(tlib, 16384, 14336, 4096)[0] in ("Fp32Mfma16Gemm_256x256", "Fp32Mfma16Gemm_128x256",
+                                                  "Fp32Mfma16Gemm_256x128")
+    assert rank(tlib, 16384, 4096, 14336)[0].startswith("Fp32Mfma16Gemm_")
+    # 6144^3: the 32x32 128x128 tile 3361, the 16x16 256x64 tile 3442, 256x256 tiles 4373 (2.25 per CU).
     assert rank(tlib, 6144, 6144, 6144)[0] == "Fp32MfmaGemm_128x128"
     assert rank(tlib, 4096, 4096, 4096, with_c=True)[0].startswith("Fp32Mfma16Gemm_")
+    # 2048^3: the 16x16 256x64 / 64x256 tiles (141.7 / 142.5) beat split-k (170+) and 256x128 (268).
+    assert rank(tlib, 2048, 2048, 2048)[0] in ("Fp32Mfma16Gemm_256x64", "Fp32Mfma16Gemm_64x256")
+    # 1024^3: whole-k 64x64 (29.9) against the best split-k tile (38.5).
+    assert rank(tlib, 1024, 1024, 1024)[0] == "Fp32MfmaGemm_64x64"
     assert rank(tlib, 1, 8192, 8192)[0] == "Fp32Gemv_SplitK"
-    assert rank(tlib, 256, 256, 65536)[0].endswith("_SplitK")
-    assert rank(tlib, 64, 4096, 4096)[0].endswith("_SplitK")
-    assert rank(tlib, 4096, 64, 4096)[0].endswith("_SplitK")
+    # Deep or skinny: split-k on the 16x16 skinny tiles (88.3, 34.9, 33.6).
+    assert rank(tlib, 256, 256, 65536)[0] == "Fp32Mfma16Gemm_256x64_SplitK"
+    assert rank(tlib, 64, 4096, 4096)[0] == "Fp32Mfma16Gemm_64x256_SplitK"
+    assert rank(tlib, 4096, 64, 4096)[0] == "Fp32Mfma16Gemm_256x64_SplitK"
     # Odd sizes: no 128-bit variant applies.
     odd = rank(tlib, 127, 97, 33)
     assert odd and all(("Unaligned" in n) or n == "Fp32Gemm" for n in odd)
