@@ -382,7 +382,10 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
                                                m, n, k, k, tm, tn, l.lda, l.ldb, l.ldc, l.ldd});
         }
         for (int o = 0; o < 4; ++o)
-            if (buckets_[o].tiles > 0) buckets_[o].kernel = gemm::groupedKernelFor(v_->input, v_->which, o & 1, o & 2);
+            if (buckets_[o].tiles > 0) {
+                buckets_[o].kernel  = gemm::groupedKernelFor(v_->input, v_->which, o & 1, o & 2);
+                buckets_[o].threads = gemm::blockThreads(v_->tile, o & 1, o & 2);
+            }
         table_.reset();
     }
 
@@ -429,11 +432,11 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
             if (!half) {
                 GroupedGemmArgs args{reinterpret_cast<const GemmParams*>(base + bk.param_off), start, groups};
                 void* kargs[] = {&args};
-                check(hipLaunchKernel(bk.kernel, dim3(uint32_t(bk.tiles)), dim3(uint32_t(gemm::info(v_->tile).threads)), kargs, 0, r.stream), v_->name);
+                check(hipLaunchKernel(bk.kernel, dim3(uint32_t(bk.tiles)), dim3(uint32_t(bk.threads)), kargs, 0, r.stream), v_->name);
             } else {
                 GroupedHalfArgs args{reinterpret_cast<const HalfGemmParams*>(base + bk.param_off), start, groups};
                 void* kargs[] = {&args};
-                check(hipLaunchKernel(bk.kernel, dim3(uint32_t(bk.tiles)), dim3(uint32_t(gemm::info(v_->tile).threads)), kargs, 0, r.stream), v_->name);
+                check(hipLaunchKernel(bk.kernel, dim3(uint32_t(bk.tiles)), dim3(uint32_t(bk.threads)), kargs, 0, r.stream), v_->name);
             }
         }
     }
@@ -446,6 +449,7 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
         std::vector<int32_t> tile_start;
         int32_t tiles       = 0;
         const void* kernel  = nullptr;
+        int threads         = 256;
         size_t param_off    = 0;
         size_t start_off    = 0;
     };

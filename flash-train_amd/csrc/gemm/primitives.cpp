@@ -78,18 +78,19 @@ Result commonChecks(const GemmProblem& p, FTrainNumericType input) {
     return Result{};
 }
 
-// The catalog's workgroup size must fit the kernel's launch bounds (a
-// mismatch would only surface as a launch failure).  Checked when HIP can
-// describe the kernel, i.e. on a host with a device.
+// The launch's workgroup size must equal the kernel's launch bounds (every
+// kernel here declares its exact size: a larger launch fails, a smaller one
+// would leave part of each tile uncomputed).  Checked when HIP can describe
+// the kernel, i.e. on a host with a device.
 void checkBlockSize(const void* kernel, int threads, const char* name) {
     hipFuncAttributes attr{};
     if (hipFuncGetAttributes(&attr, kernel) != hipSuccess) {
         (void)hipGetLastError();
         return;
     }
-    if (attr.maxThreadsPerBlock < threads)
-        throw Exception(FTRAIN_STATUS_INTERNAL_ERROR, "%s: catalog workgroup size %d exceeds the kernel's limit %d", name,
-                        threads, attr.maxThreadsPerBlock);
+    if (attr.maxThreadsPerBlock != threads)
+        throw Exception(FTRAIN_STATUS_INTERNAL_ERROR, "%s: workgroup size %d does not match the kernel's launch bounds %d",
+                        name, threads, attr.maxThreadsPerBlock);
 }
 
 void check(hipError_t e, const char* what) {
@@ -170,8 +171,9 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
         wide_ = WideParams{a, b, c, d, alpha, beta, s.m, s.n, s.k, a_rs, a_cs, b_rs, b_cs, g.ldc, g.ldd};
 
         kernel_ = gemm::kernelFor(v_, g.ta, g.tb);
-        checkBlockSize(kernel_, info_->threads, info_->name);
-        block_  = dim3(info_->threads);
+        const int threads = gemm::blockThreads(v_, g.ta, g.tb);
+        checkBlockSize(kernel_, threads, info_->name);
+        block_  = dim3(threads);
         if (info_->simt) {
             const uint64_t tiles = ceilDiv(s.m, 64) * ceilDiv(s.n, 64);
             grid_                = dim3(static_cast<uint32_t>(std::min<uint64_t>(tiles, 1u << 20)));
