@@ -394,9 +394,12 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
         const bool half = v_->input != FTRAIN_NUMERIC_TYPE_FP32;
         if (!table_) {
             // The per-group parameter tables live on the device for the
-            // Plan's lifetime; they are uploaded on the first execution, on
-            // the execution stream, ahead of the kernels.  Layout per
-            // orientation bucket: parameters, then tile starts (16-byte
+            // Plan's lifetime.  They are uploaded once, on the first
+            // execution, with a blocking copy: later executions may use other
+            // streams, which must find the table complete.  A blocking copy
+            // is illegal under stream capture, so the first execution cannot
+            // be captured (later ones can: they only launch kernels).  Layout
+            // per orientation bucket: parameters, then tile starts (16-byte
             // aligned sections).
             size_t total = 0;
             for (Bucket& bk : buckets_) {
@@ -407,22 +410,29 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
                 total += (bk.tile_start.size() * sizeof(int32_t) + 15) / 16 * 16;
             }
             if (total == 0) return;
+            hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+            check(hipStreamIsCapturing(r.stream, &capture), v_->name);
+            if (capture != hipStreamCaptureStatusNone)
+                throw Exception(FTRAIN_STATUS_UNSUPPORTED,
+                                "%s: the first execution of a grouped Plan uploads its parameter table and cannot be "
+                                "captured; execute the Plan once before capturing it",
+                                v_->name);
             void* buf = nullptr;
             if (hipMalloc(&buf, total) != hipSuccess) {
                 (void)hipGetLastError();
                 throw Exception(FTRAIN_STATUS_OUT_OF_MEMORY, "%s: device parameter table of %zu bytes", v_->name, total);
             }
-            table_.reset(buf, [](void* q) { (void)hipFree(q); });
+            std::shared_ptr<void> table(buf, [](void* q) { (void)hipFree(q); });
             for (const Bucket& bk : buckets_) {
                 if (bk.tiles == 0) continue;
                 const void* host = half ? static_cast<const void*>(bk.half_params.data()) : static_cast<const void*>(bk.params.data());
                 const size_t bytes = half ? bk.half_params.size() * sizeof(HalfGemmParams) : bk.params.size() * sizeof(GemmParams);
-                check(hipMemcpyAsync(static_cast<char*>(buf) + bk.param_off, host, bytes, hipMemcpyHostToDevice, r.stream),
-                      v_->name);
-                check(hipMemcpyAsync(static_cast<char*>(buf) + bk.start_off, bk.tile_start.data(),
-                                     bk.tile_start.size() * sizeof(int32_t), hipMemcpyHostToDevice, r.stream),
+                check(hipMemcpy(static_cast<char*>(buf) + bk.param_off, host, bytes, hipMemcpyHostToDevice), v_->name);
+                check(hipMemcpy(static_cast<char*>(buf) + bk.start_off, bk.tile_start.data(),
+                                bk.tile_start.size() * sizeof(int32_t), hipMemcpyHostToDevice),
                       v_->name);
             }
+            table_ = std::move(table);  // published only once complete
         }
         char* base = static_cast<char*>(table_.get());
         for (const Bucket& bk : buckets_) {
