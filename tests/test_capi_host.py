@@ -285,6 +285,53 @@ def test_storage_view_validation(lib, gemm_ops, view, why):
     lib.ftrainArgsDestroy(h)
 
 
+@pytest.mark.parametrize("make", [
+    # Zero-length dimension (reference storage_view_test.cpp:101-109).
+    lambda: c.View(None, [2, 0, 4]),
+    # Semantically odd strides are stored without validation (:111-120).
+    lambda: c.View(None, [2, 4], index_type=c.INDEX_INVALID, strides=[0, -1]),
+    # Highest defined numeric and index types (:122-133).
+    lambda: c.View(None, [4], numeric_type=c.NUMERIC_TYPE_COUNT - 1, index_type=c.INDEX_TYPE_COUNT - 1),
+])
+def test_storage_view_acceptances(lib, gemm_ops, make):
+    view = make()
+    h = args_handle(lib, gemm_ops)
+    assert lib.ftrainArgsSetTensor(h, gemm_ops.ids["a"], view.sv) == c.SUCCESS, lib.ftrainGetLastMessage()
+    lib.ftrainArgsDestroy(h)
+
+
+def test_rank_zero_with_non_null_metadata_is_a_scalar(lib, gemm_ops):
+    # Non-null dims and strides with num_dims 0 describe a scalar (reference
+    # storage_view_test.cpp:87-99): accepted for alpha.
+    value = ctypes.c_float(1.0)
+    dims, strides = (ctypes.c_int64 * 1)(17), (ctypes.c_int64 * 1)(19)
+    sv = c.StorageView(ctypes.addressof(value), ctypes.cast(dims, ctypes.POINTER(ctypes.c_int64)),
+                       ctypes.cast(strides, ctypes.POINTER(ctypes.c_int64)), 0, c.FP32, c.INDEX_INVALID, True)
+    h = args_handle(lib, gemm_ops)
+    assert lib.ftrainArgsSetTensor(h, gemm_ops.ids["alpha"], sv) == c.SUCCESS, lib.ftrainGetLastMessage()
+    lib.ftrainArgsDestroy(h)
+
+
+def test_failed_set_keeps_the_previous_operand(tlib, tops):
+    # A Set that fails validation leaves the operand already bound in place
+    # (reference runtime_api_test.cpp:587-628 checks the same for operation
+    # attributes): the Plan is built from the earlier, valid views.
+    h = ctypes.c_void_p()
+    c.check(tlib.ftrainArgsCreate(ctypes.byref(h), tops.ops), l=tlib)
+    al, be = c.HostScalar(1.0), c.HostScalar(0.0)
+    views = {"a": V([64, 32]), "b": V([32, 48]), "c": V([64, 48], None), "d": V([64, 48]),
+             "alpha": al.view, "beta": be.view}
+    for role, v in views.items():
+        c.check(tlib.ftrainArgsSetTensor(h, tops.ids[role], v.sv), l=tlib)
+    assert tlib.ftrainArgsSetTensor(h, tops.ids["a"], V([64, -1]).sv) == c.INVALID_ARGUMENT
+    assert tlib.ftrainArgsSetGemm(h, tops.gemm_id, c.NUMERIC_TYPE_COUNT) == c.INVALID_ARGUMENT
+    c.check(tlib.ftrainArgsSetGemm(h, tops.gemm_id, c.FP32), l=tlib)
+    p = ctypes.c_void_p()
+    assert tlib.ftrainTestingPlanCreateOnDevice(ctypes.byref(p), h, 0) == c.SUCCESS, c.last_message(tlib)
+    tlib.ftrainPlanDestroy(p)
+    tlib.ftrainArgsDestroy(h)
+
+
 def test_storage_view_null_dims_for_nonscalar(lib, gemm_ops):
     h = args_handle(lib, gemm_ops)
     sv = c.StorageView(FAKE, None, None, 2, c.FP32, c.INDEX_CONTINUOUS, False)
