@@ -116,6 +116,9 @@ GroupOperand expandGrouped(const GroupedTensor& gt, int which) {
     } else {
         for (uint32_t g = 0; g < G; ++g) s0[g] = cols[g];
     }
+    // Element offsets stay below this bound, with each group's extent, so
+    // that byte addresses cannot overflow.
+    constexpr int64_t max_off = std::numeric_limits<int64_t>::max() / 8;
     std::vector<int64_t> off(G, 0);
     if (gt.offsets()) {
         off = readIndexArray(*gt.offsets(), G, name, "offsets");
@@ -123,6 +126,8 @@ GroupOperand expandGrouped(const GroupedTensor& gt, int which) {
         int64_t run = 0;
         for (uint32_t g = 0; g < G; ++g) {
             off[g] = run;
+            if (rows[g] != 0 && cols[g] > (max_off - run) / rows[g])
+                throw Exception(FTRAIN_STATUS_OVERFLOW, "grouped %s: packed group offsets overflow", name);
             run += rows[g] * cols[g];
         }
     }
@@ -132,12 +137,19 @@ GroupOperand expandGrouped(const GroupedTensor& gt, int which) {
     const size_t eb = elementBytes(out.type);
     for (uint32_t g = 0; g < G; ++g) {
         if (off[g] < 0) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped %s: offsets[%u] is negative", name, g);
+        if (off[g] >= max_off)
+            throw Exception(FTRAIN_STATUS_OVERFLOW, "grouped %s: offsets[%u] overflows the address range", name, g);
         GroupMatrix& m = out.groups[g];
         m.rows = rows[g];
         m.cols = cols[g];
         m.memory = v.memory() == nullptr ? nullptr : static_cast<const char*>(v.memory()) + static_cast<size_t>(off[g]) * eb;
         if (const char* why = groupLayout(rows[g], cols[g], s0[g], s1[g], m.layout))
             throw Exception(FTRAIN_STATUS_UNSUPPORTED, "grouped %s, group %u: %s", name, g, why);
+        // The group's last element: offset plus its (already bounded) extent.
+        const int64_t extent = (rows[g] <= 1 ? 0 : (rows[g] - 1) * s0[g]) + (cols[g] <= 1 ? 0 : (cols[g] - 1) * s1[g]);
+        if (extent > max_off - off[g])
+            throw Exception(FTRAIN_STATUS_OVERFLOW, "grouped %s, group %u: offset plus extent overflows the address range",
+                            name, g);
     }
     return out;
 }

@@ -182,3 +182,27 @@ def test_ab_with_c_and_d_lists_and_a_column_major(tlib):
     st, msg, plan = ops.args(a=a, b=b, c=cl, d=cl, alpha=al.view, beta=be.view).plan_status_on_device(0)
     assert st == c.SUCCESS, msg
     assert sorted(plan.names()) == sorted(FP32_GROUPED)
+
+
+def test_descriptor_values_that_overflow_addresses_are_rejected(tlib):
+    # Offsets or packed extents past the addressable range report OVERFLOW
+    # instead of forming wrapped pointers.
+    G, k, n = 2, 64, 96
+    al, be = scalars()
+
+    def status(a_spec):
+        ops = c.GroupedOps("abcd", l=tlib)
+        b = c.GroupedSpec(D([G * k, n]), G, dims=[(k, n)] * G)
+        cd = lambda: c.GroupedSpec(D([128, n]), G, dims=[(64, n)] * G)
+        args = ops.args(a=a_spec, b=b, c=cd(), d=cd(), alpha=al.view, beta=be.view)
+        st, msg, _ = args.plan_status_on_device(0)
+        return st, msg
+
+    huge = 1 << 61
+    st, msg = status(c.GroupedSpec(D([128, k]), G, dims=[(64, k)] * G, offsets=[0, huge]))
+    assert st == c.OVERFLOW and "offsets[1]" in msg, msg
+    st, msg = status(c.GroupedSpec(D([128, k]), G, dims=[(64, k)] * G, offsets=[0, (1 << 60) - 64]))
+    assert st == c.OVERFLOW and "extent" in msg, msg
+    # Packed groups (no offsets) whose sizes overflow the running offset.
+    st, msg = status(c.GroupedSpec(D([128, k]), G, dims=[(1 << 40, 1 << 40), (64, k)]))
+    assert st == c.OVERFLOW and "packed" in msg, msg
