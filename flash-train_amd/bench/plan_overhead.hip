@@ -3,7 +3,9 @@
 // without synchronizing (host wall clock / iters), plus the convenience
 // ftrainGemm call, which re-creates Args and Plan per call (selection-cache
 // hit).  Mirrors the reference's L2/L3 tiers
-// (benchmarks/csrc/ftrain_bench.cpp:103-177).  Prints one JSON object.
+// (benchmarks/csrc/ftrain_bench.cpp:103-177).  For scale it also times bare
+// hipLaunchKernel calls of an empty kernel taking an argument block of the
+// GEMM kernels' size: the floor under any launch.  Prints one JSON object.
 //
 // usage: plan_overhead [m n k] [iters]
 #include <chrono>
@@ -11,7 +13,7 @@
 #include <cstdlib>
 #include <vector>
 
-#include <hip/hip_runtime_api.h>
+#include <hip/hip_runtime.h>
 
 #include <flash_train/flash_train.h>
 
@@ -31,6 +33,16 @@
             return 3;                                                            \
         }                                                                        \
     } while (0)
+
+// Same size as the GEMM kernels' parameter block (pointers, scalars, shape,
+// leading dimensions).
+struct EmptyArgs {
+    const void* p[4];
+    float s[2];
+    int32_t i[6];
+    int64_t ld[4];
+};
+__global__ void empty_kernel(EmptyArgs) {}
 
 static FTrainStorageView mat(void* p, const int64_t* dims) {
     return FTrainStorageView{p, dims, nullptr, 2, FTRAIN_NUMERIC_TYPE_FP32, FTRAIN_INDEX_TYPE_CONTINUOUS, false};
@@ -113,12 +125,26 @@ int main(int argc, char** argv) {
     CHECK_HIP(hipStreamSynchronize(stream));
     const double conv_us = std::chrono::duration<double, std::micro>(t4 - t3).count() / conv_iters;
 
-    // Bare hipLaunchKernel floor for comparison is not measurable without a
-    // kernel handle here; report the Plan numbers.
+    // Bare launch floor: the same number of hipLaunchKernel calls of an empty
+    // kernel on the same stream.
+    EmptyArgs ea{};
+    void* eargs[] = {&ea};
+    for (int i = 0; i < 100; ++i)
+        CHECK_HIP(hipLaunchKernel(reinterpret_cast<const void*>(&empty_kernel), dim3(1), dim3(64), eargs, 0, stream));
+    CHECK_HIP(hipStreamSynchronize(stream));
+    auto t5 = clock::now();
+    for (int i = 0; i < iters; ++i)
+        CHECK_HIP(hipLaunchKernel(reinterpret_cast<const void*>(&empty_kernel), dim3(1), dim3(64), eargs, 0, stream));
+    auto t6 = clock::now();
+    CHECK_HIP(hipStreamSynchronize(stream));
+    const double bare_us = std::chrono::duration<double, std::micro>(t6 - t5).count() / iters;
+
     std::printf(
         "{\"shape\": [%lld, %lld, %lld], \"primitive\": \"%s\", \"iters\": %d, \"plan_execute_host_us\": %.3f, "
-        "\"plan_execute_with_drain_us\": %.3f, \"device_us_per_call\": %.3f, \"convenience_host_us\": %.3f}\n",
-        (long long)m, (long long)n, (long long)k, name, iters, exec_us, exec_drain_us, ms * 1000.0 / 1000, conv_us);
+        "\"plan_execute_with_drain_us\": %.3f, \"device_us_per_call\": %.3f, \"convenience_host_us\": %.3f, "
+        "\"bare_launch_host_us\": %.3f}\n",
+        (long long)m, (long long)n, (long long)k, name, iters, exec_us, exec_drain_us, ms * 1000.0 / 1000, conv_us,
+        bare_us);
 
     ftrainPlanDestroy(plan);
     ftrainArgsDestroy(args);

@@ -134,9 +134,9 @@ def build_torch_binding() -> None:
 
 def build_plan_overhead() -> None:
     os.makedirs(os.path.join(HERE, "bench"), exist_ok=True)
-    src = os.path.join(HERE, "bench", "plan_overhead.cpp")
+    src = os.path.join(HERE, "bench", "plan_overhead.hip")
     out = os.path.join(HERE, "bench", "plan_overhead")
-    run([HIPCC, "-O2", "-std=c++17", f"-I{os.path.join(REPO, 'include')}", src, "-o", out, f"-L{PKG}",
+    run([HIPCC, "-O2", "-std=c++17", *DEVICE, f"-I{os.path.join(REPO, 'include')}", src, "-o", out, f"-L{PKG}",
          "-lflash_train", f"-Wl,-rpath,{PKG}", f"-Wl,-rpath,{ROCM}/lib"])
 
 
