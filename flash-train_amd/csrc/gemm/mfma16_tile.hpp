@@ -259,7 +259,12 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
         // last stage the loads re-read the final stage and the extra LDS
         // writes land in a buffer nobody reads again.
         constexpr int NM    = KS * TM * TN;
-        constexpr int FIRST = NM / 2;
+        // MFMAs before the barrier; the rest cover the next stage's operand
+        // reads.  Measured on the 256x256 tile at 8192^3: 7/8 of the stage
+        // 142.0 TFLOP/s, 1/2 141.5, 1/4 140.8.  A column-major A keeps 1/2:
+        // its split-k 256x256 instantiation spills 100 bytes per lane with
+        // 7/8 (36 with 1/2).
+        constexpr int FIRST = TA ? NM / 2 : NM * 7 / 8;
         floatx4 av[2][TM][KS / 4];
         float bv[2][KS][TN];
         auto clamp_k0 = [&](int stage) { return kbeg + min(stage, nst - 1) * BK; };
