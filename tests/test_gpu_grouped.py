@@ -208,3 +208,53 @@ def test_abcd_explicit_offsets_and_padded_strides(capi, oracle):
         store_d.fill_(7.0)
 
     run_all(capi, args, check)
+
+
+def test_many_small_groups(capi, oracle):
+    # 300 groups of 0-40 rows: the workgroup -> group binary search over
+    # hundreds of tile starts, every tile padded to its group's XCD slot.
+    rng = np.random.default_rng(7)
+    G, k, n = 300, 32, 48
+    m_list = [int(x) for x in rng.integers(0, 41, size=G)]
+    M = sum(m_list)
+    a = rnd((M, k), 50).cuda()
+    b = rnd((G * k, n), 51).cuda()
+    d = torch.full((M, n), float("nan"), device="cuda")
+    ops = capi.GroupedOps("abcd")
+    al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+    dims = [(m, n) for m in m_list]
+    args = ops.args(a=capi.GroupedSpec(capi.matrix(a), G, dims=[(m, k) for m in m_list]),
+                    b=capi.GroupedSpec(capi.matrix(b, [k, n]), G),
+                    c=capi.GroupedSpec(capi.View(None, [M, n]), G, dims=dims),
+                    d=capi.GroupedSpec(capi.matrix(d), G, dims=dims), alpha=al.view, beta=be.view)
+    a_h, b_h = a.cpu().numpy(), b.cpu().numpy()
+
+    def check(name):
+        d_h, row = d.cpu().numpy(), 0
+        for g, m in enumerate(m_list):
+            ref = oracle.gemm_f64(a_h[row:row + m], b_h[g * k:(g + 1) * k], None, 1.0, 0.0)
+            close(oracle, d_h[row:row + m], ref, k, what=(name, g))
+            row += m
+        d.fill_(float("nan"))
+
+    run_all(capi, args, check)
+
+
+def test_no_groups_and_all_empty_groups_launch_nothing(capi):
+    k, n = 32, 48
+    sentinel = torch.full((8, n), 3.0, device="cuda")
+    for m_list in ([], [0, 0, 0]):
+        G = len(m_list)
+        ops = capi.GroupedOps("abcd")
+        al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+        dims = [(m, n) for m in m_list]
+        args = ops.args(a=capi.GroupedSpec(capi.matrix(sentinel[:, :k].contiguous()), G, dims=[(m, k) for m in m_list]),
+                        b=capi.GroupedSpec(capi.View(sentinel.data_ptr(), [k, n]), G),
+                        c=capi.GroupedSpec(capi.View(None, [8, n]), G, dims=dims),
+                        d=capi.GroupedSpec(capi.matrix(sentinel), G, dims=dims), alpha=al.view, beta=be.view)
+        plan = args.plan()
+        args.close()
+        for i in range(len(plan)):
+            plan.execute(i)
+        torch.cuda.synchronize()
+        assert torch.all(sentinel == 3.0), m_list
