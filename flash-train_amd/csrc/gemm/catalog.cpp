@@ -10,7 +10,7 @@ namespace {
 // efficiency with one resident workgroup.  The fp32 efficiencies are fitted to Primitive timings
 // on MI355X (every applicable Primitive over 14 shapes from 64x4096x4096 to 16384x14336x4096,
 // random N(0,1) inputs, best of 3 interleaved passes), minimising the time lost by the top pick.
-constexpr SplitKind N = SplitKind::kNone, P = SplitKind::kPartial, A = SplitKind::kAtomic;
+constexpr SplitKind N = SplitKind::kNone, P = SplitKind::kPartial;
 constexpr FTrainNumericType FP32 = FTRAIN_NUMERIC_TYPE_FP32, BF16 = FTRAIN_NUMERIC_TYPE_BF16,
                             FP16 = FTRAIN_NUMERIC_TYPE_FP16;
 constexpr VariantInfo kInfo[] = {
@@ -37,8 +37,8 @@ constexpr VariantInfo kInfo[] = {
     {"Fp32MfmaGemm_128x128_Unaligned", 128, 128, 16, 256, 2, false, N, false, false, true, 0.66, FP32, 256.0, 0.675},
     {"Fp32MfmaGemm_128x128_Unaligned_SplitK", 128, 128, 16, 256, 2, false, P, false, false, true, 0.55, FP32, 256.0, 0.4},
     {"Fp32MfmaGemm_64x64_Unaligned", 64, 64, 16, 256, 4, false, N, false, false, true, 0.585, FP32, 256.0, 0.45},
-    {"Fp32Gemv_SplitK", kGemvRows, kGemvCols, 1, 256, 8, true, A, true, false, false, 0, FP32, 256.0, 0},
-    {"Fp32Gemv_Unaligned_SplitK", kGemvRows, kGemvCols, 1, 256, 8, false, A, true, false, false, 0, FP32, 256.0, 0},
+    {"Fp32Gemv_SplitK", kGemvRows, kGemvCols, 1, 256, 8, true, P, true, false, false, 0, FP32, 256.0, 0},
+    {"Fp32Gemv_Unaligned_SplitK", kGemvRows, kGemvCols, 1, 256, 8, false, P, true, false, false, 0, FP32, 256.0, 0},
     {"Fp32Gemm", 64, 64, 16, 256, 2, false, N, false, true, true, 0.2, FP32, 256.0, 0.2},
     {"Bf16MfmaGemm_256x256", 256, 256, 64, 512, 1, true, N, false, false, true, 0.6, BF16, 4096.0, 0.6},
     {"Bf16MfmaGemm_128x128", 128, 128, 64, 256, 2, true, N, false, false, true, 0.5, BF16, 4096.0, 0.5},

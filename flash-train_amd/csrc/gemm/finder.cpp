@@ -15,12 +15,9 @@
 //            are available), plus a fixed cost per round of resident
 //            workgroups.
 //   memory : algorithmic bytes (a, b, d, optional c) at 80% of 8 TB/s, plus
-//            the partial tiles (written and read once) for split-k with a
-//            reduction, or the beta*c prologue pass for atomic split-k.
-//   atomics: atomic split-k adds m*n*splits fp32 atomics at a measured
-//            device-scope rate.
-//   time   = max(compute, memory, atomics) + launch latency (one more for
-//            split-k).
+//            the partial tiles (written and read once) for split-k.
+//   time   = max(compute, memory) + the reduction's pass over the partial
+//            tiles (split-k) + launch latency (one more for split-k).
 #include <algorithm>
 #include <atomic>
 #include <cmath>
@@ -38,7 +35,6 @@ namespace {
 constexpr double kClockPerMicro = 2.4e3;  // peak engine clock (MHz)
 constexpr double kHbmBytesPerMicro = 8.0e6 * 0.8;  // sustained HBM bytes per microsecond
 constexpr double kLaunchMicros = 4.0;
-constexpr double kAtomicsPerMicro = 6.0e4;
 constexpr double kPoolMicros      = 2.0;  // stream-ordered workspace acquire + release
 // Fixed cost per round of resident workgroups (operand prologue, epilogue
 // stores, the ramp of the first stages); fitted with the catalog efficiencies.
@@ -83,16 +79,8 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
     const double eb   = vi.input == FTRAIN_NUMERIC_TYPE_FP32 ? 4.0 : 2.0;
     double bytes      = eb * (m * k + k * n + m * n * (has_c ? 2.0 : 1.0));
     double launch     = kLaunchMicros;
-    double atomics_us = 0.0;
     double serial_us  = 0.0;  // work in a second kernel that cannot overlap the first
-    if (vi.split == SplitKind::kAtomic) {
-        bytes += 4.0 * m * n * (has_c ? 2.0 : 1.0);  // prologue pass
-        launch += kLaunchMicros;
-        // Device-scope fp32 atomics are resolved past the XCD-private L2s;
-        // measured on MI355X at roughly 6e4 per microsecond when many
-        // workgroups hit the same lines.
-        atomics_us = m * n * double(splits) / kAtomicsPerMicro;
-    } else if (vi.split == SplitKind::kPartial) {
+    if (vi.split == SplitKind::kPartial) {
         // The GEMM kernel writes splits partial tiles instead of d; the
         // reduction kernel then reads them (and c) and writes d.
         bytes += 4.0 * m * n * (double(splits) - 1.0 - (has_c ? 1.0 : 0.0));
@@ -102,7 +90,7 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
     if (vi.gemv) {
         const double wgs = double(ceilDiv(std::max<uint64_t>(s.n, 1), kGemvCols) * splits);
         const double fill = std::min(1.0, wgs / (double(cus) * 4.0));  // too few workgroups cannot reach HBM peak
-        return std::max(bytes / (kHbmBytesPerMicro * fill), atomics_us) + serial_us + launch;
+        return bytes / (kHbmBytesPerMicro * fill) + serial_us + launch;
     }
     // Work per workgroup includes the tile padding at the m/n edges.  The
     // dispatcher refills a CU as soon as one of its workgroups retires, so a
@@ -119,7 +107,7 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
     const double cu_rate   = vi.flop_per_clk * kClockPerMicro * residentEfficiency(vi, per_cu) * (vi.simt ? 0.5 : 1.0);
     const double rounds    = double(ceilDiv(per_cu, uint64_t(vi.occupancy)));
     const double compute   = double(per_cu) * 2.0 * vi.bm * vi.bn * depth / cu_rate + rounds * kRoundMicros;
-    return std::max({compute, bytes / kHbmBytesPerMicro, atomics_us}) + serial_us + launch;
+    return std::max(compute, bytes / kHbmBytesPerMicro) + serial_us + launch;
 }
 
 }  // namespace

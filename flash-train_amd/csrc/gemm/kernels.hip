@@ -9,8 +9,7 @@
 //   * the deterministic split-k reduction;
 //   * a streaming split-k kernel for skinny m (GEMV-like, HBM bound);
 //   * a general SIMT kernel with 64-bit indexing and arbitrary strides for
-//     shapes the others cannot take;
-//   * the elementwise prologue d = beta*c (or 0) used by the skinny kernel.
+//     shapes the others cannot take.
 #include "mfma_tile.hpp"
 
 namespace ftrain::gemm {
@@ -23,15 +22,14 @@ namespace {
 // Skinny-m streaming kernel (m <= 8).  Each workgroup covers 256 columns and
 // one k range; its 4 waves interleave over the k rows of that range, each
 // lane streaming 4 adjacent columns of b.  The waves' partial sums meet in
-// LDS; alpha*sum is then added atomically into d (initialised by the
-// prologue) or, with PARTIAL, stored raw to slice z of the workspace for
-// splitk_reduce.  Bound by the one pass over b.  b is row-major (row stride
-// ldb); a is row-major (TA false) or column-major (TA true) with leading
-// dimension lda; d is row-major with row stride ldd.
+// LDS and are stored raw to slice z of the workspace; splitk_reduce then
+// forms d in a fixed order (deterministic).  Bound by the one pass over b.
+// b is row-major (row stride ldb); a is row-major (TA false) or
+// column-major (TA true) with leading dimension lda.
 // ----------------------------------------------------------------------------
 
-template <bool VEC, bool PARTIAL, bool TA>
-__global__ __launch_bounds__(256) void gemv_splitk(GemmParams p) {
+template <bool VEC, bool TA>
+__device__ __forceinline__ void gemv_partial(const GemmParams& p, float* __restrict__ W) {
     const int tid  = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -89,26 +87,15 @@ __global__ __launch_bounds__(256) void gemv_splitk(GemmParams p) {
     if (col < N) {
         for (int i = 0; i < M; ++i) {
             const float s = part[0][i][tid] + part[1][i][tid] + part[2][i][tid] + part[3][i][tid];
-            if constexpr (PARTIAL)
-                p.d[(size_t)blockIdx.z * M * N + (size_t)i * N + col] = s;
-            else
-                unsafeAtomicAdd(p.d + (size_t)i * p.ldd + col, p.alpha * s);
+            W[(size_t)blockIdx.z * M * N + (size_t)i * N + col] = s;
         }
     }
 }
 
-// ----------------------------------------------------------------------------
-// d = c ? beta * c : 0 (grid-stride, 64-bit, row strides ldc / ldd).
-// Initialises the accumulation target of the skinny split-k kernel; safe in
-// place (c == d).
-// ----------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void prologue(WideParams p) {
-    const uint64_t total  = p.m * p.n;
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-        const uint64_t r = i / p.n, c = i - r * p.n;
-        p.d[r * p.ldd + c] = p.c != nullptr ? p.beta * p.c[r * p.ldc + c] : 0.f;
-    }
+// Partial slices only (p.d is the workspace); splitk_reduce forms d.
+template <bool VEC, bool TA>
+__global__ __launch_bounds__(256) void gemv_splitk(GemmParams p) {
+    gemv_partial<VEC, TA>(p, p.d);
 }
 
 // ----------------------------------------------------------------------------
@@ -273,8 +260,8 @@ const void* kernelFor(Variant v, bool ta, bool tb) {
     }
     if (ta || tb) {
         if (v == Variant::kSimt) return reinterpret_cast<const void*>(&simt_gemm);  // strides are runtime values
-        if (v == Variant::kGemvS && !tb && ta) return reinterpret_cast<const void*>(&gemv_splitk<true, false, true>);
-        if (v == Variant::kGemvUS && !tb && ta) return reinterpret_cast<const void*>(&gemv_splitk<false, false, true>);
+        if (v == Variant::kGemvS && !tb && ta) return reinterpret_cast<const void*>(&gemv_splitk<true, true>);
+        if (v == Variant::kGemvUS && !tb && ta) return reinterpret_cast<const void*>(&gemv_splitk<false, true>);
         if (!info(v).layouts) return nullptr;
         return ta ? (tb ? layoutKernelTT(v) : layoutKernelTN(v)) : layoutKernelNT(v);
     }
@@ -286,8 +273,8 @@ const void* kernelFor(Variant v, bool ta, bool tb) {
         case Variant::kMfma64x256S: return reinterpret_cast<const void*>(&mfma_gemm<64, 256, 16, 1, 4, 3, 1, true, kPartial, false, false>);
         case Variant::kMfma256x64: return reinterpret_cast<const void*>(&mfma_gemm<256, 64, 16, 4, 1, 3, 1, true, kWhole, false, false>);
         case Variant::kMfma256x64S: return reinterpret_cast<const void*>(&mfma_gemm<256, 64, 16, 4, 1, 3, 1, true, kPartial, false, false>);
-        case Variant::kGemvS: return reinterpret_cast<const void*>(&gemv_splitk<true, false, false>);
-        case Variant::kGemvUS: return reinterpret_cast<const void*>(&gemv_splitk<false, false, false>);
+        case Variant::kGemvS: return reinterpret_cast<const void*>(&gemv_splitk<true, false>);
+        case Variant::kGemvUS: return reinterpret_cast<const void*>(&gemv_splitk<false, false>);
         case Variant::kSimt: return reinterpret_cast<const void*>(&simt_gemm);
         default: return layoutKernel<false, false>(v);
     }
@@ -310,8 +297,6 @@ const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool t
     }
     return table[t][o](which);
 }
-
-const void* prologueKernel() { return reinterpret_cast<const void*>(&prologue); }
 
 const void* reduceKernel(bool vec) {
     return vec ? reinterpret_cast<const void*>(&splitk_reduce<true>) : reinterpret_cast<const void*>(&splitk_reduce<false>);

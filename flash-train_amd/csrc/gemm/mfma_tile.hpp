@@ -92,7 +92,7 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
     tn                   = within / band_rows;
 }
 
-enum SplitMode : int { kWhole = 0, kAtomic = 1, kPartial = 2 };
+enum SplitMode : int { kWhole = 0, kPartial = 2 };
 
 // ----------------------------------------------------------------------------
 // MFMA tile kernel.
@@ -104,11 +104,9 @@ enum SplitMode : int { kWhole = 0, kAtomic = 1, kPartial = 2 };
 //   extents that are multiples of 4, and n % 4 == 0).  SPLIT selects the
 //   epilogue:
 //     kWhole   - this workgroup owns the whole reduction: d = alpha*acc + beta*c;
-//     kAtomic  - it reduces [z*k_chunk, z*k_chunk + k_chunk) and atomically
-//                adds alpha*partial into d, which the prologue kernel set to
-//                beta*c (or 0);
-//     kPartial - same k range, but the raw partial tile is stored to slice z
-//                of the workspace p.d (z*m*n floats, dense m x n); splitk_reduce
+//     kPartial - it reduces [z*k_chunk, z*k_chunk + k_chunk) and stores the raw
+//                partial tile to slice z of the workspace p.d (z*m*n floats,
+//                dense m x n); splitk_reduce
 //                then forms d = alpha * sum_z(partial_z) + beta*c in fixed z
 //                order.
 //
@@ -409,11 +407,7 @@ __device__ __forceinline__ void mfma_gemm_tile(const GemmParams& p, int bid, int
             if (row >= M) continue;
             const size_t dbase = (size_t)row * ldd + col;
             const size_t cbase = (size_t)row * ldc + col;
-            if constexpr (SPLIT == kAtomic) {
-#pragma unroll
-                for (int bj = 0; bj < TN; ++bj)
-                    if (col + bj < N) unsafeAtomicAdd(D + dbase + bj, alpha * acc[bi][bj][r]);
-            } else if constexpr (SPLIT == kPartial) {
+            if constexpr (SPLIT == kPartial) {
                 float* W           = D + (size_t)z * M * N;
                 const size_t pbase = (size_t)row * N + col;
                 if constexpr (VEC && TN > 1) {

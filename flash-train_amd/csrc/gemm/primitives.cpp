@@ -93,6 +93,18 @@ void checkBlockSize(const void* kernel, int threads, const char* name) {
                         name, threads, attr.maxThreadsPerBlock);
 }
 
+// Largest split-k partial buffer a Primitive keeps for its Plan's lifetime.
+constexpr uint64_t kOwnedPartialBytes = 16ull << 20;
+
+bool capturing(hipStream_t stream) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &status) != hipSuccess) {
+        (void)hipGetLastError();
+        return true;  // unknown: take the pool, which is stream-ordered
+    }
+    return status != hipStreamCaptureStatusNone;
+}
+
 void check(hipError_t e, const char* what) {
     if (e != hipSuccess)
         throw Exception(FTRAIN_STATUS_INTERNAL_ERROR, "%s launch failed: %s", what, hipGetErrorString(e));
@@ -155,6 +167,7 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
     }
 
     void configure(const GemmProblem& p) override {
+        owned_.reset();
         empty_ = p.emptyOutput();
         if (empty_) return;
         GemmLaunch g;
@@ -203,8 +216,6 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
             grid_           = dim3(uint32_t(params_.tiles_m) * uint32_t(params_.tiles_n), 1, splits);
         }
         const uint64_t count = s.m * s.n;
-        if (info_->split == SplitKind::kAtomic)
-            aux_grid_ = dim3(static_cast<uint32_t>(std::min<uint64_t>(ceilDiv(count, 256), 16384)));
         if (info_->split == SplitKind::kPartial) {
             partial_bytes_ = uint64_t(splits) * count * sizeof(float);
             const int32_t cd_type = !cd_half ? gemm::kCdFp32
@@ -234,18 +245,35 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
             case SplitKind::kNone:
                 check(hipLaunchKernel(kernel_, grid_, block_, args, 0, r.stream), info_->name);
                 break;
-            case SplitKind::kAtomic: {
-                void* pro[] = {&wide_};
-                check(hipLaunchKernel(gemm::prologueKernel(), aux_grid_, dim3(256), pro, 0, r.stream), "GEMM prologue");
-                check(hipLaunchKernel(kernel_, grid_, block_, args, 0, r.stream), info_->name);
-                break;
-            }
             case SplitKind::kPartial: {
                 // Partial tiles go to the caller's workspace when it is large
-                // and aligned enough, else to a stream-ordered pool buffer.
+                // and aligned enough; else, up to kOwnedPartialBytes, to a
+                // buffer this Primitive allocates on its first execution and
+                // keeps for the Plan's lifetime (executions of one Plan are
+                // externally serialised, reference common.h:576); else to a
+                // stream-ordered pool buffer.  A first execution under stream
+                // capture cannot allocate and uses the pool.
                 const bool caller = r.workspace != nullptr && r.workspace_bytes >= partial_bytes_ &&
                                     reinterpret_cast<uintptr_t>(r.workspace) % 16 == 0;
-                void* ws           = caller ? r.workspace : acquireWorkspace(partial_bytes_, r.stream);
+                bool pooled       = false;
+                void* ws          = nullptr;
+                if (caller) {
+                    ws = r.workspace;
+                } else if (partial_bytes_ <= kOwnedPartialBytes && (owned_ || !capturing(r.stream))) {
+                    if (!owned_) {
+                        void* q = nullptr;
+                        if (hipMalloc(&q, partial_bytes_) != hipSuccess) {
+                            (void)hipGetLastError();
+                            throw Exception(FTRAIN_STATUS_OUT_OF_MEMORY, "%s: split-k buffer of %llu bytes",
+                                            info_->name, static_cast<unsigned long long>(partial_bytes_));
+                        }
+                        owned_.reset(q, [](void* x) { (void)hipFree(x); });
+                    }
+                    ws = owned_.get();
+                } else {
+                    ws     = acquireWorkspace(partial_bytes_, r.stream);
+                    pooled = true;
+                }
                 params.d           = static_cast<float*>(ws);
                 half_params.d      = ws;
                 ReduceParams red   = reduce_;
@@ -254,7 +282,7 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
                 hipError_t e       = hipLaunchKernel(kernel_, grid_, block_, args, 0, r.stream);
                 if (e == hipSuccess)
                     e = hipLaunchKernel(gemm::reduceKernel(reduce_vec_), aux_grid_, dim3(256), rargs, 0, r.stream);
-                if (!caller) releaseWorkspace(ws, r.stream);
+                if (pooled) releaseWorkspace(ws, r.stream);
                 check(e, info_->name);
                 break;
             }
@@ -285,6 +313,7 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
     ReduceParams reduce_{};
     bool reduce_vec_        = false;
     uint64_t partial_bytes_ = 0;
+    std::shared_ptr<void> owned_;  // split-k partials of this Plan (small buffers only)
 };
 
 }  // namespace

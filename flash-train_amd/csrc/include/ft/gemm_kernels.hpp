@@ -36,8 +36,7 @@ struct GemmParams {
     int64_t lda, ldb, ldc, ldd;
 };
 
-// 64-bit parameters for the general SIMT kernel, the skinny kernel's
-// operand reads and the elementwise prologue.  Element (i, j) of a sits at
+// 64-bit parameters for the general SIMT kernel.  Element (i, j) of a sits at
 // a[i*a_rs + j*a_cs], likewise b; c and d are row-major with row strides ldc
 // and ldd.
 struct WideParams {
@@ -163,8 +162,7 @@ constexpr int kHalfTiles = 4;
 
 enum class SplitKind : int {
     kNone,     // one workgroup owns each output tile's whole reduction
-    kPartial,  // partial tiles to a workspace, then splitk_reduce
-    kAtomic,   // beta*c prologue, then fp32 atomic adds
+    kPartial,  // partial tiles to a workspace, then splitk_reduce (fixed order)
 };
 
 struct VariantInfo {
@@ -236,7 +234,6 @@ const void* groupedHalfKernelFp16NN(int which);
 const void* groupedHalfKernelFp16TN(int which);
 const void* groupedHalfKernelFp16NT(int which);
 const void* groupedHalfKernelFp16TT(int which);
-const void* prologueKernel();            // d = c ? beta*c : 0 over m*n elements (WideParams)
 const void* reduceKernel(bool vec);      // split-k reduction (ReduceParams)
 
 }  // namespace ftrain::gemm

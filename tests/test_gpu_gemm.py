@@ -377,3 +377,29 @@ def test_split_k_is_deterministic(capi, ops):
             torch.cuda.synchronize()
             outs.append(d.clone())
         assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2]), plan.name(i)
+
+
+def test_skinny_gemv_is_deterministic(capi, ops, oracle):
+    # The m <= 8 streaming Primitives also reduce their k splits in a fixed
+    # order (partial slices, then the split-k reduction): repeated runs agree
+    # bit for bit and match fp64 to the usual bar.
+    m, n, k = 4, 4096, 8192
+    g = torch.Generator().manual_seed(11)
+    a, b, c = (torch.randn(m, k, generator=g).cuda(), torch.randn(k, n, generator=g).cuda(),
+               torch.randn(m, n, generator=g).cuda())
+    d = torch.empty(m, n, device="cuda")
+    plan = capi.plan_for(a, b, c, d, 1.5, -0.5, ops)
+    gemv = [i for i, nm in enumerate(plan.names()) if nm.startswith("Fp32Gemv")]
+    assert gemv and plan.name(0).startswith("Fp32Gemv"), plan.names()
+    ref = oracle.gemm_f64(a.cpu().numpy(), b.cpu().numpy(), c.cpu().numpy(), 1.5, -0.5)
+    s = torch.cuda.current_stream().cuda_stream
+    for i in gemv:
+        outs = []
+        for _ in range(3):
+            d.fill_(float("nan"))
+            plan.execute(i, s)
+            torch.cuda.synchronize()
+            outs.append(d.clone())
+        assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2]), plan.name(i)
+        rep = oracle.tolerance_check(outs[0].cpu().numpy(), ref, k)
+        assert rep["ok"], (plan.name(i), rep)
