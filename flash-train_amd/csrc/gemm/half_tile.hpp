@@ -122,7 +122,7 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 // ----------------------------------------------------------------------------
 // The tile body (see mfma_tile.hpp): tile `bid` of p's grid, split `z`.
 template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, int SPLIT, bool TA, bool TB,
-          int DEPTH = 1, bool ALLSPREAD = false>
+          bool ALLSPREAD = false>
 __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid, int z) {
     using u16           = unsigned short;
     constexpr int NT    = WM * WN * 64;
@@ -171,10 +171,8 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
     constexpr int A_REGS = VEC && TA ? 8 : 1;   // vectors per staging slot
     constexpr int B_REGS = VEC && !TB ? 8 : 1;
     static_assert(VEC || (BM * BK % NT == 0 && BN * BK % NT == 0), "scalar staging");
-    // DEPTH sets of staging registers (the spread pipeline keeps DEPTH stages
-    // of global data in flight; the other schedules use set 0 only).
-    u32x4 ra[DEPTH][VEC ? A_PER : 1][A_REGS];
-    u32x4 rb[DEPTH][VEC ? B_PER : 1][B_REGS];
+    u32x4 ra[VEC ? A_PER : 1][A_REGS];
+    u32x4 rb[VEC ? B_PER : 1][B_REGS];
     u16 sa[VEC ? 1 : A_PER];
     u16 sb[VEC ? 1 : B_PER];
 
@@ -194,7 +192,7 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
         // Global loads of one stage (k range [k0, k0 + BK)) into registers.
         // Entries: A staging slots 0 .. A_PER-1, then B slots; [first, last)
         // selects a part (the whole stage by default).
-        auto load_stage = [&](int set, int k0, int first = 0, int last = 1 << 20) {
+        auto load_stage = [&](int k0, int first = 0, int last = 1 << 20) {
             if constexpr (VEC) {
 #pragma unroll
                 for (int j = 0; j < A_PER; ++j) {
@@ -204,8 +202,8 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                     if constexpr (!TA) {  // (r, 8 k) vectors, 8 threads per row of BK = 64
                         const int r = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
                         const int gm = m0 + r, gk = k0 + kq;
-                        ra[set][j][0] = zero4;
-                        if (!CHECKED || (gm < M && gk < kend)) ra[set][j][0] = *reinterpret_cast<const u32x4*>(a_at(gm, gk));
+                        ra[j][0] = zero4;
+                        if (!CHECKED || (gm < M && gk < kend)) ra[j][0] = *reinterpret_cast<const u32x4*>(a_at(gm, gk));
                     } else {
                         // 8 x 8 blocks: 8 consecutive m at k = kb..kb+7.  Consecutive
                         // threads take consecutive k blocks of the same 8 rows, so
@@ -218,9 +216,9 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
 #pragma unroll
                         for (int i = 0; i < 8; ++i) {
                             const int gk = k0 + kb + i;
-                            ra[set][j][i]     = zero4;
+                            ra[j][i]     = zero4;
                             if (!CHECKED || (gm < M && gk < kend))
-                                ra[set][j][i] = *reinterpret_cast<const u32x4*>(a_at(gm, gk));
+                                ra[j][i] = *reinterpret_cast<const u32x4*>(a_at(gm, gk));
                         }
                     }
                 }
@@ -232,17 +230,17 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                     if constexpr (TB) {  // (c, 8 k) vectors
                         const int c = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
                         const int gn = n0 + c, gk = k0 + kq;
-                        rb[set][j][0] = zero4;
-                        if (!CHECKED || (gn < N && gk < kend)) rb[set][j][0] = *reinterpret_cast<const u32x4*>(b_at(gk, gn));
+                        rb[j][0] = zero4;
+                        if (!CHECKED || (gn < N && gk < kend)) rb[j][0] = *reinterpret_cast<const u32x4*>(b_at(gk, gn));
                     } else {  // 8 x 8 blocks: 8 consecutive n at k = kb..kb+7 (thread order as for a)
                         const int kb = 8 * (idx % (BK / 8)), c = 8 * (idx / (BK / 8));
                         const int gn = n0 + c;
 #pragma unroll
                         for (int i = 0; i < 8; ++i) {
                             const int gk = k0 + kb + i;
-                            rb[set][j][i]     = zero4;
+                            rb[j][i]     = zero4;
                             if (!CHECKED || (gn < N && gk < kend))
-                                rb[set][j][i] = *reinterpret_cast<const u32x4*>(b_at(gk, gn));
+                                rb[j][i] = *reinterpret_cast<const u32x4*>(b_at(gk, gn));
                         }
                     }
                 }
@@ -265,7 +263,7 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
         };
 
         // Registers -> LDS buffer `buf` (k-contiguous rows).
-        auto store_stage = [&](int set, int buf, int first = 0, int last = 1 << 20) {
+        auto store_stage = [&](int buf, int first = 0, int last = 1 << 20) {
             if constexpr (VEC) {
 #pragma unroll
                 for (int j = 0; j < A_PER; ++j) {
@@ -274,11 +272,11 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                     if (A_VECS % NT != 0 && idx >= A_VECS) continue;
                     if constexpr (!TA) {
                         const int r = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
-                        *reinterpret_cast<u32x4*>(&As[buf][r * SK + kq]) = ra[set][j][0];
+                        *reinterpret_cast<u32x4*>(&As[buf][r * SK + kq]) = ra[j][0];
                     } else {
                         const int kb = 8 * (idx % (BK / 8)), r = 8 * (idx / (BK / 8));
                         u32x4 w[8];
-                        transpose8x8(ra[set][j], w);
+                        transpose8x8(ra[j], w);
 #pragma unroll
                         for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(&As[buf][(r + i) * SK + kb]) = w[i];
                     }
@@ -290,11 +288,11 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                     if (B_VECS % NT != 0 && idx >= B_VECS) continue;
                     if constexpr (TB) {
                         const int c = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
-                        *reinterpret_cast<u32x4*>(&Bs[buf][c * SK + kq]) = rb[set][j][0];
+                        *reinterpret_cast<u32x4*>(&Bs[buf][c * SK + kq]) = rb[j][0];
                     } else {
                         const int kb = 8 * (idx % (BK / 8)), c = 8 * (idx / (BK / 8));
                         u32x4 w[8];
-                        transpose8x8(rb[set][j], w);
+                        transpose8x8(rb[j], w);
 #pragma unroll
                         for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(&Bs[buf][(c + i) * SK + kb]) = w[i];
                     }
@@ -337,19 +335,19 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
         if constexpr (!VEC) {
             // Per-element path: straightforward two-stage loop.
             if (nst > 0) {
-                load_stage(0, kbeg);
-                store_stage(0, 0);
+                load_stage(kbeg);
+                store_stage(0);
             }
             __syncthreads();
             for (int st = 0; st < nst; ++st) {
-                if (st + 1 < nst) load_stage(0, kbeg + (st + 1) * BK);
+                if (st + 1 < nst) load_stage(kbeg + (st + 1) * BK);
 #pragma unroll
                 for (int s = 0; s < STEPS; ++s) {
                     u32x4 av[TM], bv[TN];
                     read_ops(st & 1, s, av, bv);
                     mfmas(av, bv, 0, TM * TN);
                 }
-                if (st + 1 < nst) store_stage(0, (st + 1) & 1);
+                if (st + 1 < nst) store_stage((st + 1) & 1);
                 __syncthreads();
             }
         } else {
@@ -362,12 +360,11 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
             constexpr bool SPREAD = (!TA && TB) || ALLSPREAD;
             if constexpr (SPREAD) {
                 // Software pipeline.  Stage st computes from LDS buffer st&1
-                // while DEPTH register sets hold the global data of stages
-                // st+1 .. st+DEPTH (set st % DEPTH holds stage st+1).  The
+                // while registers hold the global data of stage st+1.  The
                 // staging entries (A slots, then B slots) are split into STEPS
                 // parts; during k-step s, part s of stage st+1 is written to the
-                // other LDS buffer and part s of stage st+1+DEPTH is loaded into
-                // the registers it frees, interleaved with that step's MFMAs and the
+                // other LDS buffer and part s of stage st+2 is loaded into the
+                // registers it frees, interleaved with that step's MFMAs and the
                 // operand reads of step s+1 (the other buffer is free from the
                 // barrier of stage st-1 on: every read of it precedes that
                 // barrier).  In the last step the barrier (stage st+1 complete
@@ -389,23 +386,20 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                 u32x4 opa[2][TM], opb[2][TN];
                 auto clamp_k0 = [&](int stage) { return kbeg + min(stage, nst - 1) * BK; };
                 if (nst > 0) {
-                    load_stage(0, kbeg);
-                    store_stage(0, 0);
-#pragma unroll
-                    for (int d = 0; d < DEPTH; ++d) load_stage(d, clamp_k0(1 + d));
+                    load_stage(kbeg);
+                    store_stage(0);
+                    load_stage(clamp_k0(1));
                 }
                 __syncthreads();
                 if (nst > 0) read_ops(0, 0, opa[0], opb[0]);
-                // Register set st % DEPTH holds stage st+1 at the start of stage st.
-                auto stage_body = [&](int st, auto set_c) {
-                    constexpr int set = decltype(set_c)::value;
+                for (int st = 0; st < nst; ++st) {
                     const int cur = st & 1;
     #pragma unroll
                     for (int s = 0; s < STEPS; ++s) {
                         const int e0 = s * PART, e1 = min(ENT, (s + 1) * PART);
                         if (s + 1 < STEPS) read_ops(cur, s + 1, opa[(s + 1) & 1], opb[(s + 1) & 1]);
-                        store_stage(set, cur ^ 1, e0, e1);
-                        load_stage(set, clamp_k0(st + 1 + DEPTH), e0, e1);
+                        store_stage(cur ^ 1, e0, e1);
+                        load_stage(clamp_k0(st + 2), e0, e1);
                         if (s + 1 < STEPS) {
                             mfmas(opa[s & 1], opb[s & 1], 0, NB);
     #pragma unroll
@@ -432,14 +426,6 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                             __builtin_amdgcn_sched_barrier(0);
                         }
                     }
-                };
-                if constexpr (DEPTH == 1) {
-                    for (int st = 0; st < nst; ++st) stage_body(st, std::integral_constant<int, 0>{});
-                } else {
-                    for (int st = 0; st < nst; st += 2) {
-                        stage_body(st, std::integral_constant<int, 0>{});
-                        if (st + 1 < nst) stage_body(st + 1, std::integral_constant<int, 1>{});
-                    }
                 }
             } else {
                 // Software pipeline.  Stage st computes from LDS buffer st&1
@@ -461,9 +447,9 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                 u32x4 opa[2][TM], opb[2][TN];
                 auto clamp_k0 = [&](int stage) { return kbeg + min(stage, nst - 1) * BK; };
                 if (nst > 0) {
-                    load_stage(0, kbeg);
-                    store_stage(0, 0);
-                    load_stage(0, clamp_k0(1));
+                    load_stage(kbeg);
+                    store_stage(0);
+                    load_stage(clamp_k0(1));
                 }
                 __syncthreads();
                 if (nst > 0) read_ops(0, 0, opa[0], opb[0]);
@@ -480,8 +466,8 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                         __builtin_amdgcn_sched_barrier(0);
                     }
                     constexpr int L = (STEPS - 1) & 1;
-                    store_stage(0, cur ^ 1);
-                    load_stage(0, clamp_k0(st + 2));
+                    store_stage(cur ^ 1);
+                    load_stage(clamp_k0(st + 2));
                     mfmas(opa[L], opb[L], 0, NB - TAIL);
                     // Spread the LDS writes and global loads over these MFMAs.
                     constexpr int WR = (VEC ? (TA ? 8 * A_PER : A_PER) + (TB ? B_PER : 8 * B_PER) : 0);
@@ -540,9 +526,9 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
 }
 
 template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, int SPLIT, bool TA, bool TB,
-          int DEPTH = 1, bool ALLSPREAD = false>
+          bool ALLSPREAD = false>
 __global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p) {
-    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, SPLIT, TA, TB, DEPTH, ALLSPREAD>(p, blockIdx.x, blockIdx.z);
+    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, SPLIT, TA, TB, ALLSPREAD>(p, blockIdx.x, blockIdx.z);
 }
 
 // Grouped GEMM over a device table of per-group parameters (see
@@ -559,7 +545,7 @@ __device__ __forceinline__ int find_group(const int32_t* __restrict__ start, int
     return lo;
 }
 
-template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, bool TA, bool TB, int DEPTH = 1,
+template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, bool TA, bool TB,
           bool ALLSPREAD = false>
 __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_half_gemm(GroupedHalfArgs g) {
     const int bid = blockIdx.x;
@@ -569,7 +555,7 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_half_gemm(GroupedHa
     // hardware id's XCD (id mod 8); ids past the group's tiles are padding.
     const int local = bid - g.tile_start[grp];
     if (local >= p.tiles_m * p.tiles_n) return;
-    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, kWhole, TA, TB, DEPTH, ALLSPREAD>(p, local, 0);
+    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, kWhole, TA, TB, ALLSPREAD>(p, local, 0);
 }
 
 // The 256x256 tile per operand orientation.  Row-major a: 8 waves of 128x64,
@@ -579,12 +565,11 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_half_gemm(GroupedHa
 // (TFLOP/s, 4 waves against 8): column-major a with row-major b 965 / 783 at
 // 8192^3, 834 / 740 at MLP fwd, 758 / 648 at 4096^3; both column-major 1095 /
 // 1008, 943 / 939, 863 / 818.  Row-major a with row-major b gains at 8192^3
-// with 4 waves and DEPTH 2 (1077 / 1028) but loses at MLP fwd (924 / 944)
-// and 4096^3 (833 / 858), so it keeps 8 waves.
+// with 4 waves and a second staging register set (1077 / 1028) but loses at
+// MLP fwd (924 / 944) and 4096^3 (833 / 858), so it keeps 8 waves.
 template <bool TA, bool TB>
 struct Wide {
     static constexpr int WN      = TA ? 2 : 4;
-    static constexpr int DEPTH   = 1;
     static constexpr bool SPREAD = TA;
 };
 
@@ -596,7 +581,7 @@ const void* halfKernel(int tile) {
         case 0: {
             using W = Wide<TA, TB>;
             return reinterpret_cast<const void*>(
-                &half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, kWhole, TA, TB, W::DEPTH, W::SPREAD>);
+                &half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, kWhole, TA, TB, W::SPREAD>);
         }
         case 1: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kWhole, TA, TB>);
         case 2: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kPartial, TA, TB>);
@@ -615,7 +600,7 @@ const void* groupedHalfKernel(int which) {
         case 2: {
             using W = Wide<TA, TB>;
             return reinterpret_cast<const void*>(
-                &grouped_half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, TA, TB, W::DEPTH, W::SPREAD>);
+                &grouped_half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, TA, TB, W::SPREAD>);
         }
         default: return nullptr;
     }
