@@ -97,10 +97,14 @@ class ConveniencePlans {
     }
 
     static std::vector<uint64_t> describe(const FTrainStorageView* const views[6], FTrainNumericType compute_type,
-                                          int device) {
+                                          int device, FTrainStream stream) {
         std::vector<uint64_t> k;
         k.reserve(48);
         k.push_back(uint64_t(uint32_t(device)));
+        // A split-k Plan keeps its partial tiles in a buffer of its own, so
+        // calls on different streams, which may overlap on the device, get
+        // Plans of their own.
+        k.push_back(reinterpret_cast<uintptr_t>(stream));
         k.push_back(compute_type);
         for (int i = 0; i < 6; ++i) {
             const FTrainStorageView& v = *views[i];
@@ -398,7 +402,7 @@ FTrainStatus ftrainGemm(FTrainStorageView a, FTrainStorageView b, FTrainStorageV
     int device                        = -1;
     std::vector<uint64_t> key;
     if (cacheable && hipGetDevice(&device) == hipSuccess) {
-        key = ConveniencePlans::describe(views, compute_type, device);
+        key = ConveniencePlans::describe(views, compute_type, device, stream);
         if (FTrainPlan cached = ConveniencePlans::local().find(key))
             return ftrainPlanExecutePrimitive(cached, 0, workspace, workspace_bytes, stream);
     } else {
