@@ -497,32 +497,85 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
 
     // Epilogue: lane li owns column wcol + bj*32 + li of each block; c and d
     // are row-major (row strides ldc, ldd) in fp32 or the input type.
-    const float alpha = p.alpha, beta = p.beta;
+    if constexpr (SPLIT == kPartial) {
 #pragma unroll
-    for (int bi = 0; bi < TM; ++bi)
+        for (int bi = 0; bi < TM; ++bi)
 #pragma unroll
-        for (int bj = 0; bj < TN; ++bj) {
-            const int col = n0 + wcol + bj * 32 + li;
-            if (col >= N) continue;
+            for (int bj = 0; bj < TN; ++bj) {
+                const int col = n0 + wcol + bj * 32 + li;
+                if (col >= N) continue;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wrow + bi * 32 + 8 * (r / 4) + 4 * h + (r % 4);
-                if (row >= M) continue;
-                if constexpr (SPLIT == kPartial) {
-                    static_cast<float*>(p.d)[(size_t)z * M * N + (size_t)row * N + col] = acc[bi][bj][r];
-                } else {
-                    const size_t ci = (size_t)row * p.ldc + col, di = (size_t)row * p.ldd + col;
-                    float cv = 0.f;
-                    if (p.c != nullptr)
-                        cv = p.cd_half ? to_float<BF16>(static_cast<const u16*>(p.c)[ci]) : static_cast<const float*>(p.c)[ci];
-                    const float out = alpha * acc[bi][bj][r] + (p.c != nullptr ? beta * cv : 0.f);
-                    if (p.cd_half)
-                        static_cast<u16*>(p.d)[di] = from_float<BF16>(out);
-                    else
-                        static_cast<float*>(p.d)[di] = out;
+                for (int r = 0; r < 16; ++r) {
+                    const int row = m0 + wrow + bi * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+                    if (row < M) static_cast<float*>(p.d)[(size_t)z * M * N + (size_t)row * N + col] = acc[bi][bj][r];
                 }
             }
+    } else {
+        // c is read one unit of UB blocks ahead of the stores, so its loads
+        // are in flight while the previous unit is written.
+        const float alpha = p.alpha, beta = p.beta;
+        constexpr int UB = TN > 1 ? TN / 2 : 1;  // blocks per unit
+        constexpr int UNITS = TM * TN / UB;
+        auto run = [&](auto c_tag, auto half_tag) {
+            constexpr bool HAS_C = decltype(c_tag)::value;
+            constexpr bool HALF  = decltype(half_tag)::value;
+            float cv[HAS_C ? 2 : 1][UB][16];
+            auto load_c = [&](int u, float (&dst)[UB][16]) {
+                const int bi = u / (TN / UB), bj0 = (u % (TN / UB)) * UB;
+#pragma unroll
+                for (int t = 0; t < UB; ++t) {
+                    const int col = n0 + wcol + (bj0 + t) * 32 + li;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row     = m0 + wrow + bi * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+                        const size_t ci   = (size_t)row * p.ldc + col;
+                        const bool inside = col < N && row < M;
+                        if constexpr (HALF)
+                            dst[t][r] = inside ? to_float<BF16>(static_cast<const u16*>(p.c)[ci]) : 0.f;
+                        else
+                            dst[t][r] = inside ? static_cast<const float*>(p.c)[ci] : 0.f;
+                    }
+                }
+            };
+            if constexpr (HAS_C) load_c(0, cv[0]);
+#pragma unroll
+            for (int u = 0; u < UNITS; ++u) {
+                if constexpr (HAS_C)
+                    if (u + 1 < UNITS) load_c(u + 1, cv[(u + 1) & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+                const int bi = u / (TN / UB), bj0 = (u % (TN / UB)) * UB;
+#pragma unroll
+                for (int t = 0; t < UB; ++t) {
+                    const int col = n0 + wcol + (bj0 + t) * 32 + li;
+                    if (col >= N) continue;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = m0 + wrow + bi * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+                        if (row >= M) continue;
+                        const size_t di = (size_t)row * p.ldd + col;
+                        float out       = alpha * acc[bi][bj0 + t][r];
+                        if constexpr (HAS_C) out += beta * cv[HAS_C ? u & 1 : 0][t][r];
+                        if constexpr (HALF)
+                            static_cast<u16*>(p.d)[di] = from_float<BF16>(out);
+                        else
+                            static_cast<float*>(p.d)[di] = out;
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        if (p.c != nullptr) {
+            if (p.cd_half)
+                run(std::true_type{}, std::true_type{});
+            else
+                run(std::true_type{}, std::false_type{});
+        } else {
+            if (p.cd_half)
+                run(std::false_type{}, std::true_type{});
+            else
+                run(std::false_type{}, std::false_type{});
         }
+    }
 }
 
 template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, int SPLIT, bool TA, bool TB,
