@@ -340,33 +340,71 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
     float* __restrict__ D       = p.d;
     const size_t ldc = p.ldc, ldd = p.ldd;
     const int col = n0 + wcol + 4 * j16;
+    if constexpr (SPLIT == kPartial) {
 #pragma unroll
-    for (int bi = 0; bi < TM; ++bi) {
-        // One row block at a time: keeps the scheduler from hoisting every
-        // c load of the tile into registers at once.
-        __builtin_amdgcn_sched_barrier(0);
+        for (int bi = 0; bi < TM; ++bi) {
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int row = m0 + wrow + bi * 16 + 4 * g + r;
-            if (row >= M) continue;
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + wrow + bi * 16 + 4 * g + r;
+                if (row >= M) continue;
 #pragma unroll
-            for (int q = 0; q < TN / 4; ++q) {
-                if (col + 64 * q >= N) continue;  // n % 4 == 0: a run of 4 columns is all in or all out
-                floatx4 out;
-                if constexpr (SPLIT == kPartial) {
+                for (int q = 0; q < TN / 4; ++q) {
+                    if (col + 64 * q >= N) continue;  // n % 4 == 0: a run of 4 columns is all in or all out
+                    floatx4 out;
 #pragma unroll
                     for (int t = 0; t < 4; ++t) out[t] = acc[bi][4 * q + t][r];
                     *reinterpret_cast<floatx4*>(D + (size_t)z * M * N + (size_t)row * N + col + 64 * q) = out;
-                } else {
-                    floatx4 cv = floatx4{0.f, 0.f, 0.f, 0.f};
-                    if (C != nullptr) cv = *reinterpret_cast<const floatx4*>(C + (size_t)row * ldc + col + 64 * q);
-#pragma unroll
-                    for (int t = 0; t < 4; ++t)
-                        out[t] = alpha * acc[bi][4 * q + t][r] + (C != nullptr ? beta * cv[t] : 0.f);
-                    *reinterpret_cast<floatx4*>(D + (size_t)row * ldd + col + 64 * q) = out;
                 }
             }
         }
+    } else {
+        // One row block at a time, the c values of row block bi + 1 loaded
+        // while row block bi is written (the barriers keep the scheduler
+        // from hoisting every c load of the tile into registers at once).
+        auto run = [&](auto c_tag) {
+            constexpr bool HAS_C = decltype(c_tag)::value;
+            floatx4 cv[HAS_C ? 2 : 1][4][TN / 4];
+            auto load_c = [&](int bi, floatx4 (&dst)[4][TN / 4]) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = m0 + wrow + bi * 16 + 4 * g + r;
+#pragma unroll
+                    for (int q = 0; q < TN / 4; ++q)
+                        dst[r][q] = row < M && col + 64 * q < N
+                                        ? *reinterpret_cast<const floatx4*>(C + (size_t)row * ldc + col + 64 * q)
+                                        : floatx4{0.f, 0.f, 0.f, 0.f};
+                }
+            };
+            if constexpr (HAS_C) load_c(0, cv[0]);
+#pragma unroll
+            for (int bi = 0; bi < TM; ++bi) {
+                if constexpr (HAS_C)
+                    if (bi + 1 < TM) load_c(bi + 1, cv[(bi + 1) & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = m0 + wrow + bi * 16 + 4 * g + r;
+                    if (row >= M) continue;
+#pragma unroll
+                    for (int q = 0; q < TN / 4; ++q) {
+                        if (col + 64 * q >= N) continue;  // n % 4 == 0: a run of 4 columns is all in or all out
+                        floatx4 out;
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            out[t] = alpha * acc[bi][4 * q + t][r];
+                            if constexpr (HAS_C) out[t] += beta * cv[HAS_C ? bi & 1 : 0][r][q][t];
+                        }
+                        *reinterpret_cast<floatx4*>(D + (size_t)row * ldd + col + 64 * q) = out;
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        if (C != nullptr)
+            run(std::true_type{});
+        else
+            run(std::false_type{});
     }
 }
 
