@@ -55,9 +55,4 @@ static_assert(sizeof(kInfo) / sizeof(kInfo[0]) == static_cast<int>(Variant::kCou
 
 const VariantInfo& info(Variant v) { return kInfo[static_cast<int>(v)]; }
 
-int blockThreads(Variant v, bool ta, bool tb) {
-    if ((v == Variant::kBf16Mfma256x256 || v == Variant::kFp16Mfma256x256) && ta) return 256;
-    return info(v).threads;
-}
-
 }  // namespace ftrain::gemm

@@ -396,7 +396,7 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
         for (int o = 0; o < 4; ++o)
             if (buckets_[o].tiles > 0) {
                 buckets_[o].kernel  = gemm::groupedKernelFor(v_->input, v_->which, o & 1, o & 2);
-                buckets_[o].threads = gemm::blockThreads(v_->tile, o & 1, o & 2);
+                buckets_[o].threads = gemm::info(v_->tile).threads;
             }
         table_.reset();
     }

@@ -20,18 +20,19 @@
 // k = h*BK/2 + 8*s + (0..7): the pairing only has to agree between A and B,
 // and this choice makes each lane's operand one 16-byte LDS read.
 //
-// LDS: both tiles are stored k-contiguous, [BM][BK + 8] for A and
-// [BN][BK + 8] for B.  The 8-element pad makes the row stride 36 dwords, so
-// the 16 lanes of one 128-bit read pass (consecutive rows) hit 16 disjoint
-// 4-bank groups.
+// LDS: a k-contiguous operand is stored as [rows][BK + 8]; the 8-element pad
+// makes the row stride 36 dwords, so the 16 lanes of one 128-bit read pass
+// (consecutive rows) hit 16 disjoint 4-bank groups.
 //
 // Global -> LDS, per operand orientation:
 //   k-contiguous in memory (row-major a, column-major b): 16-byte loads of 8
 //     consecutive k, written to LDS as they are;
-//   row/column-contiguous (column-major a, row-major b): each thread loads an
-//     8 x 8 block as 8 rows of 8 consecutive m (or n) at consecutive k,
-//     transposes it in registers with 16-bit shuffles (v_perm_b32), and writes
-//     8 k-contiguous vectors.
+//   row/column-contiguous (column-major a, row-major b), TR tiles: 16-byte
+//     loads of 8 consecutive m (or n) at one k, written as they are into a
+//     k-major tile, whose operands are then read with ds_read_b64_tr_b16;
+//   the same, other tiles: each thread loads an 8 x 8 block as 8 rows of 8
+//     consecutive m (or n) at consecutive k, transposes it in registers with
+//     16-bit shuffles (v_perm_b32), and writes 8 k-contiguous vectors.
 // Consecutive threads walk each matrix's contiguous dimension, so the loads
 // stay coalesced for every orientation.
 #pragma once
@@ -122,7 +123,7 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 // ----------------------------------------------------------------------------
 // The tile body (see mfma_tile.hpp): tile `bid` of p's grid, split `z`.
 template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, int SPLIT, bool TA, bool TB,
-          bool ALLSPREAD = false>
+          bool ALLSPREAD = false, bool TR = false>
 __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid, int z) {
     using u16           = unsigned short;
     constexpr int NT    = WM * WN * 64;
@@ -133,9 +134,21 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
     constexpr int STEPS = BK / 16;  // MFMA k-steps per stage
     constexpr int SK    = BK + 8;   // LDS row stride (elements)
     static_assert(TM >= 1 && TN >= 1 && BK % 16 == 0, "tile");
+    // TR: a transposed operand (column-major a, row-major b) is stored as it
+    // lies in memory, k-major ([BK][BM + 32] / [BK][BN + 32]), and read with
+    // transposing LDS reads; otherwise it is transposed in registers.
+    constexpr bool A_TR = TR && VEC && TA;
+    constexpr bool B_TR = TR && VEC && !TB;
+    constexpr int A_LDS = A_TR ? BK * (BM + 32) + 128 : BM * SK;
+    constexpr int B_LDS = B_TR ? BK * (BN + 32) + 128 : BN * SK;
 
-    __shared__ __attribute__((aligned(16))) u16 As[2][BM * SK];
-    __shared__ __attribute__((aligned(16))) u16 Bs[2][BN * SK];
+    __shared__ __attribute__((aligned(16))) u16 As[2][A_LDS];
+    __shared__ __attribute__((aligned(16))) u16 Bs[2][B_LDS];
+    // Element (k, x) of a k-major tile with rows of W elements: row stride
+    // W + 32 elements, and the second half of the k range 256 bytes further
+    // on, so the 8 rows of one transposing read (4 per lane half, BK/2 apart)
+    // fall on distinct banks.
+    auto tr_at = [](int k, int x, int W) { return k * (W + 32) + (k >= BK / 2 ? 128 : 0) + x; };
 
     const int tid  = threadIdx.x;
     const int lane = tid & 63;
@@ -164,12 +177,12 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
     // Staging registers.  VEC, k-contiguous operand: ROWS*BK/8 vectors of 8 k;
     // VEC, transposed operand: ROWS*BK/64 blocks of 8 x 8; scalar: ROWS*BK
     // elements.  Threads beyond the count idle for that operand.
-    constexpr int A_VECS = VEC ? (TA ? BM * BK / 64 : BM * BK / 8) : 0;
-    constexpr int B_VECS = VEC ? (TB ? BN * BK / 8 : BN * BK / 64) : 0;
+    constexpr int A_VECS = VEC ? (TA && !A_TR ? BM * BK / 64 : BM * BK / 8) : 0;
+    constexpr int B_VECS = VEC ? (TB || B_TR ? BN * BK / 8 : BN * BK / 64) : 0;
     constexpr int A_PER  = VEC ? (A_VECS + NT - 1) / NT : BM * BK / NT;
     constexpr int B_PER  = VEC ? (B_VECS + NT - 1) / NT : BN * BK / NT;
-    constexpr int A_REGS = VEC && TA ? 8 : 1;   // vectors per staging slot
-    constexpr int B_REGS = VEC && !TB ? 8 : 1;
+    constexpr int A_REGS = VEC && TA && !A_TR ? 8 : 1;  // vectors per staging slot
+    constexpr int B_REGS = VEC && !TB && !B_TR ? 8 : 1;
     static_assert(VEC || (BM * BK % NT == 0 && BN * BK % NT == 0), "scalar staging");
     u32x4 ra[VEC ? A_PER : 1][A_REGS];
     u32x4 rb[VEC ? B_PER : 1][B_REGS];
@@ -204,6 +217,11 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                         const int gm = m0 + r, gk = k0 + kq;
                         ra[j][0] = zero4;
                         if (!CHECKED || (gm < M && gk < kend)) ra[j][0] = *reinterpret_cast<const u32x4*>(a_at(gm, gk));
+                    } else if constexpr (A_TR) {  // (k, 8 m) vectors along the contiguous m
+                        const int k = idx / (BM / 8), mq = 8 * (idx % (BM / 8));
+                        const int gm = m0 + mq, gk = k0 + k;
+                        ra[j][0] = zero4;
+                        if (!CHECKED || (gm < M && gk < kend)) ra[j][0] = *reinterpret_cast<const u32x4*>(a_at(gm, gk));
                     } else {
                         // 8 x 8 blocks: 8 consecutive m at k = kb..kb+7.  Consecutive
                         // threads take consecutive k blocks of the same 8 rows, so
@@ -230,6 +248,11 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                     if constexpr (TB) {  // (c, 8 k) vectors
                         const int c = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
                         const int gn = n0 + c, gk = k0 + kq;
+                        rb[j][0] = zero4;
+                        if (!CHECKED || (gn < N && gk < kend)) rb[j][0] = *reinterpret_cast<const u32x4*>(b_at(gk, gn));
+                    } else if constexpr (B_TR) {  // (k, 8 n) vectors along the contiguous n
+                        const int k = idx / (BN / 8), nq = 8 * (idx % (BN / 8));
+                        const int gn = n0 + nq, gk = k0 + k;
                         rb[j][0] = zero4;
                         if (!CHECKED || (gn < N && gk < kend)) rb[j][0] = *reinterpret_cast<const u32x4*>(b_at(gk, gn));
                     } else {  // 8 x 8 blocks: 8 consecutive n at k = kb..kb+7 (thread order as for a)
@@ -273,6 +296,9 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                     if constexpr (!TA) {
                         const int r = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
                         *reinterpret_cast<u32x4*>(&As[buf][r * SK + kq]) = ra[j][0];
+                    } else if constexpr (A_TR) {
+                        const int k = idx / (BM / 8), mq = 8 * (idx % (BM / 8));
+                        *reinterpret_cast<u32x4*>(&As[buf][tr_at(k, mq, BM)]) = ra[j][0];
                     } else {
                         const int kb = 8 * (idx % (BK / 8)), r = 8 * (idx / (BK / 8));
                         u32x4 w[8];
@@ -289,6 +315,9 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                     if constexpr (TB) {
                         const int c = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
                         *reinterpret_cast<u32x4*>(&Bs[buf][c * SK + kq]) = rb[j][0];
+                    } else if constexpr (B_TR) {
+                        const int k = idx / (BN / 8), nq = 8 * (idx % (BN / 8));
+                        *reinterpret_cast<u32x4*>(&Bs[buf][tr_at(k, nq, BN)]) = rb[j][0];
                     } else {
                         const int kb = 8 * (idx % (BK / 8)), c = 8 * (idx / (BK / 8));
                         u32x4 w[8];
@@ -316,14 +345,37 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
         // All MFMAs of one stage; operands of step s+1 are read while step
         // s's MFMAs run (the compiler hoists the reads of the unrolled loop).
         // Operands of k-step s of LDS buffer `buf`.
+        // A k-major (TR) tile is read with ds_read_b64_tr_b16: within each
+        // group of 16 lanes, lane 4j + a reads 4 consecutive elements of k
+        // row j, and lane 4a + e receives element e of lanes a, 4 + a, 8 + a,
+        // 12 + a, i.e. 4 consecutive k of one column.  Lane l's source row
+        // and column offset are j = (l & 15) >> 2 and 16 * ((l >> 4) & 1) +
+        // 4 * (l & 3); two reads (k + 0..3, k + 4..7) make one operand.
+        const int tr_k = (lane & 15) >> 2, tr_x = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+        auto read_tr = [&](const u16* tile, int W, int kk, int x) {
+            typedef short v4i16 __attribute__((ext_vector_type(4)));
+            typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+            const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(tile + tr_at(kk + tr_k, x + tr_x, W)));
+            const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(tile + tr_at(kk + 4 + tr_k, x + tr_x, W)));
+            const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+            return u32x4{l2[0], l2[1], h2[0], h2[1]};
+        };
         auto read_ops = [&](int buf, int s, u32x4 (&av)[TM], u32x4 (&bv)[TN]) {
             const int kk = h * (BK / 2) + 8 * s;
 #pragma unroll
-            for (int bi = 0; bi < TM; ++bi)
-                av[bi] = *reinterpret_cast<const u32x4*>(&As[buf][(wrow + bi * 32 + li) * SK + kk]);
+            for (int bi = 0; bi < TM; ++bi) {
+                if constexpr (A_TR)
+                    av[bi] = read_tr(As[buf], BM, kk, wrow + bi * 32);
+                else
+                    av[bi] = *reinterpret_cast<const u32x4*>(&As[buf][(wrow + bi * 32 + li) * SK + kk]);
+            }
 #pragma unroll
-            for (int bj = 0; bj < TN; ++bj)
-                bv[bj] = *reinterpret_cast<const u32x4*>(&Bs[buf][(wcol + bj * 32 + li) * SK + kk]);
+            for (int bj = 0; bj < TN; ++bj) {
+                if constexpr (B_TR)
+                    bv[bj] = read_tr(Bs[buf], BN, kk, wcol + bj * 32);
+                else
+                    bv[bj] = *reinterpret_cast<const u32x4*>(&Bs[buf][(wcol + bj * 32 + li) * SK + kk]);
+            }
         };
         // MFMAs [first, last) of one k-step, blocks in row-major order.
         auto mfmas = [&](const u32x4 (&av)[TM], const u32x4 (&bv)[TN], int first, int last) {
@@ -357,7 +409,7 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
             // k-steps; otherwise the in-register transposes do not fit beside
             // it in the register budget, and every LDS write and load stays in
             // the last k-step.
-            constexpr bool SPREAD = (!TA && TB) || ALLSPREAD;
+            constexpr bool SPREAD = (!TA && TB) || ALLSPREAD || TR;
             if constexpr (SPREAD) {
                 // Software pipeline.  Stage st computes from LDS buffer st&1
                 // while registers hold the global data of stage st+1.  The
@@ -379,8 +431,8 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                 constexpr int ENT   = A_PER + B_PER;
                 constexpr int PART  = (ENT + STEPS - 1) / STEPS;
                 // Instructions per entry: 16-byte global loads and LDS writes.
-                constexpr int A_INS = TA ? 8 : 1;
-                constexpr int B_INS = TB ? 1 : 8;
+                constexpr int A_INS = TA && !A_TR ? 8 : 1;
+                constexpr int B_INS = TB || B_TR ? 1 : 8;
                 // Upper bound of one part's loads (or writes) per tail MFMA.
                 constexpr int PER_MFMA = (PART * (A_INS > B_INS ? A_INS : B_INS) + NB - TAIL - 1) / (NB - TAIL);
                 u32x4 opa[2][TM], opb[2][TN];
@@ -470,7 +522,7 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                     load_stage(clamp_k0(st + 2));
                     mfmas(opa[L], opb[L], 0, NB - TAIL);
                     // Spread the LDS writes and global loads over these MFMAs.
-                    constexpr int WR = (VEC ? (TA ? 8 * A_PER : A_PER) + (TB ? B_PER : 8 * B_PER) : 0);
+                    constexpr int WR = (VEC ? (A_REGS * A_PER) + (B_REGS * B_PER) : 0);
                     constexpr int PER = (WR + NB - TAIL - 1) / (NB - TAIL);
     #pragma unroll
                     for (int i = 0; i < NB - TAIL; ++i) {
@@ -579,9 +631,9 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
 }
 
 template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, int SPLIT, bool TA, bool TB,
-          bool ALLSPREAD = false>
+          bool ALLSPREAD = false, bool TR = false>
 __global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p) {
-    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, SPLIT, TA, TB, ALLSPREAD>(p, blockIdx.x, blockIdx.z);
+    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, SPLIT, TA, TB, ALLSPREAD, TR>(p, blockIdx.x, blockIdx.z);
 }
 
 // Grouped GEMM over a device table of per-group parameters (see
@@ -599,7 +651,7 @@ __device__ __forceinline__ int find_group(const int32_t* __restrict__ start, int
 }
 
 template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, bool TA, bool TB,
-          bool ALLSPREAD = false>
+          bool ALLSPREAD = false, bool TR = false>
 __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_half_gemm(GroupedHalfArgs g) {
     const int bid = blockIdx.x;
     const int grp = find_group(g.tile_start, g.groups, bid);
@@ -608,22 +660,22 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_half_gemm(GroupedHa
     // hardware id's XCD (id mod 8); ids past the group's tiles are padding.
     const int local = bid - g.tile_start[grp];
     if (local >= p.tiles_m * p.tiles_n) return;
-    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, kWhole, TA, TB, ALLSPREAD>(p, local, 0);
+    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, kWhole, TA, TB, ALLSPREAD, TR>(p, local, 0);
 }
 
-// The 256x256 tile per operand orientation.  Row-major a: 8 waves of 128x64,
-// two per SIMD.  Column-major a (transposed in registers): 4 waves of
-// 128x128, one per SIMD, whose 512 registers (accumulators in AGPRs) fit the
-// spread staging beside the transposes without spilling.  Measured bf16
-// (TFLOP/s, 4 waves against 8): column-major a with row-major b 965 / 783 at
-// 8192^3, 834 / 740 at MLP fwd, 758 / 648 at 4096^3; both column-major 1095 /
-// 1008, 943 / 939, 863 / 818.  Row-major a with row-major b gains at 8192^3
-// with 4 waves and a second staging register set (1077 / 1028) but loses at
-// MLP fwd (924 / 944) and 4096^3 (833 / 858), so it keeps 8 waves.
-template <bool TA, bool TB>
+// The 256x256 tile, every operand orientation: 8 waves of 128x64 (two per
+// SIMD), transposed operands stored k-major and read with transposing LDS
+// reads (TR), staging spread over the k-steps.  Results are bit-identical to
+// transposing in registers (same MFMA sequence).  Measured bf16, TFLOP/s at
+// 8192^3 / 4096^3, TR against the in-register transposes with their best
+// wave counts: row-major a with row-major b 1221 / 1128 against 1079 / 955;
+// column-major a with row-major b 1216 / 1126 against 974 / 789; both
+// column-major 1226 / 1114 against 1146 / 946.  TR with 4 waves of 128x128:
+// 1153-1201 / 967-999.
 struct Wide {
-    static constexpr int WN      = TA ? 2 : 4;
-    static constexpr bool SPREAD = TA;
+    static constexpr int WN      = 4;
+    static constexpr bool SPREAD = false;
+    static constexpr bool TR     = true;
 };
 
 // The half-precision tiles (index as in kHalfTiles) for one input type and
@@ -632,9 +684,9 @@ template <bool BF16, bool TA, bool TB>
 const void* halfKernel(int tile) {
     switch (tile) {
         case 0: {
-            using W = Wide<TA, TB>;
+            using W = Wide;
             return reinterpret_cast<const void*>(
-                &half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, kWhole, TA, TB, W::SPREAD>);
+                &half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, kWhole, TA, TB, W::SPREAD, W::TR>);
         }
         case 1: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kWhole, TA, TB>);
         case 2: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kPartial, TA, TB>);
@@ -644,16 +696,16 @@ const void* halfKernel(int tile) {
 }
 
 // Grouped variants: 0 = 128x128 (16-byte loads), 1 = 64x64 per-element,
-// 2 = 256x256 (16-byte loads, Wide<TA, TB> waves).
+// 2 = 256x256 (16-byte loads, Wide).
 template <bool BF16, bool TA, bool TB>
 const void* groupedHalfKernel(int which) {
     switch (which) {
         case 0: return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, TA, TB>);
         case 1: return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 64, 64, 32, 2, 2, 2, false, TA, TB>);
         case 2: {
-            using W = Wide<TA, TB>;
+            using W = Wide;
             return reinterpret_cast<const void*>(
-                &grouped_half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, TA, TB, W::SPREAD>);
+                &grouped_half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, TA, TB, W::SPREAD, W::TR>);
         }
         default: return nullptr;
     }

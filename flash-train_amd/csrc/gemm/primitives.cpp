@@ -184,7 +184,7 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
         wide_ = WideParams{a, b, c, d, alpha, beta, s.m, s.n, s.k, a_rs, a_cs, b_rs, b_cs, g.ldc, g.ldd};
 
         kernel_ = gemm::kernelFor(v_, g.ta, g.tb);
-        const int threads = gemm::blockThreads(v_, g.ta, g.tb);
+        const int threads = info_->threads;
         checkBlockSize(kernel_, threads, info_->name);
         block_  = dim3(threads);
         if (info_->simt) {

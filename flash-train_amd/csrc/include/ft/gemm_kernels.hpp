@@ -186,11 +186,6 @@ constexpr uint64_t kMaxPartialBytes = 256ull << 20;
 
 const VariantInfo& info(Variant v);
 
-// Workgroup size of variant v's kernel for an operand orientation (ta: a
-// column-major, tb: b column-major): the catalog's, except the 16-bit 256x256
-// tile, which runs 4 waves (256 threads) when a is column-major.
-int blockThreads(Variant v, bool ta, bool tb);
-
 // Device entry points (host-side stubs registered by the HIP TUs).
 // kernelFor: the variant's kernel for a column-major (ta) or row-major a and
 // a column-major (tb) or row-major b; null when that layout is not
