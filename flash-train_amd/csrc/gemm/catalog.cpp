@@ -10,6 +10,8 @@ namespace {
 // efficiency with one resident workgroup.  The fp32 efficiencies are fitted to Primitive timings
 // on MI355X (every applicable Primitive over 14 shapes from 64x4096x4096 to 16384x14336x4096,
 // random N(0,1) inputs, best of 3 interleaved passes), minimising the time lost by the top pick.
+// The 16-bit efficiencies are set by hand so that the ranking matches measured timings from
+// 1024^3 to 8192^3 in every layout (the 64x64 tile loses to 128x128 from 1024^3 on).
 constexpr SplitKind N = SplitKind::kNone, P = SplitKind::kPartial;
 constexpr FTrainNumericType FP32 = FTRAIN_NUMERIC_TYPE_FP32, BF16 = FTRAIN_NUMERIC_TYPE_BF16,
                             FP16 = FTRAIN_NUMERIC_TYPE_FP16;
@@ -43,11 +45,11 @@ constexpr VariantInfo kInfo[] = {
     {"Bf16MfmaGemm_256x256", 256, 256, 64, 512, 1, true, N, false, false, true, 0.6, BF16, 4096.0, 0.6},
     {"Bf16MfmaGemm_128x128", 128, 128, 64, 256, 2, true, N, false, false, true, 0.5, BF16, 4096.0, 0.5},
     {"Bf16MfmaGemm_128x128_SplitK", 128, 128, 64, 256, 2, true, P, false, false, true, 0.4, BF16, 4096.0, 0.4},
-    {"Bf16MfmaGemm_64x64_Unaligned", 64, 64, 32, 256, 2, false, N, false, false, true, 0.15, BF16, 4096.0, 0.15},
+    {"Bf16MfmaGemm_64x64_Unaligned", 64, 64, 32, 256, 2, false, N, false, false, true, 0.1, BF16, 4096.0, 0.1},
     {"Fp16MfmaGemm_256x256", 256, 256, 64, 512, 1, true, N, false, false, true, 0.6, FP16, 4096.0, 0.6},
     {"Fp16MfmaGemm_128x128", 128, 128, 64, 256, 2, true, N, false, false, true, 0.5, FP16, 4096.0, 0.5},
     {"Fp16MfmaGemm_128x128_SplitK", 128, 128, 64, 256, 2, true, P, false, false, true, 0.4, FP16, 4096.0, 0.4},
-    {"Fp16MfmaGemm_64x64_Unaligned", 64, 64, 32, 256, 2, false, N, false, false, true, 0.15, FP16, 4096.0, 0.15},
+    {"Fp16MfmaGemm_64x64_Unaligned", 64, 64, 32, 256, 2, false, N, false, false, true, 0.1, FP16, 4096.0, 0.1},
 };
 static_assert(sizeof(kInfo) / sizeof(kInfo[0]) == static_cast<int>(Variant::kCount), "catalog");
 

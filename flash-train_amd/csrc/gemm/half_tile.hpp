@@ -139,16 +139,25 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
     // transposing LDS reads; otherwise it is transposed in registers.
     constexpr bool A_TR = TR && VEC && TA;
     constexpr bool B_TR = TR && VEC && !TB;
-    constexpr int A_LDS = A_TR ? BK * (BM + 32) + 128 : BM * SK;
-    constexpr int B_LDS = B_TR ? BK * (BN + 32) + 128 : BN * SK;
+    constexpr int A_LDS = A_TR ? (BM >= 256 ? BK * (BM + 32) + 128 : BK * BM) : BM * SK;
+    constexpr int B_LDS = B_TR ? (BN >= 256 ? BK * (BN + 32) + 128 : BK * BN) : BN * SK;
 
     __shared__ __attribute__((aligned(16))) u16 As[2][A_LDS];
     __shared__ __attribute__((aligned(16))) u16 Bs[2][B_LDS];
-    // Element (k, x) of a k-major tile with rows of W elements: row stride
-    // W + 32 elements, and the second half of the k range 256 bytes further
-    // on, so the 8 rows of one transposing read (4 per lane half, BK/2 apart)
-    // fall on distinct banks.
-    auto tr_at = [](int k, int x, int W) { return k * (W + 32) + (k >= BK / 2 ? 128 : 0) + x; };
+    // Element (k, x) of a k-major tile with rows of W elements.  One
+    // transposing read covers 64 bytes of 4 consecutive rows per lane half,
+    // the halves BK/2 rows apart; the layout puts those 8 row pieces on
+    // distinct banks.  W >= 256: row stride W + 32 elements, and the second
+    // half of the k range 256 bytes further on.  W = 128 (rows of 256
+    // bytes, no pad): 64-byte group g of row k is stored at group
+    // g ^ (k & 3) ^ ((k / (BK/2)) & 1); 16-byte writes of 8 consecutive
+    // lanes stay inside one aligned 128-byte run.
+    static_assert((!A_TR || BM == 128 || BM >= 256) && (!B_TR || BN == 128 || BN >= 256), "TR tile width");
+    auto tr_at = [](int k, int x, int W) {
+        if (W >= 256) return k * (W + 32) + (k >= BK / 2 ? 128 : 0) + x;
+        const int f = (k & 3) ^ ((k / (BK / 2)) & 1);
+        return k * W + (x ^ (32 * f));
+    };
 
     const int tid  = threadIdx.x;
     const int lane = tid & 63;
@@ -671,7 +680,10 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_half_gemm(GroupedHa
 // wave counts: row-major a with row-major b 1221 / 1128 against 1079 / 955;
 // column-major a with row-major b 1216 / 1126 against 974 / 789; both
 // column-major 1226 / 1114 against 1146 / 946.  TR with 4 waves of 128x128:
-// 1153-1201 / 967-999.
+// 1153-1201 / 967-999.  The 128x128 tiles (4 waves of 64x64, two
+// workgroups per CU) use TR too: at 2048^3 / 4096^3 row-major a with
+// row-major b 571 / 921 against 441 / 736, column-major a with row-major b
+// 565 / 875 against 287 / 507, both column-major 577 / 880 against 454 / 735.
 struct Wide {
     static constexpr int WN      = 4;
     static constexpr bool SPREAD = false;
@@ -688,8 +700,9 @@ const void* halfKernel(int tile) {
             return reinterpret_cast<const void*>(
                 &half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, kWhole, TA, TB, W::SPREAD, W::TR>);
         }
-        case 1: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kWhole, TA, TB>);
-        case 2: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kPartial, TA, TB>);
+        case 1: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kWhole, TA, TB, false, true>);
+        case 2:
+            return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kPartial, TA, TB, false, true>);
         case 3: return reinterpret_cast<const void*>(&half_gemm<BF16, 64, 64, 32, 2, 2, 2, false, kWhole, TA, TB>);
         default: return nullptr;
     }
@@ -700,7 +713,8 @@ const void* halfKernel(int tile) {
 template <bool BF16, bool TA, bool TB>
 const void* groupedHalfKernel(int which) {
     switch (which) {
-        case 0: return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, TA, TB>);
+        case 0:
+            return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, TA, TB, false, true>);
         case 1: return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 64, 64, 32, 2, 2, 2, false, TA, TB>);
         case 2: {
             using W = Wide;
