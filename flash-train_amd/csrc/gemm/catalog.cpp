@@ -40,6 +40,7 @@ constexpr VariantInfo kInfo[] = {
     {"Fp32MfmaGemm_128x128_Unaligned", 128, 128, 16, 256, 2, false, N, false, false, true, 0.66, FP32, 256.0, 0.675},
     {"Fp32MfmaGemm_128x128_Unaligned_SplitK", 128, 128, 16, 256, 2, false, P, false, false, true, 0.55, FP32, 256.0, 0.4},
     {"Fp32MfmaGemm_64x64_Unaligned", 64, 64, 16, 256, 4, false, N, false, false, true, 0.585, FP32, 256.0, 0.45},
+    {"Fp32Gemv", kGemvRows, kGemvPassCols, 1, 1024, 1, true, N, true, false, false, 0, FP32, 256.0, 0},
     {"Fp32Gemv_SplitK", kGemvRows, kGemvCols, 1, 256, 8, true, P, true, false, false, 0, FP32, 256.0, 0},
     {"Fp32Gemv_Unaligned_SplitK", kGemvRows, kGemvCols, 1, 256, 8, false, P, true, false, false, 0, FP32, 256.0, 0},
     {"Fp32Gemm", 64, 64, 16, 256, 2, false, N, false, true, true, 0.2, FP32, 256.0, 0.2},

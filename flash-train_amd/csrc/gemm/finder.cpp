@@ -88,8 +88,13 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
         launch += kLaunchMicros + kPoolMicros;
     }
     if (vi.gemv) {
-        const double wgs = double(ceilDiv(std::max<uint64_t>(s.n, 1), kGemvCols) * splits);
-        const double fill = std::min(1.0, wgs / (double(cus) * 4.0));  // too few workgroups cannot reach HBM peak
+        // Too few waves cannot reach the HBM peak; about four per CU do
+        // (measured with the one-pass kernel: 1024 waves over 256 CUs stream
+        // 5.4-6.3 TB/s, 256 waves lose to split-k).
+        int threads = vi.threads;
+        if (vi.split == SplitKind::kNone) (void)gemvKernel(int(std::max<uint64_t>(s.m, 1)), false, threads);
+        const double wgs  = double(ceilDiv(std::max<uint64_t>(s.n, 1), uint64_t(vi.bn)) * splits);
+        const double fill = std::min(1.0, wgs * (threads / 64) / (double(cus) * 4.0));
         return bytes / (kHbmBytesPerMicro * fill) + serial_us + launch;
     }
     // Work per workgroup includes the tile padding at the m/n edges.  The

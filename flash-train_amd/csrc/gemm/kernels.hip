@@ -99,6 +99,106 @@ __global__ __launch_bounds__(256) void gemv_splitk(GemmParams p) {
 }
 
 // ----------------------------------------------------------------------------
+// One-pass skinny-m kernel (m <= MR <= 8, row-major b with 16-byte aligned
+// rows, n % 4 == 0).  Workgroup x owns output columns [32x, 32x + 32) over
+// all of k, so no partial sums leave it and d is written directly.  Lane
+// (r = lane / 8, q = lane % 8) of wave w takes columns 4q .. 4q+3 and, per
+// step, the 4 consecutive k rows 4*(8*(w + NW*j) + r) + t, t = 0..3: one
+// 128-bit load of b per row (8 lanes cover a row's 128 bytes, a wave 8
+// rows), and for a row-major a one 128-bit load of a's 4 values per row of
+// a.  U steps are loaded before any is used, so each wave keeps U*4 KiB of
+// b in flight.  Reduction, fixed order: a butterfly over the 8 lanes that
+// share columns (lane bits 3..5), then the NW wave sums in wave order
+// through LDS.  a row-major (TA false) needs k % 4 == 0 and lda % 4 == 0;
+// column-major a is read per element.
+// ----------------------------------------------------------------------------
+template <int NW, int U, int MR, bool TA>
+__global__ __launch_bounds__(NW * 64) void gemv_pass(GemmParams p) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane >> 3, q = lane & 7;
+    const int M = p.m, N = p.n, K = p.k;
+    const int col0                = blockIdx.x * kGemvPassCols + 4 * q;
+    const bool col_ok             = col0 < N;  // n % 4 == 0: a run of 4 columns is all in or all out
+    const float* __restrict__ A   = p.a;
+    const float* __restrict__ B   = p.b;
+    const size_t lda = p.lda, ldb = p.ldb;
+    constexpr int KSTEP = 32 * NW;  // k rows per step over the workgroup
+
+    float acc[MR][4];
+#pragma unroll
+    for (int i = 0; i < MR; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[i][c] = 0.f;
+
+    // b rows k0 .. k0+3 and a's values at those rows; rows >= K read as 0
+    // (only a column-major a allows K % 4 != 0).
+    auto load = [&](int k0, floatx4 (&bv)[4], floatx4 (&av)[MR], bool full) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            bv[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+            if (col_ok && (full || k0 + t < K)) bv[t] = *reinterpret_cast<const floatx4*>(B + (size_t)(k0 + t) * ldb + col0);
+        }
+#pragma unroll
+        for (int i = 0; i < MR; ++i) {
+            av[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+            if (i >= M) continue;
+            if constexpr (!TA) {
+                if (full || k0 < K) av[i] = *reinterpret_cast<const floatx4*>(A + (size_t)i * lda + k0);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    if (full || k0 + t < K) av[i][t] = A[(size_t)(k0 + t) * lda + i];
+            }
+        }
+    };
+    auto fma = [&](const floatx4 (&bv)[4], const floatx4 (&av)[MR]) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < MR; ++i)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[i][c] += av[i][t] * bv[t][c];
+    };
+
+    int k = 4 * (8 * wave + r);
+    for (; k + (U - 1) * KSTEP + 3 < K; k += U * KSTEP) {
+        floatx4 bv[U][4], av[U][MR];
+#pragma unroll
+        for (int u = 0; u < U; ++u) load(k + u * KSTEP, bv[u], av[u], true);
+#pragma unroll
+        for (int u = 0; u < U; ++u) fma(bv[u], av[u]);
+    }
+    for (; k < K; k += KSTEP) {
+        floatx4 bv[4], av[MR];
+        load(k, bv, av, false);
+        fma(bv, av);
+    }
+
+#pragma unroll
+    for (int sh = 8; sh < 64; sh <<= 1)
+#pragma unroll
+        for (int i = 0; i < MR; ++i)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[i][c] += __shfl_xor(acc[i][c], sh);
+    __shared__ float part[NW][MR][kGemvPassCols];
+    if (r == 0)
+#pragma unroll
+        for (int i = 0; i < MR; ++i)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) part[wave][i][4 * q + c] = acc[i][c];
+    __syncthreads();
+    if (threadIdx.x < kGemvPassCols * MR) {
+        const int i = threadIdx.x / kGemvPassCols, c = threadIdx.x % kGemvPassCols;
+        const int col = blockIdx.x * kGemvPassCols + c;
+        if (i < M && col < N) {
+            float s = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) s += part[w][i][c];
+            p.d[(size_t)i * p.ldd + col] = p.alpha * s + (p.c != nullptr ? p.beta * p.c[(size_t)i * p.ldc + col] : 0.f);
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
 // Split-k reduction: d = alpha * sum_{z < splits} W[z] + (c ? beta*c : 0) in a
 // fixed summation order (deterministic).  The slices are dense m x n fp32; c
 // and d are row-major with row strides ldc and ldd, in fp32 or a 16-bit type
@@ -243,6 +343,27 @@ __global__ __launch_bounds__(256) void simt_gemm(WideParams p) {
 
 }  // namespace
 
+// Waves and steps in flight per row count, measured at n = k = 8192: one
+// row 8 waves x 2 steps (37.8 us), two and four rows 16 x 2 (38.9 / 38.8),
+// eight rows 8 x 4 (43.3).
+const void* gemvKernel(int m, bool ta, int& threads) {
+    const void* k = nullptr;
+    if (m <= 1) {
+        threads = 512;
+        k = ta ? reinterpret_cast<const void*>(&gemv_pass<8, 2, 1, true>) : reinterpret_cast<const void*>(&gemv_pass<8, 2, 1, false>);
+    } else if (m <= 2) {
+        threads = 1024;
+        k = ta ? reinterpret_cast<const void*>(&gemv_pass<16, 2, 2, true>) : reinterpret_cast<const void*>(&gemv_pass<16, 2, 2, false>);
+    } else if (m <= 4) {
+        threads = 1024;
+        k = ta ? reinterpret_cast<const void*>(&gemv_pass<16, 2, 4, true>) : reinterpret_cast<const void*>(&gemv_pass<16, 2, 4, false>);
+    } else {
+        threads = 512;
+        k = ta ? reinterpret_cast<const void*>(&gemv_pass<8, 4, 8, true>) : reinterpret_cast<const void*>(&gemv_pass<8, 4, 8, false>);
+    }
+    return k;
+}
+
 const void* kernelFor(Variant v, bool ta, bool tb) {
     if (v >= Variant::kMfma16_256x256 && v <= Variant::kMfma16_256x64S) {
         using Fn                     = const void* (*)(int);
@@ -260,6 +381,10 @@ const void* kernelFor(Variant v, bool ta, bool tb) {
     }
     if (ta || tb) {
         if (v == Variant::kSimt) return reinterpret_cast<const void*>(&simt_gemm);  // strides are runtime values
+        if (v == Variant::kGemv && !tb && ta) {
+            int threads = 0;
+            return gemvKernel(kGemvRows, true, threads);
+        }
         if (v == Variant::kGemvS && !tb && ta) return reinterpret_cast<const void*>(&gemv_splitk<true, true>);
         if (v == Variant::kGemvUS && !tb && ta) return reinterpret_cast<const void*>(&gemv_splitk<false, true>);
         if (!info(v).layouts) return nullptr;
@@ -273,6 +398,10 @@ const void* kernelFor(Variant v, bool ta, bool tb) {
         case Variant::kMfma64x256S: return reinterpret_cast<const void*>(&mfma_gemm<64, 256, 16, 1, 4, 3, 1, true, kPartial, false, false>);
         case Variant::kMfma256x64: return reinterpret_cast<const void*>(&mfma_gemm<256, 64, 16, 4, 1, 3, 1, true, kWhole, false, false>);
         case Variant::kMfma256x64S: return reinterpret_cast<const void*>(&mfma_gemm<256, 64, 16, 4, 1, 3, 1, true, kPartial, false, false>);
+        case Variant::kGemv: {
+            int threads = 0;
+            return gemvKernel(kGemvRows, false, threads);
+        }
         case Variant::kGemvS: return reinterpret_cast<const void*>(&gemv_splitk<true, false>);
         case Variant::kGemvUS: return reinterpret_cast<const void*>(&gemv_splitk<false, false>);
         case Variant::kSimt: return reinterpret_cast<const void*>(&simt_gemm);

@@ -183,8 +183,8 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
         const int64_t b_rs = g.tb ? 1 : g.ldb, b_cs = g.tb ? g.ldb : 1;
         wide_ = WideParams{a, b, c, d, alpha, beta, s.m, s.n, s.k, a_rs, a_cs, b_rs, b_cs, g.ldc, g.ldd};
 
-        kernel_ = gemm::kernelFor(v_, g.ta, g.tb);
-        const int threads = info_->threads;
+        int threads = info_->threads;
+        kernel_     = v_ == Variant::kGemv ? gemm::gemvKernel(int(s.m), g.ta, threads) : gemm::kernelFor(v_, g.ta, g.tb);
         checkBlockSize(kernel_, threads, info_->name);
         block_  = dim3(threads);
         if (info_->simt) {
@@ -209,7 +209,7 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
                                       0,            0,            g.lda,        g.ldb, g.ldc, g.ldd,
                                       int32_t(cd_half)};
         if (info_->gemv) {
-            grid_ = dim3(static_cast<uint32_t>(ceilDiv(s.n, gemm::kGemvCols)), 1, splits);
+            grid_ = dim3(static_cast<uint32_t>(ceilDiv(s.n, uint64_t(info_->bn))), 1, splits);
         } else {
             params_.tiles_m = half_params_.tiles_m = int32_t(ceilDiv(s.m, info_->bm));
             params_.tiles_n = half_params_.tiles_n = int32_t(ceilDiv(s.n, info_->bn));

@@ -100,6 +100,8 @@ struct ReduceParams {
 // columns per workgroup.
 constexpr int kGemvRows = 8;
 constexpr int kGemvCols = 256;
+// Columns per workgroup of the one-pass skinny kernel (128 bytes of a b row).
+constexpr int kGemvPassCols = 32;
 
 enum class Variant : int {
     // v_mfma_f32_16x16x4_f32 256x256 tiles, 4 waves of 128x128 (one per
@@ -136,7 +138,11 @@ enum class Variant : int {
     kMfma128x128U,
     kMfma128x128US,
     kMfma64x64U,
-    // Skinny m (<= 8): streaming GEMV-style split-k with atomic accumulation.
+    // Skinny m (<= 8), 128-bit loads of b: one pass, 32 columns per
+    // workgroup over all of k, reduced in the workgroup in a fixed order.
+    kGemv,
+    // Skinny m (<= 8): streaming split-k, partial slices reduced by
+    // splitk_reduce in a fixed order.
     kGemvS,
     kGemvUS,
     // General SIMT kernel with 64-bit indexing.
@@ -191,6 +197,10 @@ const VariantInfo& info(Variant v);
 // a column-major (tb) or row-major b; null when that layout is not
 // instantiated for the variant (see VariantInfo::layouts).
 const void* kernelFor(Variant v, bool ta = false, bool tb = false);
+// The one-pass skinny kernel (Variant::kGemv) for m rows of a (1..kGemvRows)
+// and a row-major (ta false) or column-major a; `threads` receives its
+// workgroup size.  b is row-major.
+const void* gemvKernel(int m, bool ta, int& threads);
 // Per-layout instantiations of the layout-capable MFMA variants (one HIP TU
 // each); null for other variants.
 const void* layoutKernelTN(Variant v);  // column-major a, row-major b

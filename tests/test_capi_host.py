@@ -556,7 +556,13 @@ def test_finder_choices_for_the_baseline_configs(tlib):
     assert rank(tlib, 2048, 2048, 2048)[0] in ("Fp32Mfma16Gemm_256x64", "Fp32Mfma16Gemm_64x256")
     # 1024^3: whole-k 64x64 (29.9) against the best split-k tile (38.5).
     assert rank(tlib, 1024, 1024, 1024)[0] == "Fp32MfmaGemm_64x64"
-    assert rank(tlib, 1, 8192, 8192)[0] == "Fp32Gemv_SplitK"
+    # GEMV: the one-pass kernel (37.8 us) against split-k plus its reduction (47.6 us).
+    assert rank(tlib, 1, 8192, 8192)[0] == "Fp32Gemv"
+    # It also wins with 128 (1x4096x8192: 24.8 against 39.2 us) and 64 workgroups of 16 waves
+    # (2x2048x4096: 10.7 against 14.7); with 32 workgroups of 8 waves split-k wins (14.3 against 16.5).
+    assert rank(tlib, 1, 4096, 8192)[0] == "Fp32Gemv"
+    assert rank(tlib, 2, 2048, 4096)[0] == "Fp32Gemv"
+    assert rank(tlib, 1, 1024, 8192)[0] == "Fp32Gemv_SplitK"
     # Deep or skinny: split-k on the 16x16 skinny tiles (88.3, 34.9, 33.6).
     assert rank(tlib, 256, 256, 65536)[0] == "Fp32Mfma16Gemm_256x64_SplitK"
     assert rank(tlib, 64, 4096, 4096)[0] == "Fp32Mfma16Gemm_64x256_SplitK"
@@ -571,6 +577,7 @@ def test_finder_respects_alignment_and_row_limits(tlib):
     assert names and all(("Unaligned" in n) or n == "Fp32Gemm" for n in names)
     assert not any(n.startswith("Fp32Gemv") for n in rank(tlib, 9, 8192, 8192))
     assert "Fp32Gemv_SplitK" in rank(tlib, 8, 8192, 8192)
+    assert "Fp32Gemv" in rank(tlib, 8, 8192, 8192)
 
 
 def test_plan_order_matches_finder_rank(tlib, tops):

@@ -403,3 +403,34 @@ def test_skinny_gemv_is_deterministic(capi, ops, oracle):
         assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2]), plan.name(i)
         rep = oracle.tolerance_check(outs[0].cpu().numpy(), ref, k)
         assert rep["ok"], (plan.name(i), rep)
+
+
+@pytest.mark.parametrize("m,n,k,col_a", [(1, 8192, 8192, False), (3, 100, 1000, False), (5, 36, 4, False),
+                                         (8, 4096, 2052, False), (4, 200, 37, True), (8, 68, 1030, True)])
+def test_one_pass_gemv(capi, ops, oracle, m, n, k, col_a):
+    # Fp32Gemv: 32 output columns per workgroup over all of k, reduced in the
+    # workgroup in a fixed order and written straight to d.  Every row count
+    # bucket (1, 2, 4, 8), column counts that leave a partial workgroup, k
+    # tails of a column-major a, and repeated runs bit for bit.
+    g = torch.Generator().manual_seed(100 + m + k)
+    a = torch.randn(k, m, generator=g).t() if col_a else torch.randn(m, k, generator=g)
+    b, c = torch.randn(k, n, generator=g), torch.randn(m, n, generator=g)
+    a, b, c = a.cuda(), b.cuda(), c.cuda()
+    d = torch.empty(m, n, device="cuda")
+    plan = capi.plan_for(a, b, c, d, 1.5, -0.5, ops)
+    names = plan.names()
+    assert "Fp32Gemv" in names, names
+    i = names.index("Fp32Gemv")
+    if (m, n, k) == (1, 8192, 8192):
+        assert i == 0, names
+    ref = oracle.gemm_f64(a.cpu().numpy(), b.cpu().numpy(), c.cpu().numpy(), 1.5, -0.5)
+    s = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for _ in range(3):
+        d.fill_(float("nan"))
+        plan.execute(i, s)
+        torch.cuda.synchronize()
+        outs.append(d.clone())
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+    rep = oracle.tolerance_check(outs[0].cpu().numpy(), ref, k)
+    assert rep["ok"], rep
