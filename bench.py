@@ -249,7 +249,7 @@ def main() -> None:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs the GEMM path on a single MI355X "
-              "(see DESIGN.md for how it would shard); use --gpus 1", file=sys.stderr)
+              "and has no multi-GPU sharding; use --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
