@@ -123,7 +123,7 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 // ----------------------------------------------------------------------------
 // The tile body (see mfma_tile.hpp): tile `bid` of p's grid, split `z`.
 template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, int SPLIT, bool TA, bool TB,
-          bool ALLSPREAD = false, bool TR = false>
+          bool TR = false>
 __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid, int z) {
     using u16           = unsigned short;
     constexpr int NT    = WM * WN * 64;
@@ -412,13 +412,12 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                 __syncthreads();
             }
         } else {
-            // Two schedules.  When both operands are copied straight into LDS
-            // (row-major a, column-major b), or when ALLSPREAD grants the
-            // registers of one wave per SIMD, the staging is spread over all
-            // k-steps; otherwise the in-register transposes do not fit beside
-            // it in the register budget, and every LDS write and load stays in
-            // the last k-step.
-            constexpr bool SPREAD = (!TA && TB) || ALLSPREAD || TR;
+            // Two schedules.  When every operand is copied straight into LDS
+            // (row-major a with column-major b, or TR tiles), the staging is
+            // spread over all k-steps; otherwise the in-register transposes
+            // do not fit beside it in the register budget, and every LDS
+            // write and load stays in the last k-step.
+            constexpr bool SPREAD = (!TA && TB) || TR;
             if constexpr (SPREAD) {
                 // Software pipeline.  Stage st computes from LDS buffer st&1
                 // while registers hold the global data of stage st+1.  The
@@ -640,9 +639,9 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
 }
 
 template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, int SPLIT, bool TA, bool TB,
-          bool ALLSPREAD = false, bool TR = false>
+          bool TR = false>
 __global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p) {
-    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, SPLIT, TA, TB, ALLSPREAD, TR>(p, blockIdx.x, blockIdx.z);
+    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, SPLIT, TA, TB, TR>(p, blockIdx.x, blockIdx.z);
 }
 
 // Grouped GEMM over a device table of per-group parameters (see
@@ -660,7 +659,7 @@ __device__ __forceinline__ int find_group(const int32_t* __restrict__ start, int
 }
 
 template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, bool TA, bool TB,
-          bool ALLSPREAD = false, bool TR = false>
+          bool TR = false>
 __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_half_gemm(GroupedHalfArgs g) {
     const int bid = blockIdx.x;
     const int grp = find_group(g.tile_start, g.groups, bid);
@@ -669,7 +668,7 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_half_gemm(GroupedHa
     // hardware id's XCD (id mod 8); ids past the group's tiles are padding.
     const int local = bid - g.tile_start[grp];
     if (local >= p.tiles_m * p.tiles_n) return;
-    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, kWhole, TA, TB, ALLSPREAD, TR>(p, local, 0);
+    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, kWhole, TA, TB, TR>(p, local, 0);
 }
 
 // The 256x256 tile, every operand orientation: 8 waves of 128x64 (two per
@@ -686,7 +685,6 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_half_gemm(GroupedHa
 // 565 / 875 against 287 / 507, both column-major 577 / 880 against 454 / 735.
 struct Wide {
     static constexpr int WN      = 4;
-    static constexpr bool SPREAD = false;
     static constexpr bool TR     = true;
 };
 
@@ -698,11 +696,11 @@ const void* halfKernel(int tile) {
         case 0: {
             using W = Wide;
             return reinterpret_cast<const void*>(
-                &half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, kWhole, TA, TB, W::SPREAD, W::TR>);
+                &half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, kWhole, TA, TB, W::TR>);
         }
-        case 1: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kWhole, TA, TB, false, true>);
+        case 1: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kWhole, TA, TB, true>);
         case 2:
-            return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kPartial, TA, TB, false, true>);
+            return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kPartial, TA, TB, true>);
         case 3: return reinterpret_cast<const void*>(&half_gemm<BF16, 64, 64, 32, 2, 2, 2, false, kWhole, TA, TB>);
         default: return nullptr;
     }
@@ -714,12 +712,12 @@ template <bool BF16, bool TA, bool TB>
 const void* groupedHalfKernel(int which) {
     switch (which) {
         case 0:
-            return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, TA, TB, false, true>);
+            return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, TA, TB, true>);
         case 1: return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 64, 64, 32, 2, 2, 2, false, TA, TB>);
         case 2: {
             using W = Wide;
             return reinterpret_cast<const void*>(
-                &grouped_half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, TA, TB, W::SPREAD, W::TR>);
+                &grouped_half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, TA, TB, W::TR>);
         }
         default: return nullptr;
     }
