@@ -223,8 +223,9 @@ def test_random_shapes_every_primitive(capi, ops, oracle, shape):
         assert rep["ok"], (name, shape, rep)
 
 
-def test_zero_depth(capi, ops):
-    m, n = 33, 20
+@pytest.mark.parametrize("m", [33, 4])  # 4 rows: the skinny (GEMV) Primitives too
+def test_zero_depth(capi, ops, m):
+    n = 20
     c = torch.randn(m, n, device="cuda")
     d = torch.empty(m, n, device="cuda")
     al, be = capi.HostScalar(2.0), capi.HostScalar(0.5)
@@ -238,19 +239,22 @@ def test_zero_depth(capi, ops):
         torch.testing.assert_close(d, 0.5 * c, rtol=0, atol=0)
 
 
-def test_nan_inf_propagation(capi, ops, oracle):
-    m, n, k = 70, 68, 96
+@pytest.mark.parametrize("m", [70, 6])  # 6 rows: the skinny (GEMV) Primitives too
+def test_nan_inf_propagation(capi, ops, oracle, m):
+    n, k = 68, 96
     g = torch.Generator().manual_seed(11)
     a_h, b_h, c_h = torch.randn(m, k, generator=g), torch.randn(k, n, generator=g), torch.randn(m, n, generator=g)
     a_h[3, 5] = float("nan")
-    a_h[10, 7] = float("inf")
+    a_h[10 % m, 7] = float("inf")
     b_h[9, 40] = float("-inf")
-    c_h[50, 50] = float("nan")
-    c_h[60, 1] = float("inf")
+    c_h[50 % m, 50] = float("nan")
+    c_h[60 % m, 1] = float("inf")
     for beta in (0.0, 0.5):
         ref = oracle.gemm_f64(a_h, b_h, c_h, 1.0, beta)
         d = torch.empty(m, n, device="cuda")
         plan = capi.plan_for(a_h.cuda(), b_h.cuda(), c_h.cuda(), d, 1.0, beta, ops)
+        if m <= 8:
+            assert "Fp32Gemv" in plan.names() and "Fp32Gemv_SplitK" in plan.names(), plan.names()
         for i, name in enumerate(plan.names()):
             plan.execute(i, torch.cuda.current_stream().cuda_stream)
             torch.cuda.synchronize()
