@@ -210,6 +210,12 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
 
     auto main_loop = [&](auto checked_tag) {
         constexpr bool CHECKED = decltype(checked_tag)::value;
+        // m / n index of a load.  The unchecked loop clamps it into the matrix
+        // (a run of `run` elements stays inside): an edge tile then reads
+        // valid memory for rows and columns past the edge, whose products
+        // land only in outputs the epilogue does not store.  Only a k tail
+        // needs the zero-filling checked loop.
+        auto row_at = [](int i, int extent, int run) { return CHECKED ? i : min(i, extent - run); };
 
         // Global loads of one stage (k range [k0, k0 + BK)) into registers.
         // Entries: A staging slots 0 .. A_PER-1, then B slots; [first, last)
@@ -223,12 +229,12 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                     if (A_VECS % NT != 0 && idx >= A_VECS) continue;
                     if constexpr (!TA) {  // (r, 8 k) vectors, 8 threads per row of BK = 64
                         const int r = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
-                        const int gm = m0 + r, gk = k0 + kq;
+                        const int gm = row_at(m0 + r, M, 1), gk = k0 + kq;
                         ra[j][0] = zero4;
                         if (!CHECKED || (gm < M && gk < kend)) ra[j][0] = *reinterpret_cast<const u32x4*>(a_at(gm, gk));
                     } else if constexpr (A_TR) {  // (k, 8 m) vectors along the contiguous m
                         const int k = idx / (BM / 8), mq = 8 * (idx % (BM / 8));
-                        const int gm = m0 + mq, gk = k0 + k;
+                        const int gm = row_at(m0 + mq, M, 8), gk = k0 + k;
                         ra[j][0] = zero4;
                         if (!CHECKED || (gm < M && gk < kend)) ra[j][0] = *reinterpret_cast<const u32x4*>(a_at(gm, gk));
                     } else {
@@ -239,7 +245,7 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                         // consecutive row blocks instead put the 8 lanes' rows 288
                         // dwords apart, an 8-way bank conflict on every write.
                         const int kb = 8 * (idx % (BK / 8)), r = 8 * (idx / (BK / 8));
-                        const int gm = m0 + r;
+                        const int gm = row_at(m0 + r, M, 8);
 #pragma unroll
                         for (int i = 0; i < 8; ++i) {
                             const int gk = k0 + kb + i;
@@ -256,17 +262,17 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                     if (B_VECS % NT != 0 && idx >= B_VECS) continue;
                     if constexpr (TB) {  // (c, 8 k) vectors
                         const int c = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
-                        const int gn = n0 + c, gk = k0 + kq;
+                        const int gn = row_at(n0 + c, N, 1), gk = k0 + kq;
                         rb[j][0] = zero4;
                         if (!CHECKED || (gn < N && gk < kend)) rb[j][0] = *reinterpret_cast<const u32x4*>(b_at(gk, gn));
                     } else if constexpr (B_TR) {  // (k, 8 n) vectors along the contiguous n
                         const int k = idx / (BN / 8), nq = 8 * (idx % (BN / 8));
-                        const int gn = n0 + nq, gk = k0 + k;
+                        const int gn = row_at(n0 + nq, N, 8), gk = k0 + k;
                         rb[j][0] = zero4;
                         if (!CHECKED || (gn < N && gk < kend)) rb[j][0] = *reinterpret_cast<const u32x4*>(b_at(gk, gn));
                     } else {  // 8 x 8 blocks: 8 consecutive n at k = kb..kb+7 (thread order as for a)
                         const int kb = 8 * (idx % (BK / 8)), c = 8 * (idx / (BK / 8));
-                        const int gn = n0 + c;
+                        const int gn = row_at(n0 + c, N, 8);
 #pragma unroll
                         for (int i = 0; i < 8; ++i) {
                             const int gk = k0 + kb + i;
@@ -281,14 +287,14 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                 for (int j = 0; j < A_PER; ++j) {
                     const int idx = tid + j * NT;
                     const int r = TA ? idx % BM : idx / BK, k = TA ? idx / BM : idx % BK;
-                    const int gm = m0 + r, gk = k0 + k;
+                    const int gm = row_at(m0 + r, M, 1), gk = k0 + k;
                     sa[j]        = (!CHECKED || (gm < M && gk < kend)) ? *a_at(gm, gk) : u16(0);
                 }
 #pragma unroll
                 for (int j = 0; j < B_PER; ++j) {
                     const int idx = tid + j * NT;
                     const int c = TB ? idx / BK : idx % BN, k = TB ? idx % BK : idx / BN;
-                    const int gn = n0 + c, gk = k0 + k;
+                    const int gn = row_at(n0 + c, N, 1), gk = k0 + k;
                     sb[j]        = (!CHECKED || (gk < kend && gn < N)) ? *b_at(gk, gn) : u16(0);
                 }
             }
@@ -549,8 +555,7 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
         }
     };
 
-    const bool interior = m0 + BM <= M && n0 + BN <= N && (kend - kbeg) % BK == 0;
-    if (interior)
+    if ((kend - kbeg) % BK == 0)
         main_loop(std::false_type{});
     else
         main_loop(std::true_type{});
