@@ -345,7 +345,8 @@ __global__ __launch_bounds__(256) void simt_gemm(WideParams p) {
 
 // Waves and steps in flight per row count, measured at n = k = 8192: one
 // row 8 waves x 2 steps (37.8 us), two and four rows 16 x 2 (38.9 / 38.8),
-// eight rows 8 x 4 (43.3).
+// eight rows 8 x 2 (the configurations with more in flight, 8 x 4 and
+// 16 x 2, spill registers there).
 const void* gemvKernel(int m, bool ta, int& threads) {
     const void* k = nullptr;
     if (m <= 1) {
@@ -359,7 +360,7 @@ const void* gemvKernel(int m, bool ta, int& threads) {
         k = ta ? reinterpret_cast<const void*>(&gemv_pass<16, 2, 4, true>) : reinterpret_cast<const void*>(&gemv_pass<16, 2, 4, false>);
     } else {
         threads = 512;
-        k = ta ? reinterpret_cast<const void*>(&gemv_pass<8, 4, 8, true>) : reinterpret_cast<const void*>(&gemv_pass<8, 4, 8, false>);
+        k = ta ? reinterpret_cast<const void*>(&gemv_pass<8, 2, 8, true>) : reinterpret_cast<const void*>(&gemv_pass<8, 2, 8, false>);
     }
     return k;
 }

@@ -157,6 +157,12 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
 
     auto main_loop = [&](auto checked_tag) {
         constexpr bool CHECKED = decltype(checked_tag)::value;
+        // m / n index of a load.  The unchecked loop clamps it into the matrix
+        // (a vector of `run` elements stays inside): an edge tile then reads
+        // valid memory for rows and columns past the edge, whose products
+        // land only in outputs the epilogue does not store.  Only a k tail
+        // needs the zero-filling checked loop.
+        auto row_at = [](int i, int extent, int run) { return CHECKED ? i : min(i, extent - run); };
         auto a_at = [&](int gm, int gk) { return A + (TA ? (size_t)gk * lda + gm : (size_t)gm * lda + gk); };
         auto b_at = [&](int gk, int gn) { return B + (TB ? (size_t)gn * ldb + gk : (size_t)gk * ldb + gn); };
 
@@ -165,7 +171,7 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
             for (int j = 0; j < A_LD; ++j) {
                 int r, k;
                 a_coord(j, r, k);
-                const int gm = m0 + r, gk = k0 + k;
+                const int gm = row_at(m0 + r, M, TA ? 4 : 1), gk = k0 + k;
                 ra[j] = floatx4{0.f, 0.f, 0.f, 0.f};
                 if (!CHECKED || (gm < M && gk < kend)) ra[j] = *reinterpret_cast<const floatx4*>(a_at(gm, gk));
             }
@@ -173,7 +179,7 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
             for (int j = 0; j < B_LD; ++j) {
                 int k, c;
                 b_coord(j, k, c);
-                const int gk = k0 + k, gn = n0 + c;
+                const int gk = k0 + k, gn = row_at(n0 + c, N, TB ? 1 : 4);
                 rb[j] = floatx4{0.f, 0.f, 0.f, 0.f};
                 if (!CHECKED || (gk < kend && gn < N)) rb[j] = *reinterpret_cast<const floatx4*>(b_at(gk, gn));
             }
@@ -327,8 +333,7 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
         }
     };
 
-    const bool interior = m0 + BM <= M && n0 + BN <= N && (kend - kbeg) % BK == 0;
-    if (interior)
+    if ((kend - kbeg) % BK == 0)
         main_loop(std::false_type{});
     else
         main_loop(std::true_type{});

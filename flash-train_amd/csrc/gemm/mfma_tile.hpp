@@ -291,6 +291,12 @@ __device__ __forceinline__ void mfma_gemm_tile(const GemmParams& p, int bid, int
 
     auto main_loop = [&](auto checked_tag) {
         constexpr bool CHECKED = decltype(checked_tag)::value;
+        // m / n index of a load.  The unchecked loop clamps it into the matrix
+        // (a vector of `run` elements stays inside): an edge tile then reads
+        // valid memory for rows and columns past the edge, whose products
+        // land only in outputs the epilogue does not store.  Only a k tail
+        // needs the zero-filling checked loop.
+        auto row_at = [](int i, int extent, int run) { return CHECKED ? i : min(i, extent - run); };
 
         // Global address of A(gm, gk) / B(gk, gn).
         auto a_at = [&](int gm, int gk) { return A + (TA ? (size_t)gk * lda + gm : (size_t)gm * lda + gk); };
@@ -301,7 +307,7 @@ __device__ __forceinline__ void mfma_gemm_tile(const GemmParams& p, int bid, int
             for (int j = 0; j < A_LD; ++j) {
                 int r, k;
                 a_coord(j, r, k);
-                const int gm = m0 + r, gk = k0 + k;
+                const int gm = row_at(m0 + r, M, VEC && TA ? 4 : 1), gk = k0 + k;
                 // A vector never straddles an edge: its contiguous extent
                 // (k, or m when TA) is a multiple of 4.
                 const bool ok = !CHECKED || (gm < M && gk < kend);
@@ -316,7 +322,7 @@ __device__ __forceinline__ void mfma_gemm_tile(const GemmParams& p, int bid, int
             for (int j = 0; j < B_LD; ++j) {
                 int k, c;
                 b_coord(j, k, c);
-                const int gk = k0 + k, gn = n0 + c;
+                const int gk = k0 + k, gn = row_at(n0 + c, N, VEC && !TB ? 4 : 1);
                 const bool ok = !CHECKED || (gk < kend && gn < N);
                 if constexpr (VEC) {
                     rb4[j] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -385,8 +391,7 @@ __device__ __forceinline__ void mfma_gemm_tile(const GemmParams& p, int bid, int
         }
     };
 
-    const bool interior = m0 + BM <= M && n0 + BN <= N && (kend - kbeg) % BK == 0;
-    if (interior)
+    if ((kend - kbeg) % BK == 0)
         main_loop(std::false_type{});
     else
         main_loop(std::true_type{});
