@@ -85,13 +85,21 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
     // Row-major A: a half-wave reads 16 rows at two 4-float k offsets, so
     // rows 24 floats apart land on 16 distinct 8-bank slots.  Row-major B: a
     // half-wave reads two k rows 4 apart, which BN + 16 places 64 banks apart.
-    constexpr int SA  = TA ? BM + 4 : BK + 8;
-    constexpr int SB  = TB ? BK + 4 : BN + 16;
-    constexpr int A_ELEMS = TA ? BK * SA : BM * SA;
-    constexpr int B_ELEMS = TB ? BN * SB : BK * SB;
-    static_assert(TN % 4 == 0 && KS % 4 == 0, "128-bit operand reads");
     constexpr int A_LD = BM * BK / 4 / NT;
     constexpr int B_LD = BK * BN / 4 / NT;
+    // Column-major A with four staging vectors per thread (BK = 16): a
+    // thread loads 4 consecutive k of one 4-row run, which transposes in
+    // registers (fp32 elements are whole registers) into the k-contiguous
+    // layout of a row-major A, read with the same 128-bit operand reads.
+    // Other column-major tiles, and the split-k ones (whose registers the
+    // transpose overflows), store A k-major and read one k per read.
+    constexpr bool TAX = TA && A_LD == 4 && BK == 16 && SPLIT == kWhole;
+    constexpr bool A_KMAJ = TA && !TAX;
+    constexpr int SA  = A_KMAJ ? BM + 4 : BK + 8;
+    constexpr int SB  = TB ? BK + 4 : BN + 16;
+    constexpr int A_ELEMS = A_KMAJ ? BK * SA : BM * SA;
+    constexpr int B_ELEMS = TB ? BN * SB : BK * SB;
+    static_assert(TN % 4 == 0 && KS % 4 == 0, "128-bit operand reads");
     static_assert(A_LD >= 1 && B_LD >= 1 && BM * BK / 4 % NT == 0 && BK * BN / 4 % NT == 0, "staging");
 
     __shared__ __attribute__((aligned(16))) float As[2][A_ELEMS];
@@ -121,7 +129,14 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
     // threads along each matrix's contiguous dimension.
     auto a_coord = [&](int j, int& r, int& k) {
         const int idx = tid + j * NT;
-        if constexpr (TA) {
+        if constexpr (TAX) {
+            // Slot j: k = 4*(tid % 4) + j of rows 4*(tid / 4) .. +3.  The 8
+            // lanes of one LDS write group then cover 2 row runs x 4 k
+            // quarters: after the transpose each write hits 128 distinct
+            // bytes (rows 4 apart, SA = 24: 384 bytes; k quarters 16 bytes).
+            r = 4 * (tid >> 2);
+            k = 4 * (tid & 3) + j;
+        } else if constexpr (TA) {
             r = 4 * (idx % (BM / 4));
             k = idx / (BM / 4);
         } else {
@@ -145,7 +160,7 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
             c = 4 * (idx % (BN / 4));
         }
     };
-    auto a_lds = [&](int r, int k) { return TA ? k * SA + r : r * SA + k; };
+    auto a_lds = [&](int r, int k) { return A_KMAJ ? k * SA + r : r * SA + k; };
     auto b_lds = [&](int k, int c) { return TB ? c * SB + k : k * SB + c; };
 
     floatx4 ra[A_LD], rb[B_LD];
@@ -185,11 +200,21 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
             }
         };
         auto store_stage = [&](int buf) {
+            if constexpr (TAX) {
+                // ra[j] holds rows r .. r+3 at k = k0 + j: row r + i gets
+                // k0 .. k0+3 from element i of each.
+                int r, k0;
+                a_coord(0, r, k0);
 #pragma unroll
-            for (int j = 0; j < A_LD; ++j) {
-                int r, k;
-                a_coord(j, r, k);
-                *reinterpret_cast<floatx4*>(&As[buf][a_lds(r, k)]) = ra[j];
+                for (int i = 0; i < 4; ++i)
+                    *reinterpret_cast<floatx4*>(&As[buf][(r + i) * SA + k0]) = floatx4{ra[0][i], ra[1][i], ra[2][i], ra[3][i]};
+            } else {
+#pragma unroll
+                for (int j = 0; j < A_LD; ++j) {
+                    int r, k;
+                    a_coord(j, r, k);
+                    *reinterpret_cast<floatx4*>(&As[buf][a_lds(r, k)]) = ra[j];
+                }
             }
 #pragma unroll
             for (int j = 0; j < B_LD; ++j) {
@@ -206,7 +231,7 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
                 const int r = wrow + bi * 16 + j16;
 #pragma unroll
                 for (int q = 0; q < KS / 4; ++q) {
-                    if constexpr (TA) {
+                    if constexpr (A_KMAJ) {
 #pragma unroll
                         for (int t = 0; t < 4; ++t) av[bi][q][t] = As[buf][(g * KS + 4 * q + t) * SA + r];
                     } else {
@@ -268,8 +293,8 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
         // MFMAs before the barrier; the rest cover the next stage's operand
         // reads.  Measured on the 256x256 tile at 8192^3: 7/8 of the stage
         // 142.0 TFLOP/s, 1/2 141.5, 1/4 140.8.  A column-major A keeps 1/2:
-        // its split-k 256x256 instantiation spills 100 bytes per lane with
-        // 7/8 (36 with 1/2).
+        // with 7/8 its k-major reads spill registers, and its transposed
+        // staging runs at 120 TFLOP/s against 139 with 1/2.
         constexpr int FIRST = TA ? NM / 2 : NM * 7 / 8;
         floatx4 av[2][TM][KS / 4];
         float bv[2][KS][TN];
