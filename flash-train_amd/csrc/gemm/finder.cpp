@@ -91,8 +91,7 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
         // Too few waves cannot reach the HBM peak; about four per CU do
         // (measured with the one-pass kernel: 1024 waves over 256 CUs stream
         // 5.4-6.3 TB/s, 256 waves lose to split-k).
-        int threads = vi.threads;
-        if (vi.split == SplitKind::kNone) (void)gemvKernel(int(std::max<uint64_t>(s.m, 1)), false, threads);
+        const int threads = vi.split == SplitKind::kNone ? gemvPassThreads(int(std::max<uint64_t>(s.m, 1))) : vi.threads;
         const double wgs  = double(ceilDiv(std::max<uint64_t>(s.n, 1), uint64_t(vi.bn)) * splits);
         const double fill = std::min(1.0, wgs * (threads / 64) / (double(cus) * 4.0));
         return bytes / (kHbmBytesPerMicro * fill) + serial_us + launch;
@@ -141,7 +140,7 @@ uint32_t chooseSplits(Variant v, const GemmShape& s, int cus) {
 
 double estimateMicros(Variant v, const GemmShape& s, bool has_c, int cus) {
     const VariantInfo& vi = info(v);
-    if (vi.gemv && s.m > uint64_t(kGemvRows)) return std::numeric_limits<double>::infinity();
+    if (vi.gemv && s.m > uint64_t(vi.bm)) return std::numeric_limits<double>::infinity();
     const uint32_t splits = vi.split != SplitKind::kNone ? chooseSplits(v, s, cus) : 1;
     if (splits == 0) return std::numeric_limits<double>::infinity();
     return modelMicros(vi, s, has_c, cus, splits);

@@ -343,35 +343,33 @@ __global__ __launch_bounds__(256) void simt_gemm(WideParams p) {
 
 }  // namespace
 
-// Waves and steps in flight per row count, measured at n = k = 8192: one
-// row 8 waves x 2 steps (37.8 us), two and four rows 16 x 2 (38.9 / 38.8),
-// eight rows 8 x 2 (the configurations with more in flight, 8 x 4 and
-// 16 x 2, spill registers there).
-const void* gemvKernel(int m, bool ta, int& threads) {
-    const void* k = nullptr;
-    if (m <= 1) {
-        threads = 512;
-        k = ta ? reinterpret_cast<const void*>(&gemv_pass<8, 2, 1, true>) : reinterpret_cast<const void*>(&gemv_pass<8, 2, 1, false>);
-    } else if (m <= 2) {
-        threads = 1024;
-        k = ta ? reinterpret_cast<const void*>(&gemv_pass<16, 2, 2, true>) : reinterpret_cast<const void*>(&gemv_pass<16, 2, 2, false>);
-    } else if (m <= 4) {
-        threads = 1024;
-        k = ta ? reinterpret_cast<const void*>(&gemv_pass<16, 2, 4, true>) : reinterpret_cast<const void*>(&gemv_pass<16, 2, 4, false>);
-    } else {
-        threads = 512;
-        k = ta ? reinterpret_cast<const void*>(&gemv_pass<8, 2, 8, true>) : reinterpret_cast<const void*>(&gemv_pass<8, 2, 8, false>);
-    }
-    return k;
+// Waves and steps in flight per row count, measured at n = k = 8192 (fp32):
+// one row 8 waves x 2 steps (37.8 us), two and four rows 16 x 2 (38.9 /
+// 38.8), eight rows 8 x 2 (the configurations with more in flight, 8 x 4
+// and 16 x 2, spill registers there).  The 16-bit kernel uses the same.
+int gemvPassThreads(int m) { return m <= 1 || m > 4 ? 512 : 1024; }
+
+const void* gemvKernel(Variant v, int m, bool ta, int& threads) {
+    threads = gemvPassThreads(m);
+    if (v == Variant::kBf16Gemv || v == Variant::kFp16Gemv) return ta ? nullptr : gemvHalfKernel(v == Variant::kBf16Gemv, m);
+    if (m <= 1) return ta ? reinterpret_cast<const void*>(&gemv_pass<8, 2, 1, true>) : reinterpret_cast<const void*>(&gemv_pass<8, 2, 1, false>);
+    if (m <= 2) return ta ? reinterpret_cast<const void*>(&gemv_pass<16, 2, 2, true>) : reinterpret_cast<const void*>(&gemv_pass<16, 2, 2, false>);
+    if (m <= 4) return ta ? reinterpret_cast<const void*>(&gemv_pass<16, 2, 4, true>) : reinterpret_cast<const void*>(&gemv_pass<16, 2, 4, false>);
+    return ta ? reinterpret_cast<const void*>(&gemv_pass<8, 2, 8, true>) : reinterpret_cast<const void*>(&gemv_pass<8, 2, 8, false>);
 }
 
 const void* kernelFor(Variant v, bool ta, bool tb) {
+    if (info(v).gemv && info(v).split == SplitKind::kNone) {
+        if (tb) return nullptr;
+        int threads = 0;
+        return gemvKernel(v, kGemvRows, ta, threads);
+    }
     if (v >= Variant::kMfma16_256x256 && v <= Variant::kMfma16_256x64S) {
         using Fn                     = const void* (*)(int);
         static constexpr Fn table[4] = {mfma16KernelNN, mfma16KernelTN, mfma16KernelNT, mfma16KernelTT};
         return table[(ta ? 1 : 0) + (tb ? 2 : 0)](static_cast<int>(v) - static_cast<int>(Variant::kMfma16_256x256));
     }
-    if (v >= Variant::kBf16Mfma256x256 && v < Variant::kCount) {
+    if (v >= Variant::kBf16Mfma256x256 && v <= Variant::kFp16Mfma64x64U) {
         const int i    = static_cast<int>(v) - static_cast<int>(Variant::kBf16Mfma256x256);
         const int tile = i % kHalfTiles;
         using Fn       = const void* (*)(int);
@@ -382,10 +380,6 @@ const void* kernelFor(Variant v, bool ta, bool tb) {
     }
     if (ta || tb) {
         if (v == Variant::kSimt) return reinterpret_cast<const void*>(&simt_gemm);  // strides are runtime values
-        if (v == Variant::kGemv && !tb && ta) {
-            int threads = 0;
-            return gemvKernel(kGemvRows, true, threads);
-        }
         if (v == Variant::kGemvS && !tb && ta) return reinterpret_cast<const void*>(&gemv_splitk<true, true>);
         if (v == Variant::kGemvUS && !tb && ta) return reinterpret_cast<const void*>(&gemv_splitk<false, true>);
         if (!info(v).layouts) return nullptr;
@@ -399,10 +393,6 @@ const void* kernelFor(Variant v, bool ta, bool tb) {
         case Variant::kMfma64x256S: return reinterpret_cast<const void*>(&mfma_gemm<64, 256, 16, 1, 4, 3, 1, true, kPartial, false, false>);
         case Variant::kMfma256x64: return reinterpret_cast<const void*>(&mfma_gemm<256, 64, 16, 4, 1, 3, 1, true, kWhole, false, false>);
         case Variant::kMfma256x64S: return reinterpret_cast<const void*>(&mfma_gemm<256, 64, 16, 4, 1, 3, 1, true, kPartial, false, false>);
-        case Variant::kGemv: {
-            int threads = 0;
-            return gemvKernel(kGemvRows, false, threads);
-        }
         case Variant::kGemvS: return reinterpret_cast<const void*>(&gemv_splitk<true, false>);
         case Variant::kGemvUS: return reinterpret_cast<const void*>(&gemv_splitk<false, false>);
         case Variant::kSimt: return reinterpret_cast<const void*>(&simt_gemm);

@@ -158,7 +158,7 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
                 if (!vecAligned(p.port(i).memory()))
                     return Result(FTRAIN_STATUS_UNSUPPORTED, "a matrix address is not 16-byte aligned");
         }
-        if (info_->gemv && s.m > uint64_t(gemm::kGemvRows))
+        if (info_->gemv && s.m > uint64_t(info_->bm))
             return Result(FTRAIN_STATUS_UNSUPPORTED, "m exceeds the skinny-kernel row limit");
         if (info_->split == SplitKind::kPartial &&
             gemm::chooseSplits(v_, s, gemm::computeUnits(constraints.device())) == 0)
@@ -184,7 +184,8 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
         wide_ = WideParams{a, b, c, d, alpha, beta, s.m, s.n, s.k, a_rs, a_cs, b_rs, b_cs, g.ldc, g.ldd};
 
         int threads = info_->threads;
-        kernel_     = v_ == Variant::kGemv ? gemm::gemvKernel(int(s.m), g.ta, threads) : gemm::kernelFor(v_, g.ta, g.tb);
+        kernel_     = info_->gemv && info_->split == SplitKind::kNone ? gemm::gemvKernel(v_, int(s.m), g.ta, threads)
+                                                                  : gemm::kernelFor(v_, g.ta, g.tb);
         checkBlockSize(kernel_, threads, info_->name);
         block_  = dim3(threads);
         if (info_->simt) {

@@ -100,8 +100,13 @@ struct ReduceParams {
 // columns per workgroup.
 constexpr int kGemvRows = 8;
 constexpr int kGemvCols = 256;
-// Columns per workgroup of the one-pass skinny kernel (128 bytes of a b row).
+// Columns per workgroup of the one-pass skinny kernels (128 bytes of a b
+// row): fp32 and 16-bit inputs.
 constexpr int kGemvPassCols = 32;
+constexpr int kGemvHalfCols = 64;
+// Rows of a the 16-bit one-pass kernel takes (measured: it wins at one and
+// two rows, ties at four and loses at eight to the split-k 128x128 tile).
+constexpr int kGemvHalfRows = 2;
 
 enum class Variant : int {
     // v_mfma_f32_16x16x4_f32 256x256 tiles, 4 waves of 128x128 (one per
@@ -158,6 +163,9 @@ enum class Variant : int {
     kFp16Mfma128x128,
     kFp16Mfma128x128S,
     kFp16Mfma64x64U,
+    // One-pass skinny-m kernels (m <= 8, row-major b) for bf16 / fp16 inputs.
+    kBf16Gemv,
+    kFp16Gemv,
     kCount
 };
 
@@ -197,10 +205,13 @@ const VariantInfo& info(Variant v);
 // a column-major (tb) or row-major b; null when that layout is not
 // instantiated for the variant (see VariantInfo::layouts).
 const void* kernelFor(Variant v, bool ta = false, bool tb = false);
-// The one-pass skinny kernel (Variant::kGemv) for m rows of a (1..kGemvRows)
-// and a row-major (ta false) or column-major a; `threads` receives its
-// workgroup size.  b is row-major.
-const void* gemvKernel(int m, bool ta, int& threads);
+// The one-pass skinny kernels (Variant::kGemv, kBf16Gemv, kFp16Gemv) for m
+// rows of a (up to the variant's row limit) and a row-major (ta false) or,
+// fp32 only, column-major a; null otherwise.  `threads` receives the
+// workgroup size, gemvPassThreads(m).  b is row-major.
+int gemvPassThreads(int m);
+const void* gemvKernel(Variant v, int m, bool ta, int& threads);
+const void* gemvHalfKernel(bool bf16, int m);
 // Per-layout instantiations of the layout-capable MFMA variants (one HIP TU
 // each); null for other variants.
 const void* layoutKernelTN(Variant v);  // column-major a, row-major b

@@ -529,9 +529,10 @@ def test_zero_depth_needs_no_a_or_b(tlib, tops):
 # ------------------------------------------------------------------ Finder choices
 
 
-def rank(tlib, m, n, k, addr=FAKE, with_c=False, device=0):
+def rank(tlib, m, n, k, addr=FAKE, with_c=False, device=0, ab_type=c.FP32):
     views = (c.StorageView * 6)()
-    keep = [V([m, k], addr), V([k, n], addr), V([m, n], addr if with_c else None), V([m, n], addr)]
+    keep = [V([m, k], addr, numeric_type=ab_type), V([k, n], addr, numeric_type=ab_type),
+            V([m, n], addr if with_c else None), V([m, n], addr)]
     al, be = c.HostScalar(1.0), c.HostScalar(0.0)
     for i, v in enumerate(keep + [al.view, be.view]):
         views[i] = v.sv
@@ -570,6 +571,16 @@ def test_finder_choices_for_the_baseline_configs(tlib):
     # Odd sizes: no 128-bit variant applies.
     odd = rank(tlib, 127, 97, 33)
     assert odd and all(("Unaligned" in n) or n == "Fp32Gemm" for n in odd)
+
+
+def test_finder_choices_for_16_bit_skinny_m(tlib):
+    # bf16, MI355X (us): 1x8192x8192 Bf16Gemv 24.1 against the split-k 128x128 tile 34.3; 2 rows 25.3
+    # against 34.1; at 8 rows the one-pass kernel lost (92.7 against 35.7) and is limited to 2 rows.
+    for t in (c.BF16, c.FP16):
+        name = "Bf16Gemv" if t == c.BF16 else "Fp16Gemv"
+        assert rank(tlib, 1, 8192, 8192, ab_type=t)[0] == name
+        assert rank(tlib, 2, 8192, 8192, ab_type=t)[0] == name
+        assert name not in rank(tlib, 3, 8192, 8192, ab_type=t)
 
 
 def test_finder_respects_alignment_and_row_limits(tlib):
