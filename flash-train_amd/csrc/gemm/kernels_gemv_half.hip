@@ -27,8 +27,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_pass_half(HalfGemmParams p) {
     using u16      = unsigned short;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane >> 3, q = lane & 7;
     const int M = p.m, N = p.n, K = p.k;
-    const int col0              = blockIdx.x * kGemvHalfCols + 8 * q;
-    const bool col_ok           = col0 < N;  // n % 8 == 0: a run of 8 columns is all in or all out
+    // Columns past n (n % 8 == 0) and rows of a past m are read at a clamped
+    // index instead of behind a branch (which would give every load a block
+    // of its own); they feed only sums the final store skips.
+    const int col0              = min(blockIdx.x * kGemvHalfCols + 8 * q, N - 8);
     const u16* __restrict__ A   = static_cast<const u16*>(p.a);
     const u16* __restrict__ B   = static_cast<const u16*>(p.b);
     const size_t lda = p.lda, ldb = p.ldb;
@@ -44,16 +46,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_pass_half(HalfGemmParams p) {
     // (k % 8 == 0, so a step is whole or past the end).
     auto load = [&](int k0, u32x4 (&bv)[4], float (&av)[MR][4]) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            bv[t] = u32x4{0u, 0u, 0u, 0u};
-            if (col_ok) bv[t] = *reinterpret_cast<const u32x4*>(B + (size_t)(k0 + t) * ldb + col0);
-        }
+        for (int t = 0; t < 4; ++t) bv[t] = *reinterpret_cast<const u32x4*>(B + (size_t)(k0 + t) * ldb + col0);
 #pragma unroll
         for (int i = 0; i < MR; ++i) {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) av[i][t] = 0.f;
-            if (i >= M) continue;
-            const u32x2 v = *reinterpret_cast<const u32x2*>(A + (size_t)i * lda + k0);
+            const u32x2 v = *reinterpret_cast<const u32x2*>(A + (size_t)min(i, M - 1) * lda + k0);
 #pragma unroll
             for (int t = 0; t < 4; ++t) av[i][t] = to_float<BF16>(u16(v[t / 2] >> (16 * (t % 2))));
         }
