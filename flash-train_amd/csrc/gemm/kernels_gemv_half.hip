@@ -13,7 +13,8 @@ using hdev::u32x2;
 using hdev::u32x4;
 
 // m <= MR <= kGemvHalfRows, row-major a and b (16-byte aligned rows,
-// k % 8 == 0, n % 8 == 0; a column-major a would need m % 8 == 0).
+// k % 8 == 0, n % 8 == 0; a column-major a would need m % 8 == 0, more rows
+// than the kernel takes).
 // Workgroup x owns output columns [64x, 64x + 64) over all of k, so d is
 // written directly.  Lane (r = lane / 8, q = lane % 8) of wave w takes
 // columns 8q .. 8q+7 and, per step, the 4 consecutive k rows
@@ -118,7 +119,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_pass_half(HalfGemmParams p) {
 template <bool BF16>
 const void* pick(int m) {
     if (m <= 1) return reinterpret_cast<const void*>(&gemv_pass_half<BF16, 8, 2, 1>);
-    return reinterpret_cast<const void*>(&gemv_pass_half<BF16, 16, 2, 2>);
+    if (m <= 2) return reinterpret_cast<const void*>(&gemv_pass_half<BF16, 16, 2, 2>);
+    return reinterpret_cast<const void*>(&gemv_pass_half<BF16, 16, 2, 4>);
 }
 
 }  // namespace

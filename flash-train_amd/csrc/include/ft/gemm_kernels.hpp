@@ -104,9 +104,10 @@ constexpr int kGemvCols = 256;
 // row): fp32 and 16-bit inputs.
 constexpr int kGemvPassCols = 32;
 constexpr int kGemvHalfCols = 64;
-// Rows of a the 16-bit one-pass kernel takes (measured: it wins at one and
-// two rows, ties at four and loses at eight to the split-k 128x128 tile).
-constexpr int kGemvHalfRows = 2;
+// Rows of a the 16-bit one-pass kernel takes (measured at 8192^2 against the
+// split-k 128x128 tile: one, two and four rows 23.5 / 25.0 / 31.0 us against
+// 34.3-34.7; eight rows 38.3 against 35.7).
+constexpr int kGemvHalfRows = 4;
 
 enum class Variant : int {
     // v_mfma_f32_16x16x4_f32 256x256 tiles, 4 waves of 128x128 (one per
