@@ -620,10 +620,13 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                         const size_t di = (size_t)row * p.ldd + col;
                         float out       = alpha * acc[bi][bj0 + t][r];
                         if constexpr (HAS_C) out += beta * cv[HAS_C ? u & 1 : 0][t][r];
+                        // d is not read again here: non-temporal stores keep
+                        // the burst of a round's outputs from allocating in
+                        // L2 (bf16 8192^3: +1.7-2.4%).
                         if constexpr (HALF)
-                            static_cast<u16*>(p.d)[di] = from_float<BF16>(out);
+                            __builtin_nontemporal_store(from_float<BF16>(out), static_cast<u16*>(p.d) + di);
                         else
-                            static_cast<float*>(p.d)[di] = out;
+                            __builtin_nontemporal_store(out, static_cast<float*>(p.d) + di);
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
