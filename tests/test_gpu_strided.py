@@ -96,7 +96,7 @@ LAYOUTS = list(itertools.product((False, True), (False, True), (False, True)))
 
 
 @pytest.mark.parametrize("la,lb,lcd", LAYOUTS)
-@pytest.mark.parametrize("m,n,k,pad", [(256, 192, 160, 4), (129, 67, 37, 3), (64, 64, 1024, 0)])
+@pytest.mark.parametrize("m,n,k,pad", [(256, 192, 160, 4), (256, 192, 150, 4), (129, 67, 37, 3), (64, 64, 1024, 0)])
 def test_layouts_every_primitive(capi, ops, oracle, la, lb, lcd, m, n, k, pad):
     if pad == 0 and not (la or lb or lcd):
         pytest.skip("plain continuous layout is covered by test_gpu_gemm.py")
