@@ -27,12 +27,10 @@
 // Global -> LDS, per operand orientation:
 //   k-contiguous in memory (row-major a, column-major b): 16-byte loads of 8
 //     consecutive k, written to LDS as they are;
-//   row/column-contiguous (column-major a, row-major b), TR tiles: 16-byte
-//     loads of 8 consecutive m (or n) at one k, written as they are into a
-//     k-major tile, whose operands are then read with ds_read_b64_tr_b16;
-//   the same, other tiles: each thread loads an 8 x 8 block as 8 rows of 8
-//     consecutive m (or n) at consecutive k, transposes it in registers with
-//     16-bit shuffles (v_perm_b32), and writes 8 k-contiguous vectors.
+//   row/column-contiguous (column-major a, row-major b): 16-byte loads of 8
+//     consecutive m (or n) at one k, written as they are into a k-major
+//     tile, whose operands are then read with ds_read_b64_tr_b16 (TR);
+//   per-element tiles (any shape): one element per load, stored k-contiguous.
 // Consecutive threads walk each matrix's contiguous dimension, so the loads
 // stay coalesced for every orientation.
 #pragma once
@@ -81,21 +79,6 @@ __device__ __forceinline__ floatx16 mfma(u32x4 a, u32x4 b, floatx16 acc) {
                                                       acc, 0, 0, 0);
 }
 
-// Transposes an 8 x 8 block of 16-bit values held as 8 vectors (v[i] =
-// row i, elements 0..7) into w[j] = column j (elements v[0][j] .. v[7][j]).
-__device__ __forceinline__ void transpose8x8(const u32x4 (&v)[8], u32x4 (&w)[8]) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            // w[j] dword q = (v[2q][j], v[2q+1][j]): low half from row 2q.
-            // Element j of a row sits in dword j/2, low half when j is even.
-            // (The compiler turns each pair into one v_perm_b32.)
-            const unsigned int lo = v[2 * q][j / 2], hi = v[2 * q + 1][j / 2];
-            w[j][q] = (j & 1) ? (lo >> 16) | (hi & 0xFFFF0000u) : (lo & 0xFFFFu) | (hi << 16);
-        }
-}
-
 // Same XCD-aware tile order as the fp32 kernels: each XCD (workgroup id mod
 // 8) receives a contiguous range of tiles, walked in bands of 8 tile rows.
 __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -122,8 +105,7 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 // z of the workspace (dense m x n) for splitk_reduce.
 // ----------------------------------------------------------------------------
 // The tile body (see mfma_tile.hpp): tile `bid` of p's grid, split `z`.
-template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, int SPLIT, bool TA, bool TB,
-          bool TR = false>
+template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, int SPLIT, bool TA, bool TB>
 __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid, int z) {
     using u16           = unsigned short;
     constexpr int NT    = WM * WN * 64;
@@ -134,11 +116,11 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
     constexpr int STEPS = BK / 16;  // MFMA k-steps per stage
     constexpr int SK    = BK + 8;   // LDS row stride (elements)
     static_assert(TM >= 1 && TN >= 1 && BK % 16 == 0, "tile");
-    // TR: a transposed operand (column-major a, row-major b) is stored as it
-    // lies in memory, k-major ([BK][BM + 32] / [BK][BN + 32]), and read with
-    // transposing LDS reads; otherwise it is transposed in registers.
-    constexpr bool A_TR = TR && VEC && TA;
-    constexpr bool B_TR = TR && VEC && !TB;
+    // A transposed operand (column-major a, row-major b) of a 16-byte tile is
+    // stored as it lies in memory, k-major, and read with transposing LDS
+    // reads (TR); the per-element tile transposes while staging.
+    constexpr bool A_TR = VEC && TA;
+    constexpr bool B_TR = VEC && !TB;
     constexpr int A_LDS = A_TR ? (BM >= 256 ? BK * (BM + 32) + 128 : BK * BM) : BM * SK;
     constexpr int B_LDS = B_TR ? (BN >= 256 ? BK * (BN + 32) + 128 : BK * BN) : BN * SK;
 
@@ -183,18 +165,16 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
     auto a_at = [&](int gm, int gk) { return A + (TA ? (size_t)gk * lda + gm : (size_t)gm * lda + gk); };
     auto b_at = [&](int gk, int gn) { return B + (TB ? (size_t)gn * ldb + gk : (size_t)gk * ldb + gn); };
 
-    // Staging registers.  VEC, k-contiguous operand: ROWS*BK/8 vectors of 8 k;
-    // VEC, transposed operand: ROWS*BK/64 blocks of 8 x 8; scalar: ROWS*BK
+    // Staging registers.  VEC: ROWS*BK/8 vectors of 8 elements (8 k of a
+    // k-contiguous operand, 8 m or n of a transposed one); scalar: ROWS*BK
     // elements.  Threads beyond the count idle for that operand.
-    constexpr int A_VECS = VEC ? (TA && !A_TR ? BM * BK / 64 : BM * BK / 8) : 0;
-    constexpr int B_VECS = VEC ? (TB || B_TR ? BN * BK / 8 : BN * BK / 64) : 0;
+    constexpr int A_VECS = VEC ? BM * BK / 8 : 0;
+    constexpr int B_VECS = VEC ? BN * BK / 8 : 0;
     constexpr int A_PER  = VEC ? (A_VECS + NT - 1) / NT : BM * BK / NT;
     constexpr int B_PER  = VEC ? (B_VECS + NT - 1) / NT : BN * BK / NT;
-    constexpr int A_REGS = VEC && TA && !A_TR ? 8 : 1;  // vectors per staging slot
-    constexpr int B_REGS = VEC && !TB && !B_TR ? 8 : 1;
     static_assert(VEC || (BM * BK % NT == 0 && BN * BK % NT == 0), "scalar staging");
-    u32x4 ra[VEC ? A_PER : 1][A_REGS];
-    u32x4 rb[VEC ? B_PER : 1][B_REGS];
+    u32x4 ra[VEC ? A_PER : 1][1];
+    u32x4 rb[VEC ? B_PER : 1][1];
     u16 sa[VEC ? 1 : A_PER];
     u16 sb[VEC ? 1 : B_PER];
 
@@ -232,27 +212,11 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                         const int gm = row_at(m0 + r, M, 1), gk = k0 + kq;
                         ra[j][0] = zero4;
                         if (!CHECKED || (gm < M && gk < kend)) ra[j][0] = *reinterpret_cast<const u32x4*>(a_at(gm, gk));
-                    } else if constexpr (A_TR) {  // (k, 8 m) vectors along the contiguous m
+                    } else {  // (k, 8 m) vectors along the contiguous m
                         const int k = idx / (BM / 8), mq = 8 * (idx % (BM / 8));
                         const int gm = row_at(m0 + mq, M, 8), gk = k0 + k;
                         ra[j][0] = zero4;
                         if (!CHECKED || (gm < M && gk < kend)) ra[j][0] = *reinterpret_cast<const u32x4*>(a_at(gm, gk));
-                    } else {
-                        // 8 x 8 blocks: 8 consecutive m at k = kb..kb+7.  Consecutive
-                        // threads take consecutive k blocks of the same 8 rows, so
-                        // each group of 8 lanes writes one contiguous 128-byte run
-                        // of LDS (32 distinct banks) after the transpose; taking
-                        // consecutive row blocks instead put the 8 lanes' rows 288
-                        // dwords apart, an 8-way bank conflict on every write.
-                        const int kb = 8 * (idx % (BK / 8)), r = 8 * (idx / (BK / 8));
-                        const int gm = row_at(m0 + r, M, 8);
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) {
-                            const int gk = k0 + kb + i;
-                            ra[j][i]     = zero4;
-                            if (!CHECKED || (gm < M && gk < kend))
-                                ra[j][i] = *reinterpret_cast<const u32x4*>(a_at(gm, gk));
-                        }
                     }
                 }
 #pragma unroll
@@ -265,21 +229,11 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                         const int gn = row_at(n0 + c, N, 1), gk = k0 + kq;
                         rb[j][0] = zero4;
                         if (!CHECKED || (gn < N && gk < kend)) rb[j][0] = *reinterpret_cast<const u32x4*>(b_at(gk, gn));
-                    } else if constexpr (B_TR) {  // (k, 8 n) vectors along the contiguous n
+                    } else {  // (k, 8 n) vectors along the contiguous n
                         const int k = idx / (BN / 8), nq = 8 * (idx % (BN / 8));
                         const int gn = row_at(n0 + nq, N, 8), gk = k0 + k;
                         rb[j][0] = zero4;
                         if (!CHECKED || (gn < N && gk < kend)) rb[j][0] = *reinterpret_cast<const u32x4*>(b_at(gk, gn));
-                    } else {  // 8 x 8 blocks: 8 consecutive n at k = kb..kb+7 (thread order as for a)
-                        const int kb = 8 * (idx % (BK / 8)), c = 8 * (idx / (BK / 8));
-                        const int gn = row_at(n0 + c, N, 8);
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) {
-                            const int gk = k0 + kb + i;
-                            rb[j][i]     = zero4;
-                            if (!CHECKED || (gn < N && gk < kend))
-                                rb[j][i] = *reinterpret_cast<const u32x4*>(b_at(gk, gn));
-                        }
                     }
                 }
             } else {
@@ -311,15 +265,9 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                     if constexpr (!TA) {
                         const int r = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
                         *reinterpret_cast<u32x4*>(&As[buf][r * SK + kq]) = ra[j][0];
-                    } else if constexpr (A_TR) {
+                    } else {
                         const int k = idx / (BM / 8), mq = 8 * (idx % (BM / 8));
                         *reinterpret_cast<u32x4*>(&As[buf][tr_at(k, mq, BM)]) = ra[j][0];
-                    } else {
-                        const int kb = 8 * (idx % (BK / 8)), r = 8 * (idx / (BK / 8));
-                        u32x4 w[8];
-                        transpose8x8(ra[j], w);
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(&As[buf][(r + i) * SK + kb]) = w[i];
                     }
                 }
 #pragma unroll
@@ -330,15 +278,9 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                     if constexpr (TB) {
                         const int c = idx / (BK / 8), kq = 8 * (idx % (BK / 8));
                         *reinterpret_cast<u32x4*>(&Bs[buf][c * SK + kq]) = rb[j][0];
-                    } else if constexpr (B_TR) {
+                    } else {
                         const int k = idx / (BN / 8), nq = 8 * (idx % (BN / 8));
                         *reinterpret_cast<u32x4*>(&Bs[buf][tr_at(k, nq, BN)]) = rb[j][0];
-                    } else {
-                        const int kb = 8 * (idx % (BK / 8)), c = 8 * (idx / (BK / 8));
-                        u32x4 w[8];
-                        transpose8x8(rb[j], w);
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(&Bs[buf][(c + i) * SK + kb]) = w[i];
                     }
                 }
             } else {
@@ -418,13 +360,7 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                 __syncthreads();
             }
         } else {
-            // Two schedules.  When every operand is copied straight into LDS
-            // (row-major a with column-major b, or TR tiles), the staging is
-            // spread over all k-steps; otherwise the in-register transposes
-            // do not fit beside it in the register budget, and every LDS
-            // write and load stays in the last k-step.
-            constexpr bool SPREAD = (!TA && TB) || TR;
-            if constexpr (SPREAD) {
+            {
                 // Software pipeline.  Stage st computes from LDS buffer st&1
                 // while registers hold the global data of stage st+1.  The
                 // staging entries (A slots, then B slots) are split into STEPS
@@ -444,11 +380,9 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                 constexpr int TAIL  = NB >= 8 ? 4 : NB / 2;  // MFMAs left after the barrier
                 constexpr int ENT   = A_PER + B_PER;
                 constexpr int PART  = (ENT + STEPS - 1) / STEPS;
-                // Instructions per entry: 16-byte global loads and LDS writes.
-                constexpr int A_INS = TA && !A_TR ? 8 : 1;
-                constexpr int B_INS = TB || B_TR ? 1 : 8;
-                // Upper bound of one part's loads (or writes) per tail MFMA.
-                constexpr int PER_MFMA = (PART * (A_INS > B_INS ? A_INS : B_INS) + NB - TAIL - 1) / (NB - TAIL);
+                // Upper bound of one part's 16-byte loads (or LDS writes) per
+                // tail MFMA.
+                constexpr int PER_MFMA = (PART + NB - TAIL - 1) / (NB - TAIL);
                 u32x4 opa[2][TM], opb[2][TN];
                 auto clamp_k0 = [&](int stage) { return kbeg + min(stage, nst - 1) * BK; };
                 if (nst > 0) {
@@ -492,64 +426,6 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
                             __builtin_amdgcn_sched_barrier(0);
                         }
                     }
-                }
-            } else {
-                // Software pipeline.  Stage st computes from LDS buffer st&1
-                // while registers hold the global data of stage st+1:
-                //   steps 0..STEPS-2: each step's MFMAs run while the operands
-                //     of the next step are read (two operand register sets);
-                //   last step: its first MFMAs run while stage st+1 is written
-                //     to the other buffer and the global loads of stage st+2 are
-                //     issued; then the barrier (stage st+1 visible, and every
-                //     read of buffer st&1 done before stage st+1 overwrites it
-                //     with stage st+2); then the operands of stage st+1's first
-                //     step are read under the last few MFMAs.
-                // Past the last stage the loads re-read the final stage (no
-                // branch in the loop body) and the extra LDS writes land in a
-                // buffer nobody reads again.
-                static_assert(STEPS % 2 == 0, "operand register sets alternate by step");
-                constexpr int NB   = TM * TN;
-                constexpr int TAIL = NB >= 8 ? 4 : NB / 2;  // MFMAs left after the barrier
-                u32x4 opa[2][TM], opb[2][TN];
-                auto clamp_k0 = [&](int stage) { return kbeg + min(stage, nst - 1) * BK; };
-                if (nst > 0) {
-                    load_stage(kbeg);
-                    store_stage(0);
-                    load_stage(clamp_k0(1));
-                }
-                __syncthreads();
-                if (nst > 0) read_ops(0, 0, opa[0], opb[0]);
-                for (int st = 0; st < nst; ++st) {
-                    const int cur = st & 1;
-                    // sched_barrier(0) fences keep each phase where it is
-                    // written: the compiler would otherwise sink every operand
-                    // read next to its MFMA and wait for it there.
-    #pragma unroll
-                    for (int s = 0; s + 1 < STEPS; ++s) {
-                        read_ops(cur, s + 1, opa[(s + 1) & 1], opb[(s + 1) & 1]);
-                        __builtin_amdgcn_sched_barrier(0);
-                        mfmas(opa[s & 1], opb[s & 1], 0, NB);
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-                    constexpr int L = (STEPS - 1) & 1;
-                    store_stage(cur ^ 1);
-                    load_stage(clamp_k0(st + 2));
-                    mfmas(opa[L], opb[L], 0, NB - TAIL);
-                    // Spread the LDS writes and global loads over these MFMAs.
-                    constexpr int WR = (VEC ? (A_REGS * A_PER) + (B_REGS * B_PER) : 0);
-                    constexpr int PER = (WR + NB - TAIL - 1) / (NB - TAIL);
-    #pragma unroll
-                    for (int i = 0; i < NB - TAIL; ++i) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
-                        __builtin_amdgcn_sched_group_barrier(0x200, PER, 0);  // DS write
-                        __builtin_amdgcn_sched_group_barrier(0x020, PER, 0);  // VMEM read
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-                    __syncthreads();
-                    read_ops(cur ^ 1, 0, opa[0], opb[0]);
-                    __builtin_amdgcn_sched_barrier(0);
-                    mfmas(opa[L], opb[L], NB - TAIL, NB);
-                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
         }
@@ -646,10 +522,9 @@ __device__ __forceinline__ void half_gemm_tile(const HalfGemmParams& p, int bid,
     }
 }
 
-template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, int SPLIT, bool TA, bool TB,
-          bool TR = false>
+template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, int SPLIT, bool TA, bool TB>
 __global__ __launch_bounds__(WM* WN * 64, MINB) void half_gemm(HalfGemmParams p) {
-    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, SPLIT, TA, TB, TR>(p, blockIdx.x, blockIdx.z);
+    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, SPLIT, TA, TB>(p, blockIdx.x, blockIdx.z);
 }
 
 // Grouped GEMM over a device table of per-group parameters (see
@@ -666,8 +541,7 @@ __device__ __forceinline__ int find_group(const int32_t* __restrict__ start, int
     return lo;
 }
 
-template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, bool TA, bool TB,
-          bool TR = false>
+template <bool BF16, int BM, int BN, int BK, int WM, int WN, int MINB, bool VEC, bool TA, bool TB>
 __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_half_gemm(GroupedHalfArgs g) {
     const int bid = blockIdx.x;
     const int grp = find_group(g.tile_start, g.groups, bid);
@@ -676,13 +550,13 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_half_gemm(GroupedHa
     // hardware id's XCD (id mod 8); ids past the group's tiles are padding.
     const int local = bid - g.tile_start[grp];
     if (local >= p.tiles_m * p.tiles_n) return;
-    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, kWhole, TA, TB, TR>(p, local, 0);
+    half_gemm_tile<BF16, BM, BN, BK, WM, WN, MINB, VEC, kWhole, TA, TB>(p, local, 0);
 }
 
 // The 256x256 tile, every operand orientation: 8 waves of 128x64 (two per
 // SIMD), transposed operands stored k-major and read with transposing LDS
 // reads (TR), staging spread over the k-steps.  Results are bit-identical to
-// transposing in registers (same MFMA sequence).  Measured bf16, TFLOP/s at
+// the 8x8 in-register transposes this replaced (same MFMA sequence).  Measured bf16, TFLOP/s at
 // 8192^3 / 4096^3, TR against the in-register transposes with their best
 // wave counts: row-major a with row-major b 1221 / 1128 against 1079 / 955;
 // column-major a with row-major b 1216 / 1126 against 974 / 789; both
@@ -692,8 +566,7 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_half_gemm(GroupedHa
 // row-major b 571 / 921 against 441 / 736, column-major a with row-major b
 // 565 / 875 against 287 / 507, both column-major 577 / 880 against 454 / 735.
 struct Wide {
-    static constexpr int WN      = 4;
-    static constexpr bool TR     = true;
+    static constexpr int WN = 4;
 };
 
 // The half-precision tiles (index as in kHalfTiles) for one input type and
@@ -704,11 +577,11 @@ const void* halfKernel(int tile) {
         case 0: {
             using W = Wide;
             return reinterpret_cast<const void*>(
-                &half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, kWhole, TA, TB, W::TR>);
+                &half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, kWhole, TA, TB>);
         }
-        case 1: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kWhole, TA, TB, true>);
+        case 1: return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kWhole, TA, TB>);
         case 2:
-            return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kPartial, TA, TB, true>);
+            return reinterpret_cast<const void*>(&half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, kPartial, TA, TB>);
         case 3: return reinterpret_cast<const void*>(&half_gemm<BF16, 64, 64, 32, 2, 2, 2, false, kWhole, TA, TB>);
         default: return nullptr;
     }
@@ -720,12 +593,12 @@ template <bool BF16, bool TA, bool TB>
 const void* groupedHalfKernel(int which) {
     switch (which) {
         case 0:
-            return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, TA, TB, true>);
+            return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 128, 128, 64, 2, 2, 2, true, TA, TB>);
         case 1: return reinterpret_cast<const void*>(&grouped_half_gemm<BF16, 64, 64, 32, 2, 2, 2, false, TA, TB>);
         case 2: {
             using W = Wide;
             return reinterpret_cast<const void*>(
-                &grouped_half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, TA, TB, W::TR>);
+                &grouped_half_gemm<BF16, 256, 256, 64, 2, W::WN, 1, true, TA, TB>);
         }
         default: return nullptr;
     }
