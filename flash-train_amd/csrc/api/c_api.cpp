@@ -3,7 +3,7 @@
 // implementations src/api/{common,pattern,ops_args,plan,gemm}_api.cpp).
 //
 // Each entry point runs its body through `guarded`, which maps exceptions to
-// status codes (Exception -> its status, bad_alloc -> OUT_OF_MEMORY, any
+// status codes (Failure -> its status, bad_alloc -> OUT_OF_MEMORY, any
 // other exception -> INTERNAL_ERROR) and records the status and message as
 // the thread's last result (reference src/include/flash_train/api.hpp:37-62).
 #include <algorithm>
@@ -27,7 +27,7 @@ Result& lastResult() noexcept {
 
 namespace {
 
-[[noreturn]] void invalid(const char* message) { throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "%s", message); }
+[[noreturn]] void invalid(const char* message) { raise(FTRAIN_STATUS_INVALID_ARGUMENT, "%s", message); }
 
 template <typename T>
 void requireNonNull(const T* p, const char* message) {
@@ -41,8 +41,8 @@ OpNode gemmNode(OperationKind kind, uint64_t a, uint64_t b, uint64_t c, uint64_t
 template <typename Id>
 FTrainStatus addOperand(FTrainPattern pattern, Id* out, OperandKind kind, const char* fn) {
     return guarded([&] {
-        if (pattern == nullptr) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: pattern must not be null", fn);
-        if (out == nullptr) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: output must not be null", fn);
+        if (pattern == nullptr) raise(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: pattern must not be null", fn);
+        if (out == nullptr) raise(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: output must not be null", fn);
         *out = Id{pattern->builder.addOperand(kind)};
     });
 }
@@ -51,8 +51,8 @@ template <typename Id>
 FTrainStatus addGemmLike(FTrainPattern pattern, Id* op, OperationKind kind, uint64_t a, uint64_t b, uint64_t c,
                          uint64_t d, uint64_t alpha, uint64_t beta, const char* fn) {
     return guarded([&] {
-        if (pattern == nullptr) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: pattern must not be null", fn);
-        if (op == nullptr) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: op output must not be null", fn);
+        if (pattern == nullptr) raise(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: pattern must not be null", fn);
+        if (op == nullptr) raise(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: op output must not be null", fn);
         *op = Id{pattern->builder.addOperation(gemmNode(kind, a, b, c, d, alpha, beta))};
     });
 }
@@ -60,9 +60,9 @@ FTrainStatus addGemmLike(FTrainPattern pattern, Id* op, OperationKind kind, uint
 FTrainStatus setOperation(FTrainArgs args, uint64_t op, OperationKind kind, FTrainNumericType compute_type,
                           const char* fn) {
     return guarded([&] {
-        if (args == nullptr) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: args handle must not be null", fn);
+        if (args == nullptr) raise(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: args handle must not be null", fn);
         if (compute_type == FTRAIN_NUMERIC_TYPE_INVALID || compute_type >= FTRAIN_NUMERIC_TYPE_COUNT)
-            throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: compute_type %u is invalid", fn,
+            raise(FTRAIN_STATUS_INVALID_ARGUMENT, "%s: compute_type %u is invalid", fn,
                             unsigned(compute_type));
         args->args.setOperation(op, OperationAttributes{kind, compute_type});
     });
@@ -224,7 +224,7 @@ FTrainStatus ftrainOpsCreate(FTrainOps* ops, FTrainPattern pattern) {
         const Pattern user = pattern->builder.build();
         const auto engine  = globalHandle().find(user.key());
         if (!engine)
-            throw Exception(FTRAIN_STATUS_UNSUPPORTED,
+            raise(FTRAIN_STATUS_UNSUPPORTED,
                             "ftrainOpsCreate: PatternBuilder does not match any registered OpsEngine");
         *ops = new FTrainOpsStruct{Ops(user, engine->pattern())};
     });
@@ -267,7 +267,7 @@ FTrainStatus ftrainArgsSetTensorList(FTrainArgs args, FTrainTensorListId tensor_
     return guarded([&] {
         requireNonNull(args, "ftrainArgsSetTensorList: args handle must not be null");
         if (storage_views == nullptr && num_storage_views != 0)
-            throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT,
+            raise(FTRAIN_STATUS_INVALID_ARGUMENT,
                             "ftrainArgsSetTensorList: storage_views must not be null when num_storage_views is %u",
                             num_storage_views);
         TensorList list;
@@ -322,7 +322,7 @@ FTrainStatus ftrainPlanCreate(FTrainPlan* plan, FTrainArgs args) {
         requireNonNull(plan, "ftrainPlanCreate: plan output must not be null");
         requireNonNull(args, "ftrainPlanCreate: args handle must not be null");
         const auto engine = globalHandle().find(args->args.key());
-        if (!engine) throw Exception(FTRAIN_STATUS_INTERNAL_ERROR, "OpsEngine registered for Args is unavailable");
+        if (!engine) raise(FTRAIN_STATUS_INTERNAL_ERROR, "OpsEngine registered for Args is unavailable");
         *plan = new FTrainPlanStruct{engine->createPlan(args->args)};
     });
 }

@@ -34,9 +34,9 @@ const GemmEngine& gemmEngine() {
 // selection and configuration).
 FTRAIN_TESTING_API FTrainStatus ftrainTestingPlanCreateOnDevice(FTrainPlan* plan, FTrainArgs args, int32_t device) {
     return guarded([&] {
-        if (plan == nullptr || args == nullptr) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "null argument");
+        if (plan == nullptr || args == nullptr) raise(FTRAIN_STATUS_INVALID_ARGUMENT, "null argument");
         const auto engine = globalHandle().find(args->args.key());
-        if (!engine) throw Exception(FTRAIN_STATUS_INTERNAL_ERROR, "OpsEngine registered for Args is unavailable");
+        if (!engine) raise(FTRAIN_STATUS_INTERNAL_ERROR, "OpsEngine registered for Args is unavailable");
         *plan = new FTrainPlanStruct{Plan(engine->createPrimitives(args->args, Constraints(device)), device)};
     });
 }
@@ -117,3 +117,15 @@ FTRAIN_TESTING_API void ftrainTestingParseNameList(const char* value, char* out,
 }
 
 FTRAIN_TESTING_API bool ftrainTestingParseSwitch(const char* value) { return parseSwitch(value); }
+
+// Raises a failure whose message is `length` repetitions of 'x' (formatted
+// when `formatted`, literal otherwise) through the C boundary, so the
+// last-message capacity can be checked.
+FTRAIN_TESTING_API FTrainStatus ftrainTestingFailWithLength(FTrainStatus status, size_t length, bool formatted) {
+    return guarded([&] {
+        const std::string text(length, 'x');
+        if (formatted) raise(status, "%s", text.c_str());
+        Result r(status, text.c_str());
+        throw Failure(r);
+    });
+}

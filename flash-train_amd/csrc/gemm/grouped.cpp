@@ -27,11 +27,11 @@ const char* groupName(int i) {
 // Values of a rank-one descriptor array of `groups` integers in host memory.
 std::vector<int64_t> readIndexArray(const StorageView& v, uint32_t groups, const char* operand, const char* what) {
     if (!v.isHost())
-        throw Exception(FTRAIN_STATUS_UNSUPPORTED, "grouped %s: %s must be in host memory", operand, what);
+        raise(FTRAIN_STATUS_UNSUPPORTED, "grouped %s: %s must be in host memory", operand, what);
     std::vector<int64_t> out(groups);
     if (groups == 0) return out;
     if (v.memory() == nullptr)
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped %s: %s memory is null", operand, what);
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped %s: %s memory is null", operand, what);
     const void* m = v.memory();
     for (uint32_t g = 0; g < groups; ++g) {
         switch (v.numericType()) {
@@ -41,13 +41,13 @@ std::vector<int64_t> readIndexArray(const StorageView& v, uint32_t groups, const
             case FTRAIN_NUMERIC_TYPE_UINT64: {
                 const uint64_t x = static_cast<const uint64_t*>(m)[g];
                 if (x > static_cast<uint64_t>(std::numeric_limits<int64_t>::max()))
-                    throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped %s: %s[%u] is out of range", operand,
+                    raise(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped %s: %s[%u] is out of range", operand,
                                     what, g);
                 out[g] = static_cast<int64_t>(x);
                 break;
             }
             default:
-                throw Exception(FTRAIN_STATUS_UNSUPPORTED, "grouped %s: %s must hold int32, uint32, int64 or uint64",
+                raise(FTRAIN_STATUS_UNSUPPORTED, "grouped %s: %s must hold int32, uint32, int64 or uint64",
                                 operand, what);
         }
     }
@@ -96,10 +96,10 @@ GroupOperand expandGrouped(const GroupedTensor& gt, int which) {
     const char* name     = groupName(which);
     const StorageView& v = gt.data();
     if (v.rank() != 2)
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped Gemm operand %s needs rank-two data, got rank %zu",
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped Gemm operand %s needs rank-two data, got rank %zu",
                         name, v.rank());
     if (v.isHost())
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped Gemm operand %s must be in device memory", name);
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped Gemm operand %s must be in device memory", name);
     const uint32_t G = gt.numGroups();
     std::vector<int64_t> rows(G, v.dims()[0]), cols(G, v.dims()[1]);
     if (!gt.dimSizes().empty()) {
@@ -108,7 +108,7 @@ GroupOperand expandGrouped(const GroupedTensor& gt, int which) {
     }
     for (uint32_t g = 0; g < G; ++g)
         if (rows[g] < 0 || cols[g] < 0)
-            throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped %s: group %u has a negative size", name, g);
+            raise(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped %s: group %u has a negative size", name, g);
     std::vector<int64_t> s0(G), s1(G, 1);
     if (!gt.strides().empty()) {
         s0 = readIndexArray(gt.strides()[0], G, name, "strides[0]");
@@ -127,7 +127,7 @@ GroupOperand expandGrouped(const GroupedTensor& gt, int which) {
         for (uint32_t g = 0; g < G; ++g) {
             off[g] = run;
             if (rows[g] != 0 && cols[g] > (max_off - run) / rows[g])
-                throw Exception(FTRAIN_STATUS_OVERFLOW, "grouped %s: packed group offsets overflow", name);
+                raise(FTRAIN_STATUS_OVERFLOW, "grouped %s: packed group offsets overflow", name);
             run += rows[g] * cols[g];
         }
     }
@@ -136,19 +136,19 @@ GroupOperand expandGrouped(const GroupedTensor& gt, int which) {
     out.groups.resize(G);
     const size_t eb = elementBytes(out.type);
     for (uint32_t g = 0; g < G; ++g) {
-        if (off[g] < 0) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped %s: offsets[%u] is negative", name, g);
+        if (off[g] < 0) raise(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped %s: offsets[%u] is negative", name, g);
         if (off[g] >= max_off)
-            throw Exception(FTRAIN_STATUS_OVERFLOW, "grouped %s: offsets[%u] overflows the address range", name, g);
+            raise(FTRAIN_STATUS_OVERFLOW, "grouped %s: offsets[%u] overflows the address range", name, g);
         GroupMatrix& m = out.groups[g];
         m.rows = rows[g];
         m.cols = cols[g];
         m.memory = v.memory() == nullptr ? nullptr : static_cast<const char*>(v.memory()) + static_cast<size_t>(off[g]) * eb;
         if (const char* why = groupLayout(rows[g], cols[g], s0[g], s1[g], m.layout))
-            throw Exception(FTRAIN_STATUS_UNSUPPORTED, "grouped %s, group %u: %s", name, g, why);
+            raise(FTRAIN_STATUS_UNSUPPORTED, "grouped %s, group %u: %s", name, g, why);
         // The group's last element: offset plus its (already bounded) extent.
         const int64_t extent = (rows[g] <= 1 ? 0 : (rows[g] - 1) * s0[g]) + (cols[g] <= 1 ? 0 : (cols[g] - 1) * s1[g]);
         if (extent > max_off - off[g])
-            throw Exception(FTRAIN_STATUS_OVERFLOW, "grouped %s, group %u: offset plus extent overflows the address range",
+            raise(FTRAIN_STATUS_OVERFLOW, "grouped %s, group %u: offset plus extent overflows the address range",
                             name, g);
     }
     return out;
@@ -161,20 +161,20 @@ GroupOperand expandList(const TensorList& tl, int which) {
     for (size_t g = 0; g < tl.views.size(); ++g) {
         const StorageView& v = tl.views[g];
         if (v.rank() != 2)
-            throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm TensorList %s[%zu] must be rank two, got rank %zu",
+            raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm TensorList %s[%zu] must be rank two, got rank %zu",
                             name, g, v.rank());
         if (v.isHost())
-            throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm TensorList %s[%zu] must be in device memory", name, g);
+            raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm TensorList %s[%zu] must be in device memory", name, g);
         if (g == 0)
             out.type = v.numericType();
         else if (v.numericType() != out.type)
-            throw Exception(FTRAIN_STATUS_UNSUPPORTED, "Gemm TensorList %s elements differ in numeric type", name);
+            raise(FTRAIN_STATUS_UNSUPPORTED, "Gemm TensorList %s elements differ in numeric type", name);
         GroupMatrix& m = out.groups[g];
         m.rows         = v.dims()[0];
         m.cols         = v.dims()[1];
         m.memory       = v.memory();
         if (const char* why = matrixLayout(v, m.layout))
-            throw Exception(FTRAIN_STATUS_UNSUPPORTED, "Gemm TensorList %s[%zu]: %s", name, g, why);
+            raise(FTRAIN_STATUS_UNSUPPORTED, "Gemm TensorList %s[%zu]: %s", name, g, why);
     }
     return out;
 }
@@ -182,7 +182,7 @@ GroupOperand expandList(const TensorList& tl, int which) {
 GroupOperand expand(const OperandValue& value, int which) {
     if (const auto* gt = std::get_if<GroupedTensor>(&value)) return expandGrouped(*gt, which);
     if (const auto* tl = std::get_if<TensorList>(&value)) return expandList(*tl, which);
-    throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped Gemm operand %s has the wrong storage family",
+    raise(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped Gemm operand %s has the wrong storage family",
                     groupName(which));
 }
 
@@ -197,9 +197,9 @@ GroupedGemmProblem::GroupedGemmProblem(GroupedKind kind, const OperandValue& a, 
                                        FTrainNumericType compute_type)
     : kind_(kind), alpha_(std::move(alpha)), beta_(std::move(beta)), compute_type_(compute_type) {
     if (alpha_.view.rank() != 0 || beta_.view.rank() != 0)
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm requires scalar alpha and beta Tensors");
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm requires scalar alpha and beta Tensors");
     if (!alpha_.view.isHost() || !beta_.view.isHost())
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm requires alpha and beta in host memory");
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm requires alpha and beta in host memory");
     a_      = expand(a, 0);
     b_      = expand(b, 1);
     c_      = expand(c, 2);
@@ -208,24 +208,24 @@ GroupedGemmProblem::GroupedGemmProblem(GroupedKind kind, const OperandValue& a, 
     const GroupOperand* ops[4] = {&a_, &b_, &c_, &d_};
     for (int i = 0; i < 4; ++i)
         if (ops[i]->groups.size() != groups_)
-            throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped Gemm operand %s has %zu groups, d has %u",
+            raise(FTRAIN_STATUS_INVALID_ARGUMENT, "grouped Gemm operand %s has %zu groups, d has %u",
                             groupName(i), ops[i]->groups.size(), groups_);
     const bool has_c = !nullOperand(c_);
     for (uint32_t g = 0; g < groups_; ++g) {
         const GroupMatrix &ma = a_.groups[g], &mb = b_.groups[g], &mc = c_.groups[g], &md = d_.groups[g];
         if (ma.cols != mb.rows)
-            throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "group %u: a column count %lld does not match b row count %lld",
+            raise(FTRAIN_STATUS_INVALID_ARGUMENT, "group %u: a column count %lld does not match b row count %lld",
                             g, static_cast<long long>(ma.cols), static_cast<long long>(mb.rows));
         if (md.rows != ma.rows || md.cols != mb.cols)
-            throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "group %u: d must be m-by-n", g);
+            raise(FTRAIN_STATUS_INVALID_ARGUMENT, "group %u: d must be m-by-n", g);
         if (has_c && mc.memory != nullptr && (mc.rows != md.rows || mc.cols != md.cols))
-            throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "group %u: c must be m-by-n", g);
+            raise(FTRAIN_STATUS_INVALID_ARGUMENT, "group %u: c must be m-by-n", g);
         constexpr uint64_t max_elems = std::numeric_limits<uint64_t>::max() / sizeof(double);
         const auto over          = [](int64_t x, int64_t y) {
             return y != 0 && static_cast<uint64_t>(x) > max_elems / static_cast<uint64_t>(y);
         };
         if (over(ma.rows, ma.cols) || over(mb.rows, mb.cols) || over(md.rows, md.cols))
-            throw Exception(FTRAIN_STATUS_OVERFLOW, "group %u: matrix byte size overflows uint64_t", g);
+            raise(FTRAIN_STATUS_OVERFLOW, "group %u: matrix byte size overflows uint64_t", g);
     }
 }
 
@@ -301,7 +301,7 @@ uint64_t ceilDiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
 void check(hipError_t e, const char* what) {
     if (e != hipSuccess)
-        throw Exception(FTRAIN_STATUS_INTERNAL_ERROR, "%s launch failed: %s", what, hipGetErrorString(e));
+        raise(FTRAIN_STATUS_INTERNAL_ERROR, "%s launch failed: %s", what, hipGetErrorString(e));
 }
 
 class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
@@ -376,7 +376,7 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
         for (uint32_t g = 0; g < p.groups(); ++g) {
             if (p.emptyOutput(g)) continue;
             GemmLaunch l;
-            if (const char* why = p.launch(g, l)) throw Exception(FTRAIN_STATUS_UNSUPPORTED, "%s", why);
+            if (const char* why = p.launch(g, l)) raise(FTRAIN_STATUS_UNSUPPORTED, "%s", why);
             // Groups are launched per operand orientation (one kernel
             // instantiation each); a degenerate matrix may read as either.
             Bucket& bk       = buckets_[(l.ta ? 1 : 0) + (l.tb ? 2 : 0)];
@@ -425,14 +425,14 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
             hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
             check(hipStreamIsCapturing(r.stream, &capture), v_->name);
             if (capture != hipStreamCaptureStatusNone)
-                throw Exception(FTRAIN_STATUS_UNSUPPORTED,
+                raise(FTRAIN_STATUS_UNSUPPORTED,
                                 "%s: the first execution of a grouped Plan uploads its parameter table and cannot be "
                                 "captured; execute the Plan once before capturing it",
                                 v_->name);
             void* buf = nullptr;
             if (hipMalloc(&buf, total) != hipSuccess) {
                 (void)hipGetLastError();
-                throw Exception(FTRAIN_STATUS_OUT_OF_MEMORY, "%s: device parameter table of %zu bytes", v_->name, total);
+                raise(FTRAIN_STATUS_OUT_OF_MEMORY, "%s: device parameter table of %zu bytes", v_->name, total);
             }
             std::shared_ptr<void> table(buf, [](void* q) { (void)hipFree(q); });
             for (const Bucket& bk : buckets_) {

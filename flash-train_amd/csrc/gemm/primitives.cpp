@@ -89,7 +89,7 @@ void checkBlockSize(const void* kernel, int threads, const char* name) {
         return;
     }
     if (attr.maxThreadsPerBlock != threads)
-        throw Exception(FTRAIN_STATUS_INTERNAL_ERROR, "%s: workgroup size %d does not match the kernel's launch bounds %d",
+        raise(FTRAIN_STATUS_INTERNAL_ERROR, "%s: workgroup size %d does not match the kernel's launch bounds %d",
                         name, threads, attr.maxThreadsPerBlock);
 }
 
@@ -107,7 +107,7 @@ bool capturing(hipStream_t stream) {
 
 void check(hipError_t e, const char* what) {
     if (e != hipSuccess)
-        throw Exception(FTRAIN_STATUS_INTERNAL_ERROR, "%s launch failed: %s", what, hipGetErrorString(e));
+        raise(FTRAIN_STATUS_INTERNAL_ERROR, "%s launch failed: %s", what, hipGetErrorString(e));
 }
 
 class GemmPrimitive final : public Primitive<GemmProblem> {
@@ -171,7 +171,7 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
         empty_ = p.emptyOutput();
         if (empty_) return;
         GemmLaunch g;
-        if (const char* why = p.launch(g)) throw Exception(FTRAIN_STATUS_UNSUPPORTED, "%s", why);
+        if (const char* why = p.launch(g)) raise(FTRAIN_STATUS_UNSUPPORTED, "%s", why);
         const GemmShape s = g.shape;
         const float alpha = *static_cast<const float*>(p.alpha().memory());
         const float beta  = *static_cast<const float*>(p.beta().memory());
@@ -265,7 +265,7 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
                         void* q = nullptr;
                         if (hipMalloc(&q, partial_bytes_) != hipSuccess) {
                             (void)hipGetLastError();
-                            throw Exception(FTRAIN_STATUS_OUT_OF_MEMORY, "%s: split-k buffer of %llu bytes",
+                            raise(FTRAIN_STATUS_OUT_OF_MEMORY, "%s: split-k buffer of %llu bytes",
                                             info_->name, static_cast<unsigned long long>(partial_bytes_));
                         }
                         owned_.reset(q, [](void* x) { (void)hipFree(x); });

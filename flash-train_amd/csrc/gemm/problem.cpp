@@ -13,25 +13,25 @@ GemmProblem::GemmProblem(Tensor a, Tensor b, Tensor c, Tensor d, Tensor alpha, T
     : a_(std::move(a)), b_(std::move(b)), c_(std::move(c)), d_(std::move(d)), alpha_(std::move(alpha)),
       beta_(std::move(beta)), compute_type_(compute_type) {
     if (a_.view.rank() != 2 || b_.view.rank() != 2 || c_.view.rank() != 2 || d_.view.rank() != 2)
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm requires rank-two a, b, c, and d Tensors");
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm requires rank-two a, b, c, and d Tensors");
     if (alpha_.view.rank() != 0 || beta_.view.rank() != 0)
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm requires scalar alpha and beta Tensors");
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm requires scalar alpha and beta Tensors");
     if (a_.view.isHost() || b_.view.isHost() || c_.view.isHost() || d_.view.isHost())
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm requires a, b, c, and d in device memory");
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm requires a, b, c, and d in device memory");
     if (!alpha_.view.isHost() || !beta_.view.isHost())
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm requires alpha and beta in host memory");
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm requires alpha and beta in host memory");
     if (a_.view.dims()[1] != b_.view.dims()[0])
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm a column count %lld does not match b row count %lld",
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm a column count %lld does not match b row count %lld",
                         static_cast<long long>(a_.view.dims()[1]), static_cast<long long>(b_.view.dims()[0]));
     const GemmShape s = shape();
     const std::vector<int64_t> mn{static_cast<int64_t>(s.m), static_cast<int64_t>(s.n)};
     if (c_.view.dims() != mn || d_.view.dims() != mn)
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm c and d shapes must both be m-by-n");
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Gemm c and d shapes must both be m-by-n");
     // Each matrix's byte size must fit in uint64.
     const uint64_t max_elems = std::numeric_limits<uint64_t>::max() / sizeof(float);
     const auto over          = [max_elems](uint64_t x, uint64_t y) { return y != 0 && x > max_elems / y; };
     if (over(s.m, s.k) || over(s.k, s.n) || over(s.m, s.n))
-        throw Exception(FTRAIN_STATUS_OVERFLOW, "Gemm matrix byte size overflows uint64_t");
+        raise(FTRAIN_STATUS_OVERFLOW, "Gemm matrix byte size overflows uint64_t");
 }
 
 const char* matrixLayout(const StorageView& v, MatrixLayout& out) {

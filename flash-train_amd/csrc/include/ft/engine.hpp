@@ -10,6 +10,8 @@
 //   publish -> clone + configure.  UNSUPPORTED names every rejection.
 #pragma once
 
+#include <algorithm>
+
 #include <memory>
 #include <shared_mutex>
 #include <string>
@@ -53,21 +55,21 @@ class OpsEngine final : public OpsEngineBase {
 
     OpsEngine() : OpsEngineBase(Family::makePattern()), records_(Family::makeRecords()) {
         for (std::size_t i = 0; i < records_.size(); ++i) {
-            if (!records_[i]) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "OpsEngine Primitive %zu must not be null", i);
+            if (!records_[i]) raise(FTRAIN_STATUS_INVALID_ARGUMENT, "OpsEngine Primitive %zu must not be null", i);
             const char* n = records_[i]->name();
             if (n == nullptr)
-                throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "OpsEngine Primitive %zu must not return a null name", i);
+                raise(FTRAIN_STATUS_INVALID_ARGUMENT, "OpsEngine Primitive %zu must not return a null name", i);
             if (!by_name_.emplace(n, i).second)
-                throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "OpsEngine Primitive %zu repeats the name %s", i, n);
+                raise(FTRAIN_STATUS_INVALID_ARGUMENT, "OpsEngine Primitive %zu repeats the name %s", i, n);
         }
     }
 
     std::vector<std::unique_ptr<PrimitiveBase>> createPrimitives(const Args& args,
                                                                  const Constraints& constraints) const override {
         if (args.key() != pattern().key())
-            throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Args PatternKey does not match this OpsEngine");
+            raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Args PatternKey does not match this OpsEngine");
         if (!args.isComplete())
-            throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Args has one or more unset Operand or Op parameters");
+            raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Args has one or more unset Operand or Op parameters");
         const Problem problem = Family::makeProblem(args);
         const CacheKey key(constraints.key(), problem.key());
         if (!selectionCacheDisabled()) {
@@ -89,7 +91,19 @@ class OpsEngine final : public OpsEngineBase {
     struct Walk {
         std::vector<std::size_t> chosen;
         std::unordered_set<std::size_t> seen;
-        std::string rejections;
+        // Rejections grouped by reason, in order of first appearance, so a
+        // family of variants that fail for one reason costs one clause of
+        // the 2047-character message: "A, B: reason; C: other reason".
+        std::vector<std::pair<std::string, std::string>> rejections;  // (reason, names)
+
+        std::string joined() const {
+            std::string out;
+            for (const auto& [reason, names] : rejections) {
+                if (!out.empty()) out += "; ";
+                out += names + ": " + reason;
+            }
+            return out;
+        }
     };
 
     bool offer(std::size_t i, const Problem& problem, const Constraints& constraints, Walk& w) const {
@@ -98,10 +112,13 @@ class OpsEngine final : public OpsEngineBase {
         if (!primitiveAllowed(r->name())) return false;
         const Result ok = r->isApplicable(problem, constraints);
         if (!ok.isSuccess()) {
-            if (!w.rejections.empty()) w.rejections += "; ";
-            w.rejections += r->name();
-            w.rejections += ": ";
-            w.rejections += ok.getMessage();
+            const std::string reason = ok.getMessage();
+            auto group = std::find_if(w.rejections.begin(), w.rejections.end(),
+                                      [&](const auto& g) { return g.first == reason; });
+            if (group == w.rejections.end())
+                w.rejections.emplace_back(reason, r->name());
+            else
+                group->second += std::string(", ") + r->name();
             return false;
         }
         w.chosen.push_back(i);
@@ -125,9 +142,8 @@ class OpsEngine final : public OpsEngineBase {
         if (!found)
             for (std::size_t i = 0; i < records_.size(); ++i) offer(i, problem, constraints, w);
         if (w.chosen.empty())
-            throw Exception(FTRAIN_STATUS_UNSUPPORTED,
-                            "No Primitive supports the supplied Args and runtime constraints (%s)",
-                            w.rejections.c_str());
+            raise(FTRAIN_STATUS_UNSUPPORTED, "No Primitive supports the supplied Args and runtime constraints (%s)",
+                  w.joined().c_str());
         return w.chosen;
     }
 
@@ -144,7 +160,7 @@ class OpsEngine final : public OpsEngineBase {
         out.reserve(positions.size());
         for (std::size_t i : positions) {
             std::unique_ptr<PrimitiveBase> p = records_[i]->clone();
-            if (!p) throw Exception(FTRAIN_STATUS_INTERNAL_ERROR, "Applicable Primitive returned a null clone");
+            if (!p) raise(FTRAIN_STATUS_INTERNAL_ERROR, "Applicable Primitive returned a null clone");
             static_cast<Primitive<Problem>&>(*p).configure(problem);
             out.push_back(std::move(p));
         }

@@ -27,7 +27,7 @@ namespace ftrain {
 Result& lastResult() noexcept;
 
 // Runs `body` at the C boundary: success clears the thread's last result;
-// Exception -> its own status and message, std::bad_alloc -> OUT_OF_MEMORY,
+// Failure -> its own status and message, std::bad_alloc -> OUT_OF_MEMORY,
 // any other exception -> INTERNAL_ERROR.  Never throws.
 template <typename F>
 inline FTrainStatus guarded(F&& body) noexcept {
@@ -35,9 +35,9 @@ inline FTrainStatus guarded(F&& body) noexcept {
         body();
         lastResult().clear();
         return FTRAIN_STATUS_SUCCESS;
-    } catch (const Exception& e) {
-        lastResult() = e.getResult();
-        return e.getResult().getStatus();
+    } catch (const Failure& e) {
+        lastResult() = e.result();
+        return e.result().getStatus();
     } catch (const std::bad_alloc& e) {
         lastResult().set(FTRAIN_STATUS_OUT_OF_MEMORY, e.what());
         return FTRAIN_STATUS_OUT_OF_MEMORY;
@@ -45,7 +45,7 @@ inline FTrainStatus guarded(F&& body) noexcept {
         lastResult().set(FTRAIN_STATUS_INTERNAL_ERROR, e.what());
         return FTRAIN_STATUS_INTERNAL_ERROR;
     } catch (...) {
-        lastResult().set(FTRAIN_STATUS_INTERNAL_ERROR, "Unknown exception caught at C API boundary");
+        lastResult().set(FTRAIN_STATUS_INTERNAL_ERROR, "a non-standard exception reached the C entry point");
         return FTRAIN_STATUS_INTERNAL_ERROR;
     }
 }

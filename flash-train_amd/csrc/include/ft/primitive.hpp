@@ -56,11 +56,11 @@ class PrimitiveBase {
     void execute(const Resources& resources) {
         const uint64_t need = requiredWorkspaceBytes();
         if (resources.workspace_bytes < need)
-            throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Primitive requires %llu workspace bytes but received %llu",
+            raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Primitive requires %llu workspace bytes but received %llu",
                             static_cast<unsigned long long>(need),
                             static_cast<unsigned long long>(resources.workspace_bytes));
         if (need != 0 && resources.workspace == nullptr)
-            throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Primitive requires a non-null workspace for %llu bytes",
+            raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Primitive requires a non-null workspace for %llu bytes",
                             static_cast<unsigned long long>(need));
         run(resources);
     }

@@ -2,6 +2,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <iterator>
 #include <mutex>
 
 #include <flash_train/env.h>
@@ -48,46 +49,57 @@ CacheKey::CacheKey(const std::vector<uint64_t>& constraint_tokens, const std::ve
 }
 
 SelectionCache::SelectionCache(std::size_t max_entries, std::size_t shards) {
-    if (max_entries == 0)
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "SelectionCache requires a positive entry limit");
-    if (shards == 0) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "SelectionCache requires a positive shard count");
-    const std::size_t per_shard = std::max<std::size_t>(1, (max_entries + shards - 1) / shards);
-    shards_.reserve(shards);
-    for (std::size_t i = 0; i < shards; ++i) {
-        shards_.push_back(std::make_unique<Shard>());
-        shards_.back()->limit = per_shard;
+    if (max_entries == 0 || shards == 0)
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "selection cache: max_entries=%zu and shards=%zu must both be non-zero",
+              max_entries, shards);
+    // Each shard holds its even share of the limit, rounded up.
+    const std::size_t share = max_entries / shards + (max_entries % shards != 0);
+    shards_.resize(shards);
+    for (auto& s : shards_) {
+        s = std::make_unique<Shard>();
+        s->limit = share;
     }
 }
 
 std::optional<std::vector<std::size_t>> SelectionCache::find(const CacheKey& key) const {
     Shard& s = shardFor(key);
     std::shared_lock lock(s.mutex);
-    auto it = s.map.find(key);
+    const auto it = s.map.find(key);
     if (it == s.map.end()) return std::nullopt;
     it->second.hits.fetch_add(1, std::memory_order_relaxed);
     return it->second.positions;
 }
 
 void SelectionCache::publish(const CacheKey& key, std::vector<std::size_t> positions) {
-    if (positions.empty())
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "SelectionCache cannot publish an empty selection");
+    if (positions.empty()) raise(FTRAIN_STATUS_INVALID_ARGUMENT, "selection cache: a selection must list a Primitive");
     Shard& s = shardFor(key);
     std::unique_lock lock(s.mutex);
-    if (s.map.count(key)) return;
+    // First publisher wins; a racing second publisher of the same key keeps it.
+    if (s.map.find(key) != s.map.end()) return;
     if (s.map.size() >= s.limit) evictBatch(s);
     s.map.emplace(key, Entry(std::move(positions)));
 }
 
+// Drops one eighth of a full shard (at least one entry), the entries with the
+// fewest hits first.  Two passes: the batch's largest hit count is found by
+// selection over the counts alone, then every entry below it goes, and
+// entries equal to it go until the batch is complete.
 void SelectionCache::evictBatch(Shard& shard) {
     const std::size_t batch = std::max<std::size_t>(1, shard.map.size() / 8);
-    using It                = decltype(shard.map)::iterator;
-    std::vector<std::pair<uint64_t, It>> by_hits;
-    by_hits.reserve(shard.map.size());
-    for (It it = shard.map.begin(); it != shard.map.end(); ++it)
-        by_hits.emplace_back(it->second.hits.load(std::memory_order_relaxed), it);
-    std::nth_element(by_hits.begin(), by_hits.begin() + (batch - 1), by_hits.end(),
-                     [](const auto& x, const auto& y) { return x.first < y.first; });
-    for (std::size_t i = 0; i < batch; ++i) shard.map.erase(by_hits[i].second);
+    std::vector<uint64_t> counts;
+    counts.reserve(shard.map.size());
+    for (const auto& kv : shard.map) counts.push_back(kv.second.hits.load(std::memory_order_relaxed));
+    std::nth_element(counts.begin(), counts.begin() + (batch - 1), counts.end());
+    const uint64_t cut = counts[batch - 1];
+    std::size_t below = 0;
+    for (uint64_t c : counts) below += c < cut;
+    std::size_t ties = batch - below;
+    for (auto it = shard.map.begin(); it != shard.map.end();) {
+        const uint64_t h = it->second.hits.load(std::memory_order_relaxed);
+        const bool drop = h < cut || (h == cut && ties > 0);
+        if (drop && h == cut) --ties;
+        it = drop ? shard.map.erase(it) : std::next(it);
+    }
 }
 
 std::size_t SelectionCache::size() const {

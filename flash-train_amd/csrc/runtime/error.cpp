@@ -1,51 +1,48 @@
 #include "ft/error.hpp"
 
 #include <cstdio>
-#include <cstring>
 
 namespace ftrain {
 
-namespace {
-constexpr const char* kSuccessException = "Exception cannot be constructed with FTRAIN_STATUS_SUCCESS";
-}
-
-void Result::set(FTrainStatus status, const char* message) noexcept {
-    status_  = status;
-    text_[0] = '\0';
-    if (status == FTRAIN_STATUS_SUCCESS || message == nullptr) return;
-    const std::size_t n = strnlen(message, kCapacity - 1);
-    std::memcpy(text_, message, n);
-    text_[n] = '\0';
+void Result::compose(FTrainStatus status, const char* text, std::va_list* args) noexcept {
+    status_ = status;
+    char* out = text_.data();
+    out[0] = '\0';
+    if (status == FTRAIN_STATUS_SUCCESS || text == nullptr) return;
+    // "%s" on a literal and the caller's format on arguments go through the
+    // same bounded formatter, so truncation is identical for both.
+    int written = args ? std::vsnprintf(out, kMessageBytes, text, *args) : std::snprintf(out, kMessageBytes, "%s", text);
+    if (written < 0) out[0] = '\0';
+    out[kMessageBytes - 1] = '\0';
 }
 
 void Result::vformat(FTrainStatus status, const char* fmt, std::va_list args) noexcept {
-    status_  = status;
-    text_[0] = '\0';
-    if (status == FTRAIN_STATUS_SUCCESS || fmt == nullptr) return;
-    if (std::vsnprintf(text_, kCapacity, fmt, args) < 0) text_[0] = '\0';
-    text_[kCapacity - 1] = '\0';
+    std::va_list copy;
+    va_copy(copy, args);
+    compose(status, fmt, &copy);
+    va_end(copy);
 }
 
 void Result::format(FTrainStatus status, const char* fmt, ...) noexcept {
     std::va_list args;
     va_start(args, fmt);
-    vformat(status, fmt, args);
+    compose(status, fmt, &args);
     va_end(args);
 }
 
-Exception::Exception(const Result& result) noexcept : result_(result) {
-    if (result_.isSuccess()) result_.set(FTRAIN_STATUS_INTERNAL_ERROR, kSuccessException);
+Failure::Failure(const Result& result) noexcept : result_(result) {
+    // A Failure always reports a failure: a success status here is a bug in
+    // the raising code, reported as such rather than as a silent success.
+    if (result_.isSuccess()) result_.set(FTRAIN_STATUS_INTERNAL_ERROR, "internal: a failure was raised with a success status");
 }
 
-Exception::Exception(FTrainStatus status, const char* fmt, ...) noexcept {
-    if (status == FTRAIN_STATUS_SUCCESS) {
-        result_.set(FTRAIN_STATUS_INTERNAL_ERROR, kSuccessException);
-        return;
-    }
+void raise(FTrainStatus status, const char* fmt, ...) {
+    Result r;
     std::va_list args;
     va_start(args, fmt);
-    result_.vformat(status, fmt, args);
+    r.vformat(status, fmt, args);
     va_end(args);
+    throw Failure(r);
 }
 
 }  // namespace ftrain

@@ -5,11 +5,11 @@
 namespace ftrain {
 
 void Handle::add(std::shared_ptr<OpsEngineBase> engine) {
-    if (!engine) throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "OpsEngine must not be null");
+    if (!engine) raise(FTRAIN_STATUS_INVALID_ARGUMENT, "engine registry: cannot register a null engine");
     std::unique_lock lock(mutex_);
     const PatternKey key = engine->pattern().key();
     if (!engines_.emplace(key, std::move(engine)).second)
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "An OpsEngine is already registered for this PatternKey");
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "engine registry: this Pattern already has an engine");
 }
 
 std::shared_ptr<const OpsEngineBase> Handle::find(const PatternKey& key) const {

@@ -55,12 +55,12 @@ Pattern PatternBuilder::build() const {
         for (std::size_t port = 0; port < node.inputs.size(); ++port) {
             const uint64_t id = node.inputs[port];
             if (id >= n_operands)
-                throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT,
+                raise(FTRAIN_STATUS_INVALID_ARGUMENT,
                                 "Operation %zu input port %zu references out-of-range operand %llu for %zu operands", o,
                                 port, static_cast<unsigned long long>(id), n_operands);
             for (std::size_t q = 0; q < port; ++q)
                 if (node.inputs[q] == id)
-                    throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT,
+                    raise(FTRAIN_STATUS_INVALID_ARGUMENT,
                                     "Operation %zu repeats operand %llu across input ports", o,
                                     static_cast<unsigned long long>(id));
             p.consumers_[id].push_back(PortRef{o, port});
@@ -68,20 +68,20 @@ Pattern PatternBuilder::build() const {
         for (std::size_t port = 0; port < node.outputs.size(); ++port) {
             const uint64_t id = node.outputs[port];
             if (id >= n_operands)
-                throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT,
+                raise(FTRAIN_STATUS_INVALID_ARGUMENT,
                                 "Operation %zu output port %zu references out-of-range operand %llu for %zu operands",
                                 o, port, static_cast<unsigned long long>(id), n_operands);
             if (std::find(node.inputs.begin(), node.inputs.end(), id) != node.inputs.end())
-                throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT,
+                raise(FTRAIN_STATUS_INVALID_ARGUMENT,
                                 "Operation %zu output port %zu reuses operand %llu from an input port", o, port,
                                 static_cast<unsigned long long>(id));
             for (std::size_t q = 0; q < port; ++q)
                 if (node.outputs[q] == id)
-                    throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT,
+                    raise(FTRAIN_STATUS_INVALID_ARGUMENT,
                                     "Operation %zu repeats operand %llu across output ports", o,
                                     static_cast<unsigned long long>(id));
             if (p.producer_[id])
-                throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT,
+                raise(FTRAIN_STATUS_INVALID_ARGUMENT,
                                 "Operation %zu output port %zu reuses operand %llu that already has a producer", o,
                                 port, static_cast<unsigned long long>(id));
             p.producer_[id] = PortRef{o, port};
@@ -118,12 +118,12 @@ Pattern PatternBuilder::build() const {
             for (uint64_t in : ops_[o].inputs) {
                 const auto& prod = p.producer_[in];
                 if (prod && indegree[prod->op] != 0)
-                    throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT,
+                    raise(FTRAIN_STATUS_INVALID_ARGUMENT,
                                     "Operation %zu input port participates in a dependency cycle through operand %llu",
                                     o, static_cast<unsigned long long>(in));
             }
         }
-        throw Exception(FTRAIN_STATUS_INTERNAL_ERROR, "cycle check peeled %zu of %zu operations but found no edge",
+        raise(FTRAIN_STATUS_INTERNAL_ERROR, "cycle check peeled %zu of %zu operations but found no edge",
                         peeled, n_ops);
     }
 
@@ -271,9 +271,9 @@ class Matcher {
 
 Ops::Ops(const Pattern& user, const Pattern& supported) : key_(user.key()) {
     if (user.key() != supported.key())
-        throw Exception(FTRAIN_STATUS_UNSUPPORTED, "Ops: user Pattern does not match the supported Pattern");
+        raise(FTRAIN_STATUS_UNSUPPORTED, "Ops: user Pattern does not match the supported Pattern");
     Matcher m(user, supported);
-    if (!m.run()) throw Exception(FTRAIN_STATUS_UNSUPPORTED, "Ops: user Pattern does not match the supported Pattern");
+    if (!m.run()) raise(FTRAIN_STATUS_UNSUPPORTED, "Ops: user Pattern does not match the supported Pattern");
     operand_map_ = m.operandMap();
     op_map_      = m.opMap();
     for (std::size_t i = 0; i < supported.numOperands(); ++i) operand_kinds_.push_back(supported.operandKind(i));
@@ -302,36 +302,36 @@ bool Args::isComplete() const noexcept {
 
 const std::optional<OperandValue>& Args::operand(uint64_t id) const {
     if (id >= operands_.size())
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Supported operand role index %llu is out of range [0, %zu)",
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Supported operand role index %llu is out of range [0, %zu)",
                         static_cast<unsigned long long>(id), operands_.size());
     return operands_[id];
 }
 
 const std::optional<OperationAttributes>& Args::operation(uint64_t id) const {
     if (id >= operations_.size())
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "Supported op role index %llu is out of range [0, %zu)",
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Supported op role index %llu is out of range [0, %zu)",
                         static_cast<unsigned long long>(id), operations_.size());
     return operations_[id];
 }
 
 void Args::setOperand(uint64_t user_id, OperandValue value) {
     if (user_id >= operand_map_.size())
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "User operand role index %llu is out of range [0, %zu)",
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "User operand role index %llu is out of range [0, %zu)",
                         static_cast<unsigned long long>(user_id), operand_map_.size());
     const uint64_t slot = operand_map_[user_id];
     if (static_cast<std::size_t>(operand_kinds_[slot]) != value.index())
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "User operand role %llu has a different storage family",
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "User operand role %llu has a different storage family",
                         static_cast<unsigned long long>(user_id));
     operands_[slot] = std::move(value);
 }
 
 void Args::setOperation(uint64_t user_id, OperationAttributes attributes) {
     if (user_id >= op_map_.size())
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "User op role index %llu is out of range [0, %zu)",
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "User op role index %llu is out of range [0, %zu)",
                         static_cast<unsigned long long>(user_id), op_map_.size());
     const uint64_t slot = op_map_[user_id];
     if (op_kinds_[slot] != attributes.kind)
-        throw Exception(FTRAIN_STATUS_INVALID_ARGUMENT, "User op role %llu has a different operation kind",
+        raise(FTRAIN_STATUS_INVALID_ARGUMENT, "User op role %llu has a different operation kind",
                         static_cast<unsigned long long>(user_id));
     operations_[slot] = attributes;
 }

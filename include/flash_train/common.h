@@ -120,7 +120,8 @@ typedef struct FTrainPlanStruct* FTrainPlan;
 /* Last status recorded on this thread; SUCCESS before any call. */
 FTRAIN_API FTrainStatus ftrainGetLastStatus(void);
 
-/* Last message recorded on this thread ("" after a success).  Owned by the
+/* Last message recorded on this thread ("" after a success), at most 2047
+ * characters (reference error.hpp:17,52).  Owned by the
  * library; valid until this thread's next non-query call. */
 FTRAIN_API const char* ftrainGetLastMessage(void);
 
@@ -138,9 +139,10 @@ FTRAIN_API FTrainStatus ftrainPatternAddGemm(FTrainPattern pattern, FTrainGemmOp
                                              FTrainTensorId b, FTrainTensorId c, FTrainTensorId d, FTrainTensorId alpha,
                                              FTrainTensorId beta);
 
-/* Grouped GEMM topologies: accepted into a Pattern, but no engine is
- * registered for them, so ftrainOpsCreate() returns UNSUPPORTED -- the
- * reference's behaviour (src/engine.cpp:25-27). */
+/* Grouped GEMM topologies (reference common.h, grouped op builders).  The
+ * reference registers no engine for them, so its ftrainOpsCreate() returns
+ * UNSUPPORTED (src/engine.cpp:25-27); this library registers an engine for
+ * each, so ftrainOpsCreate() returns an Ops and Plans run grouped kernels. */
 FTRAIN_API FTrainStatus ftrainPatternAddGroupedABCDGemm(FTrainPattern pattern, FTrainGroupedABCDGemmOpId* op,
                                                         FTrainGroupedTensorId a, FTrainGroupedTensorId b,
                                                         FTrainGroupedTensorId c, FTrainGroupedTensorId d,

@@ -473,8 +473,34 @@ def test_unsupported_reasons_name_every_primitive(tlib, tops, kw, why):
                              compute=kw.get("compute", c.FP32))
     assert st == c.UNSUPPORTED, msg
     assert why in msg
+    assert len(msg) <= 2047
+    # Rejections are grouped by reason ("A, B: reason; C: other"); every
+    # variant is named unless the message reached the 2047-character cap.
     for v in range(tlib.ftrainTestingVariantCount()):
-        assert tlib.ftrainTestingVariantName(v).decode() in msg
+        name = tlib.ftrainTestingVariantName(v).decode()
+        assert name in msg or len(msg) == 2047, (name, msg)
+    assert msg.count(": " + why) <= 1 or why == "", msg
+
+
+@pytest.mark.parametrize("formatted", [True, False])
+@pytest.mark.parametrize("length,kept", [(10, 10), (2046, 2046), (2047, 2047), (2048, 2047), (10000, 2047)])
+def test_last_message_holds_at_most_2047_characters(tlib, formatted, length, kept):
+    """Reference error.hpp:17,52: 2048 bytes of storage, terminator included."""
+    tlib.ftrainTestingFailWithLength.restype = ctypes.c_int
+    tlib.ftrainTestingFailWithLength.argtypes = [ctypes.c_int, ctypes.c_size_t, ctypes.c_bool]
+    st = tlib.ftrainTestingFailWithLength(c.UNSUPPORTED, length, formatted)
+    assert st == c.UNSUPPORTED
+    assert tlib.ftrainGetLastStatus() == c.UNSUPPORTED
+    msg = ctypes.string_at(tlib.ftrainGetLastMessage())
+    assert msg == b"x" * kept
+
+
+def test_failure_with_success_status_reports_internal_error(tlib):
+    tlib.ftrainTestingFailWithLength.restype = ctypes.c_int
+    tlib.ftrainTestingFailWithLength.argtypes = [ctypes.c_int, ctypes.c_size_t, ctypes.c_bool]
+    st = tlib.ftrainTestingFailWithLength(c.SUCCESS, 5, False)
+    assert st == c.INTERNAL_ERROR
+    assert b"success status" in ctypes.string_at(tlib.ftrainGetLastMessage())
 
 
 def S(dims, strides, mem=FAKE):
