@@ -49,7 +49,6 @@ LIB_SOURCES = [
     "csrc/runtime/plan.cpp",
     "csrc/runtime/handle.cpp",
     "csrc/runtime/trace.cpp",
-    "csrc/runtime/workspace.cpp",
     "csrc/gemm/catalog.cpp",
     "csrc/gemm/problem.cpp",
     "csrc/gemm/finder.cpp",

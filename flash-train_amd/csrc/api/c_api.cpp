@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <cstring>
 #include <exception>
+#include <mutex>
 #include <new>
 #include <optional>
 #include <utility>
@@ -68,6 +69,15 @@ FTrainStatus setOperation(FTrainArgs args, uint64_t op, OperationKind kind, FTra
     });
 }
 
+// Keeps `plan` alive until the process ends (for Plans a captured graph may
+// replay: its kernels point at the Plan's split-k buffer).
+void retire(FTrainPlan plan) {
+    static std::mutex mutex;
+    static auto* retired = new std::vector<FTrainPlan>();
+    std::lock_guard<std::mutex> lock(mutex);
+    retired->push_back(plan);
+}
+
 // Plans created by ftrainGemm, kept per thread and reused when a later call
 // describes exactly the same problem: the same six views (addresses, dims,
 // strides, types, placement), the same host alpha/beta values, compute type
@@ -125,29 +135,58 @@ class ConveniencePlans {
 
     FTrainPlan find(const std::vector<uint64_t>& key) {
         for (std::size_t i = 0; i < entries_.size(); ++i) {
-            if (entries_[i].first == key) {
+            if (entries_[i].key == key) {
                 if (i != 0) std::rotate(entries_.begin(), entries_.begin() + i, entries_.begin() + i + 1);
-                return entries_.front().second;
+                return entries_.front().plan;
             }
         }
         return nullptr;
     }
 
     void insert(std::vector<uint64_t> key, FTrainPlan plan) {
-        entries_.insert(entries_.begin(), {std::move(key), plan});
+        entries_.insert(entries_.begin(), Entry{std::move(key), plan, false});
         while (entries_.size() > kCapacity) {
-            delete entries_.back().second;
+            drop(entries_.back());
             entries_.pop_back();
         }
     }
 
+    // The most recent entry (the one just found or inserted) was executed
+    // under stream capture: a graph may replay its kernels, which point at
+    // the Plan's split-k buffer, at any later time.
+    void markFrontCaptured() {
+        if (!entries_.empty()) entries_.front().captured = true;
+    }
+
     ~ConveniencePlans() {
-        for (auto& e : entries_) delete e.second;
+        for (auto& e : entries_) drop(e);
     }
 
   private:
-    std::vector<std::pair<std::vector<uint64_t>, FTrainPlan>> entries_;  // most recent first
+    struct Entry {
+        std::vector<uint64_t> key;
+        FTrainPlan plan;
+        bool captured;
+    };
+
+    static void drop(Entry& e) {
+        if (e.captured)
+            retire(e.plan);
+        else
+            delete e.plan;
+    }
+
+    std::vector<Entry> entries_;  // most recent first
 };
+
+bool streamCapturing(FTrainStream stream) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &status) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return status != hipStreamCaptureStatusNone;
+}
 
 }  // namespace
 }  // namespace ftrain
@@ -323,7 +362,9 @@ FTrainStatus ftrainPlanCreate(FTrainPlan* plan, FTrainArgs args) {
         requireNonNull(args, "ftrainPlanCreate: args handle must not be null");
         const auto engine = globalHandle().find(args->args.key());
         if (!engine) raise(FTRAIN_STATUS_INTERNAL_ERROR, "OpsEngine registered for Args is unavailable");
-        *plan = new FTrainPlanStruct{engine->createPlan(args->args)};
+        auto made = std::make_unique<FTrainPlanStruct>(FTrainPlanStruct{engine->createPlan(args->args)});
+        made->plan.prepare();
+        *plan = made.release();
     });
 }
 
@@ -403,8 +444,10 @@ FTrainStatus ftrainGemm(FTrainStorageView a, FTrainStorageView b, FTrainStorageV
     std::vector<uint64_t> key;
     if (cacheable && hipGetDevice(&device) == hipSuccess) {
         key = ConveniencePlans::describe(views, compute_type, device, stream);
-        if (FTrainPlan cached = ConveniencePlans::local().find(key))
+        if (FTrainPlan cached = ConveniencePlans::local().find(key)) {
+            if (streamCapturing(stream)) ConveniencePlans::local().markFrontCaptured();
             return ftrainPlanExecutePrimitive(cached, 0, workspace, workspace_bytes, stream);
+        }
     } else {
         (void)hipGetLastError();
     }
@@ -422,10 +465,14 @@ FTrainStatus ftrainGemm(FTrainStorageView a, FTrainStorageView b, FTrainStorageV
     // Keep the failing step's diagnostic across the clean-up calls.
     const Result failure = s != FTRAIN_STATUS_SUCCESS ? lastResult() : Result{};
     if (plan != nullptr) {
-        if (s == FTRAIN_STATUS_SUCCESS && !key.empty())
+        if (s == FTRAIN_STATUS_SUCCESS && !key.empty()) {
             ConveniencePlans::local().insert(std::move(key), plan);  // the cache now owns it
-        else
+            if (streamCapturing(stream)) ConveniencePlans::local().markFrontCaptured();
+        } else if (s == FTRAIN_STATUS_SUCCESS && streamCapturing(stream)) {
+            retire(plan);
+        } else {
             ftrainPlanDestroy(plan);
+        }
     }
     if (args != nullptr) ftrainArgsDestroy(args);
     if (s != FTRAIN_STATUS_SUCCESS) lastResult() = failure;

@@ -401,51 +401,50 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
         table_.reset();
     }
 
+    // The per-group parameter tables live on the device for the Plan's
+    // lifetime.  They are uploaded here, at Plan creation, with blocking
+    // copies, so executions on any stream find them complete and every
+    // execution, the first included, only launches kernels (and can be
+    // captured).  Layout per orientation bucket: parameters, then tile
+    // starts (16-byte aligned sections).
+    void prepare(bool) override {
+        if (table_) return;
+        const bool half = v_->input != FTRAIN_NUMERIC_TYPE_FP32;
+        size_t total = 0;
+        for (Bucket& bk : buckets_) {
+            if (bk.tiles == 0) continue;
+            bk.param_off = total;
+            total += ((half ? bk.half_params.size() * sizeof(HalfGemmParams) : bk.params.size() * sizeof(GemmParams)) + 15) / 16 * 16;
+            bk.start_off = total;
+            total += (bk.tile_start.size() * sizeof(int32_t) + 15) / 16 * 16;
+        }
+        if (total == 0) return;
+        void* buf = nullptr;
+        if (hipMalloc(&buf, total) != hipSuccess) {
+            (void)hipGetLastError();
+            raise(FTRAIN_STATUS_OUT_OF_MEMORY, "%s: device parameter table of %zu bytes", v_->name, total);
+        }
+        std::shared_ptr<void> table(buf, [](void* q) { (void)hipFree(q); });
+        for (const Bucket& bk : buckets_) {
+            if (bk.tiles == 0) continue;
+            const void* host = half ? static_cast<const void*>(bk.half_params.data()) : static_cast<const void*>(bk.params.data());
+            const size_t bytes = half ? bk.half_params.size() * sizeof(HalfGemmParams) : bk.params.size() * sizeof(GemmParams);
+            check(hipMemcpy(static_cast<char*>(buf) + bk.param_off, host, bytes, hipMemcpyHostToDevice), v_->name);
+            check(hipMemcpy(static_cast<char*>(buf) + bk.start_off, bk.tile_start.data(),
+                            bk.tile_start.size() * sizeof(int32_t), hipMemcpyHostToDevice),
+                  v_->name);
+        }
+        table_ = std::move(table);
+    }
+
   protected:
     void run(const Resources& r) override {
         const bool half = v_->input != FTRAIN_NUMERIC_TYPE_FP32;
-        if (!table_) {
-            // The per-group parameter tables live on the device for the
-            // Plan's lifetime.  They are uploaded once, on the first
-            // execution, with a blocking copy: later executions may use other
-            // streams, which must find the table complete.  A blocking copy
-            // is illegal under stream capture, so the first execution cannot
-            // be captured (later ones can: they only launch kernels).  Layout
-            // per orientation bucket: parameters, then tile starts (16-byte
-            // aligned sections).
-            size_t total = 0;
-            for (Bucket& bk : buckets_) {
-                if (bk.tiles == 0) continue;
-                bk.param_off = total;
-                total += ((half ? bk.half_params.size() * sizeof(HalfGemmParams) : bk.params.size() * sizeof(GemmParams)) + 15) / 16 * 16;
-                bk.start_off = total;
-                total += (bk.tile_start.size() * sizeof(int32_t) + 15) / 16 * 16;
-            }
-            if (total == 0) return;
-            hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-            check(hipStreamIsCapturing(r.stream, &capture), v_->name);
-            if (capture != hipStreamCaptureStatusNone)
-                raise(FTRAIN_STATUS_UNSUPPORTED,
-                                "%s: the first execution of a grouped Plan uploads its parameter table and cannot be "
-                                "captured; execute the Plan once before capturing it",
-                                v_->name);
-            void* buf = nullptr;
-            if (hipMalloc(&buf, total) != hipSuccess) {
-                (void)hipGetLastError();
-                raise(FTRAIN_STATUS_OUT_OF_MEMORY, "%s: device parameter table of %zu bytes", v_->name, total);
-            }
-            std::shared_ptr<void> table(buf, [](void* q) { (void)hipFree(q); });
-            for (const Bucket& bk : buckets_) {
-                if (bk.tiles == 0) continue;
-                const void* host = half ? static_cast<const void*>(bk.half_params.data()) : static_cast<const void*>(bk.params.data());
-                const size_t bytes = half ? bk.half_params.size() * sizeof(HalfGemmParams) : bk.params.size() * sizeof(GemmParams);
-                check(hipMemcpy(static_cast<char*>(buf) + bk.param_off, host, bytes, hipMemcpyHostToDevice), v_->name);
-                check(hipMemcpy(static_cast<char*>(buf) + bk.start_off, bk.tile_start.data(),
-                                bk.tile_start.size() * sizeof(int32_t), hipMemcpyHostToDevice),
-                      v_->name);
-            }
-            table_ = std::move(table);  // published only once complete
-        }
+        bool any = false;
+        for (const Bucket& bk : buckets_) any = any || bk.tiles > 0;
+        if (!any) return;
+        if (!table_)
+            raise(FTRAIN_STATUS_INTERNAL_ERROR, "%s: the Plan's device parameter table was never uploaded", v_->name);
         char* base = static_cast<char*>(table_.get());
         for (const Bucket& bk : buckets_) {
             if (bk.tiles == 0) continue;

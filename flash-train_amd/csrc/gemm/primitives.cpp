@@ -10,7 +10,6 @@
 #include <hip/hip_runtime.h>
 
 #include "ft/gemm.hpp"
-#include "ft/workspace.hpp"
 
 namespace ftrain {
 namespace {
@@ -93,18 +92,6 @@ void checkBlockSize(const void* kernel, int threads, const char* name) {
                         name, threads, attr.maxThreadsPerBlock);
 }
 
-// Largest split-k partial buffer a Primitive keeps for its Plan's lifetime.
-constexpr uint64_t kOwnedPartialBytes = 16ull << 20;
-
-bool capturing(hipStream_t stream) {
-    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &status) != hipSuccess) {
-        (void)hipGetLastError();
-        return true;  // unknown: take the pool, which is stream-ordered
-    }
-    return status != hipStreamCaptureStatusNone;
-}
-
 void check(hipError_t e, const char* what) {
     if (e != hipSuccess)
         raise(FTRAIN_STATUS_INTERNAL_ERROR, "%s launch failed: %s", what, hipGetErrorString(e));
@@ -117,7 +104,22 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
 
     const char* name() const noexcept override { return info_->name; }
     std::unique_ptr<PrimitiveBase> clone() const override { return std::make_unique<GemmPrimitive>(*this); }
-    uint64_t requiredWorkspaceBytes() const noexcept override { return 0; }
+    // Split-k partial tiles: Primitive 0 of a Plan made by ftrainPlanCreate
+    // owns its buffer (allocated at Plan creation), so it needs none; any
+    // other split Primitive needs its partial bytes from the caller.
+    uint64_t requiredWorkspaceBytes() const noexcept override { return owned_ ? 0 : partial_bytes_; }
+    uint64_t scratchBytes() const noexcept override { return partial_bytes_; }
+
+    void prepare(bool default_slot) override {
+        if (!default_slot || partial_bytes_ == 0 || owned_) return;
+        void* q = nullptr;
+        if (hipMalloc(&q, partial_bytes_) != hipSuccess) {
+            (void)hipGetLastError();
+            raise(FTRAIN_STATUS_OUT_OF_MEMORY, "%s: split-k partial buffer of %llu bytes", info_->name,
+                  static_cast<unsigned long long>(partial_bytes_));
+        }
+        owned_.reset(q, [](void* x) { (void)hipFree(x); });
+    }
 
     Result isApplicable(const GemmProblem& p, const Constraints& constraints) const override {
         Result r = commonChecks(p, info_->input);
@@ -248,33 +250,18 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
                 break;
             case SplitKind::kPartial: {
                 // Partial tiles go to the caller's workspace when it is large
-                // and aligned enough; else, up to kOwnedPartialBytes, to a
-                // buffer this Primitive allocates on its first execution and
-                // keeps for the Plan's lifetime (executions of one Plan are
-                // externally serialised, reference common.h:576); else to a
-                // stream-ordered pool buffer.  A first execution under stream
-                // capture cannot allocate and uses the pool.
+                // and aligned enough, else to the buffer this Primitive got
+                // at Plan creation.  Nothing is allocated here, so every
+                // execution, the first included, can be captured.  Executions
+                // of one Plan are serialised by the caller (reference
+                // common.h:576), so they may share the owned buffer.
                 const bool caller = r.workspace != nullptr && r.workspace_bytes >= partial_bytes_ &&
                                     reinterpret_cast<uintptr_t>(r.workspace) % 16 == 0;
-                bool pooled       = false;
-                void* ws          = nullptr;
-                if (caller) {
-                    ws = r.workspace;
-                } else if (partial_bytes_ <= kOwnedPartialBytes && (owned_ || !capturing(r.stream))) {
-                    if (!owned_) {
-                        void* q = nullptr;
-                        if (hipMalloc(&q, partial_bytes_) != hipSuccess) {
-                            (void)hipGetLastError();
-                            raise(FTRAIN_STATUS_OUT_OF_MEMORY, "%s: split-k buffer of %llu bytes",
-                                            info_->name, static_cast<unsigned long long>(partial_bytes_));
-                        }
-                        owned_.reset(q, [](void* x) { (void)hipFree(x); });
-                    }
-                    ws = owned_.get();
-                } else {
-                    ws     = acquireWorkspace(partial_bytes_, r.stream);
-                    pooled = true;
-                }
+                void* ws = caller ? r.workspace : owned_.get();
+                if (ws == nullptr)
+                    raise(FTRAIN_STATUS_INVALID_ARGUMENT,
+                          "%s requires a 16-byte aligned workspace of %llu bytes for its split-k partial tiles",
+                          info_->name, static_cast<unsigned long long>(partial_bytes_));
                 params.d           = static_cast<float*>(ws);
                 half_params.d      = ws;
                 ReduceParams red   = reduce_;
@@ -283,7 +270,6 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
                 hipError_t e       = hipLaunchKernel(kernel_, grid_, block_, args, 0, r.stream);
                 if (e == hipSuccess)
                     e = hipLaunchKernel(gemm::reduceKernel(reduce_vec_), aux_grid_, dim3(256), rargs, 0, r.stream);
-                if (pooled) releaseWorkspace(ws, r.stream);
                 check(e, info_->name);
                 break;
             }
@@ -314,7 +300,7 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
     ReduceParams reduce_{};
     bool reduce_vec_        = false;
     uint64_t partial_bytes_ = 0;
-    std::shared_ptr<void> owned_;  // split-k partials of this Plan (small buffers only)
+    std::shared_ptr<void> owned_;  // split-k partials of Primitive 0 (shared by clones)
 };
 
 }  // namespace

@@ -51,6 +51,16 @@ class PrimitiveBase {
     virtual std::unique_ptr<PrimitiveBase> clone() const        = 0;
     virtual uint64_t requiredWorkspaceBytes() const noexcept    = 0;
 
+    // Device memory beyond the operands that one execution writes and reads
+    // back (split-k partial tiles), whoever provides it.
+    virtual uint64_t scratchBytes() const noexcept { return 0; }
+
+    // Acquires the device resources the Primitive keeps for its Plan's
+    // lifetime, on the Plan's device, once, at Plan creation (never during
+    // an execution).  `default_slot` is true for Primitive 0, the one
+    // ftrainGemm runs without a workspace.
+    virtual void prepare(bool default_slot) { (void)default_slot; }
+
     // Checks the workspace against the requirement (INVALID_ARGUMENT) and
     // enqueues the work on resources.stream without synchronizing.
     void execute(const Resources& resources) {
@@ -90,6 +100,9 @@ class Plan {
     FTrainDeviceId device() const noexcept { return device_; }
     const char* primitiveName(uint64_t index) const { return at(index).name(); }
     uint64_t requiredWorkspaceBytes(uint64_t index) const { return at(index).requiredWorkspaceBytes(); }
+
+    // Runs every Primitive's prepare() (Primitive 0 as the default slot).
+    void prepare();
 
     // Device check (calling thread's device must be the Plan's), index check,
     // then the Primitive's workspace check and launch.

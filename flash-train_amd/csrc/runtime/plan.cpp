@@ -19,6 +19,10 @@ Plan::Plan(std::vector<std::unique_ptr<PrimitiveBase>> primitives, FTrainDeviceI
         if (!p) raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Plan Primitive must not be null");
 }
 
+void Plan::prepare() {
+    for (std::size_t i = 0; i < primitives_.size(); ++i) primitives_[i]->prepare(i == 0);
+}
+
 PrimitiveBase& Plan::at(uint64_t index) const {
     if (index >= primitives_.size())
         raise(FTRAIN_STATUS_INVALID_ARGUMENT, "Plan primitive index %llu is out of range for %llu primitives",

@@ -310,6 +310,17 @@ class Plan:
         return self.lib.ftrainPlanExecutePrimitive(self.handle, i, workspace or None, workspace_bytes, stream or None)
 
     def execute(self, i: int = 0, stream: int = 0, workspace: int = 0, workspace_bytes: int = 0) -> None:
+        """ftrainPlanExecutePrimitive.  With no workspace given, a Primitive that
+        requires one gets a device buffer of the required size, allocated once
+        per Plan through torch and kept with this object."""
+        if not workspace:
+            need = self.workspace_bytes(i)
+            if need:
+                import torch
+
+                if getattr(self, "_ws", None) is None or self._ws.numel() < need:
+                    self._ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+                workspace, workspace_bytes = self._ws.data_ptr(), need
         check(self.execute_status(i, stream, workspace, workspace_bytes), "ftrainPlanExecutePrimitive", self.lib)
 
     def close(self) -> None:
@@ -333,13 +344,20 @@ def gemm_status(a: View, b: View, c: View, d: View, alpha: View, beta: View, com
 
 def plan_for(a: torch.Tensor, b: torch.Tensor, c: Optional[torch.Tensor], d: torch.Tensor, alpha: float,
              beta: float, ops: Optional[GemmOps] = None) -> Plan:
-    """Creates a Plan for device tensors (c may be None: null c memory)."""
+    """Creates a Plan for device tensors (c may be None: null c memory).
+
+    The Plan binds the tensors' addresses, so the returned object keeps the
+    tensors alive (a temporary such as `x.cuda()` passed here would otherwise
+    be freed, and its memory handed out again, while the Plan still points
+    at it)."""
     ops = ops or GemmOps()
     al, be = HostScalar(alpha), HostScalar(beta)
     m, n = d.shape
     args = ops.args(matrix(a), matrix(b), matrix(c, [m, n]), matrix(d), al.view, be.view)
     try:
-        return args.plan()
+        plan = args.plan()
+        plan._operands = (a, b, c, d)
+        return plan
     finally:
         args.close()
 

@@ -540,6 +540,26 @@ def test_strided_alignment_rules(tlib, tops):
     plan.close()
 
 
+def test_split_k_primitives_report_their_partial_bytes(tlib, tops):
+    """Without Plan preparation (the host hook skips it) every split-k
+    Primitive states its partial-tile bytes as required workspace: a whole
+    number of m x n fp32 slices, at least two, within the 256 MiB cap.  Whole-k
+    Primitives need none."""
+    m, n, k = 64, 4096, 4096
+    st, msg, plan = plan_status(tlib, tops, V([m, k]), V([k, n]), V([m, n], None), V([m, n]))
+    assert st == c.SUCCESS, msg
+    split = 0
+    for i, name in enumerate(plan.names()):
+        w = plan.workspace_bytes(i)
+        if name.endswith("SplitK"):
+            split += 1
+            assert w % (m * n * 4) == 0 and 2 <= w // (m * n * 4) and w <= 256 << 20, (name, w)
+        else:
+            assert w == 0, (name, w)
+    assert split >= 2
+    plan.close()
+
+
 def test_empty_output_needs_no_storage(tlib, tops):
     st, msg, plan = plan_status(tlib, tops, V([0, 2], None), V([2, 4], None), V([0, 4], None), V([0, 4], None))
     assert st == c.SUCCESS, msg

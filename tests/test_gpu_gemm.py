@@ -342,25 +342,38 @@ def test_convenience_calls_reuse_plans_without_changing_results(capi, oracle):
 
 
 def test_caller_workspace_is_used_for_split_k(capi, ops, oracle):
-    """A split-k Primitive takes its partial tiles from the caller's workspace
-    when one is passed, and from the library pool otherwise; results agree."""
+    """Workspace contract of split-k Primitives (reference common.h:548-576):
+    Primitive 0 owns a partial buffer allocated at Plan creation and requires
+    no workspace; every other split Primitive reports its partial bytes, is
+    rejected with INVALID_ARGUMENT without them, and runs with them.  Results
+    agree either way."""
     m, n, k = 64, 512, 8192
     g = torch.Generator().manual_seed(5)
     a_h, b_h = torch.randn(m, k, generator=g), torch.randn(k, n, generator=g)
     ref = oracle.gemm_f64(a_h, b_h)
     d = torch.empty(m, n, device="cuda")
     plan = capi.plan_for(a_h.cuda(), b_h.cuda(), None, d, 1.0, 0.0, ops)
-    split = [i for i, nm in enumerate(plan.names()) if nm.startswith("Fp32MfmaGemm") and nm.endswith("_SplitK")]
-    assert split, plan.names()
+    names = plan.names()
+    split = [i for i, nm in enumerate(names) if nm.endswith("_SplitK")]
+    assert len(split) >= 2, names
+    assert plan.workspace_bytes(0) == 0
     ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
     s = torch.cuda.current_stream().cuda_stream
     for i in split:
-        for workspace in (0, ws.data_ptr()):
+        need = plan.workspace_bytes(i)
+        if i == 0:
+            assert need == 0
+        else:
+            assert need > 0 and need % (m * n * 4) == 0, (names[i], need)
+            assert plan.execute_status(i, s) == capi.INVALID_ARGUMENT
+            assert "workspace" in capi.last_message()
+            assert plan.execute_status(i, s, ws.data_ptr(), need - 1) == capi.INVALID_ARGUMENT
+        for workspace in ((0, ws.data_ptr()) if i == 0 else (ws.data_ptr(),)):
             d.fill_(float("nan"))
-            plan.execute(i, s, workspace, ws.numel() if workspace else 0)
+            assert plan.execute_status(i, s, workspace, ws.numel() if workspace else 0) == capi.SUCCESS
             torch.cuda.synchronize()
             rep = oracle.tolerance_check(d.cpu().numpy(), ref, k)
-            assert rep["ok"], (plan.name(i), workspace != 0, rep)
+            assert rep["ok"], (names[i], workspace != 0, rep)
 
 
 def test_split_k_is_deterministic(capi, ops):

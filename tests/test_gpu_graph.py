@@ -1,14 +1,13 @@
 """Plans inside HIP graphs and across streams, called through the C ABI.
 
-A cached Plan's execution is kernel launches only (a split-k Primitive given
-the caller's workspace included), so it can be captured into a HIP graph and
-replayed.  Every replay here runs after the inputs were changed eagerly, and
-its d is compared with the fp64 oracle on the new inputs, so a replay that
-reused stale results or a stale parameter table fails.
-
-A grouped Plan uploads its per-group parameter table with a blocking copy on
-its first execution: that execution cannot be captured (UNSUPPORTED with a
-reason), and any stream may execute the Plan afterwards.
+Every execution of a Plan is kernel launches only: split-k partial tiles go
+to the caller's workspace or to the buffer Primitive 0 got at Plan creation,
+and a grouped Plan's parameter table is uploaded at Plan creation.  So any
+execution, the first included, can be captured into a HIP graph and
+replayed.  Every replay here runs after the inputs were changed eagerly,
+with eager work and synchronisations between replays, and its d is compared
+with the fp64 oracle on the new inputs, so a replay that reused stale
+results, a stale table or freed memory fails.
 """
 
 import numpy as np
@@ -33,23 +32,28 @@ def rnd(shape, seed):
     return torch.randn(*shape, generator=g)
 
 
-@pytest.mark.parametrize("shape,want", [((1024, 1024, 1024), ""), ((64, 4096, 4096), "_SplitK")])
-def test_plan_replays_in_a_hip_graph(capi, oracle, shape, want):
+@pytest.mark.parametrize("shape,want,workspace,warm", [
+    ((1024, 1024, 1024), "", False, True),
+    ((64, 4096, 4096), "_SplitK", True, True),     # partials in the caller's workspace
+    ((64, 4096, 4096), "_SplitK", False, False),   # partials in the Plan's own buffer, first execution captured
+])
+def test_plan_replays_in_a_hip_graph(capi, oracle, shape, want, workspace, warm):
     m, n, k = shape
     a, b, c = rnd((m, k), 1).cuda(), rnd((k, n), 2).cuda(), rnd((m, n), 3).cuda()
     d = torch.empty(m, n, device="cuda")
     plan = capi.plan_for(a, b, c, d, 1.5, -0.5)
     name = plan.name(0)
     assert name.endswith(want) if want else not name.endswith("_SplitK"), plan.names()
-    # Split-k Primitives write their partial tiles to the caller's workspace here.
     ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    wsa = (ws.data_ptr(), ws.numel()) if workspace else (0, 0)
     side = torch.cuda.Stream()
-    with torch.cuda.stream(side):
-        plan.execute(0, side.cuda_stream, ws.data_ptr(), ws.numel())  # warm-up outside the capture
-    torch.cuda.synchronize()
+    if warm:
+        with torch.cuda.stream(side):
+            plan.execute(0, side.cuda_stream, *wsa)  # warm-up outside the capture
+        torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=side):
-        plan.execute(0, side.cuda_stream, ws.data_ptr(), ws.numel())
+        plan.execute(0, side.cuda_stream, *wsa)
     for rep in range(3):
         a.copy_(rnd((m, k), 10 + rep).cuda())
         d.fill_(float("nan"))
@@ -92,27 +96,19 @@ def check_grouped(oracle, a, b, d, m_list, k, what):
 def test_grouped_plan_on_a_second_stream(capi, oracle):
     plan, a, b, d, m_list, k, keep = grouped_plan(capi)
     s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
-    plan.execute(0, s1.cuda_stream)  # uploads the table
+    plan.execute(0, s1.cuda_stream)
+    s1.synchronize()
+    check_grouped(oracle, a, b, d, m_list, k, "first stream")
     d.fill_(float("nan"))
     torch.cuda.synchronize()
-    plan.execute(0, s2.cuda_stream)  # no ordering with s1: the table must already be complete
+    plan.execute(0, s2.cuda_stream)
     s2.synchronize()
     check_grouped(oracle, a, b, d, m_list, k, "second stream")
 
 
-def test_grouped_plan_capture_after_first_execution(capi, oracle):
+def test_grouped_plan_first_execution_is_captured(capi, oracle):
     plan, a, b, d, m_list, k, keep = grouped_plan(capi)
     side = torch.cuda.Stream()
-    scratch = torch.zeros(16, device="cuda")
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=side):
-        scratch.add_(1.0)  # keeps the captured graph non-empty
-        status = plan.execute_status(0, side.cuda_stream)
-    assert status == capi.UNSUPPORTED, status
-    assert "cannot be captured" in capi.last_message()
-    plan.execute(0, side.cuda_stream)  # eager first execution
-    side.synchronize()
-    check_grouped(oracle, a, b, d, m_list, k, "eager")
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=side):
         plan.execute(0, side.cuda_stream)
@@ -123,3 +119,40 @@ def test_grouped_plan_capture_after_first_execution(capi, oracle):
         graph.replay()
         torch.cuda.synchronize()
         check_grouped(oracle, a, b, d, m_list, k, ("replay", rep))
+
+
+def test_convenience_graph_survives_plan_cache_eviction(capi, oracle):
+    """ftrainGemm keeps up to 32 Plans per thread and destroys the least
+    recently used one beyond that.  A Plan it executed under capture is kept
+    instead: the graph's split-k kernels point at that Plan's partial buffer.
+    Warm up and capture on one stream, evict with 40 other problems, replay."""
+    m, n, k = 64, 4096, 4096
+    a, b = rnd((m, k), 31).cuda(), rnd((k, n), 32).cuda()
+    d = torch.empty(m, n, device="cuda")
+    al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+    views = (capi.matrix(a), capi.matrix(b), capi.matrix(None, [m, n]), capi.matrix(d), al.view, be.view)
+    side = torch.cuda.Stream()
+    assert capi.gemm_status(*views, stream=side.cuda_stream) == capi.SUCCESS  # warm-up: creates the cached Plan
+    side.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        assert capi.gemm_status(*views, stream=side.cuda_stream) == capi.SUCCESS
+    # 40 other problems on the same thread and stream push the captured Plan out of the cache.
+    for i in range(40):
+        mm = 8 + i
+        x, y, z = torch.ones(mm, 32, device="cuda"), torch.ones(32, 16, device="cuda"), torch.empty(mm, 16, device="cuda")
+        v = (capi.matrix(x), capi.matrix(y), capi.matrix(None, [mm, 16]), capi.matrix(z), al.view, be.view)
+        assert capi.gemm_status(*v, stream=side.cuda_stream) == capi.SUCCESS
+    side.synchronize()
+    # Memory freed by an evicted Plan would now be handed out again: fill some.
+    junk = [torch.full((1 << 20,), 7.0, device="cuda") for _ in range(8)]
+    for rep in range(3):
+        a.copy_(rnd((m, k), 40 + rep).cuda())
+        d.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = oracle.gemm_f64(a.cpu().numpy(), b.cpu().numpy(), None, 1.0, 0.0)
+        rep_ = oracle.tolerance_check(d.cpu().numpy(), ref, k)
+        assert rep_["ok"], (rep, rep_)
+    del junk

@@ -97,7 +97,8 @@ def run_case(capi, ops, oracle, kind, cd, m, n, k, la, lb, lcd=False, pad=0, wit
 @pytest.mark.parametrize("kind", ["bf16", "fp16"])
 @pytest.mark.parametrize("cd", ["fp32", "same"])
 @pytest.mark.parametrize("la,lb", list(itertools.product((False, True), (False, True))))
-@pytest.mark.parametrize("m,n,k,pad", [(256, 192, 160, 8), (129, 67, 37, 3), (384, 256, 1024, 0)])
+@pytest.mark.parametrize("m,n,k,pad", [(256, 192, 160, 8), (129, 67, 37, 3), (384, 256, 1024, 0),
+                                       (384, 200, 1024, 8)])  # last: n-edge tiles with no k tail (clamped columns)
 def test_half_every_primitive(capi, ops, oracle, kind, cd, la, lb, m, n, k, pad):
     run_case(capi, ops, oracle, kind, kind if cd == "same" else "fp32", m, n, k, la, lb, pad=pad)
 
