@@ -72,6 +72,7 @@ LIB_SOURCES = [
     "csrc/gemm/kernels_half_fp16_tt.hip",
     "csrc/gemm/kernels_gemv_half.hip",
     "csrc/api/c_api.cpp",
+    "csrc/api/scratch.hip",
 ]
 TESTING_SOURCES = ["csrc/api/testing_api.cpp"]
 

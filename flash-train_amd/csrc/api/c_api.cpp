@@ -17,6 +17,7 @@
 #include <flash_train/flash_train.h>
 
 #include "ft/handles.hpp"
+#include "ft/scratch.hpp"
 #include "ft/trace.hpp"
 
 namespace ftrain {
@@ -88,9 +89,12 @@ class ConveniencePlans {
   public:
     static constexpr std::size_t kCapacity = 32;
 
-    static ConveniencePlans& local() {
-        static thread_local ConveniencePlans cache;
-        return cache;
+    // One cache per thread for each convenience entry point: ftrainGemm's
+    // Plans are prepared (they own split-k buffers), ftrainGemmNoAlloc's are
+    // not.
+    static ConveniencePlans& local(bool no_alloc) {
+        static thread_local ConveniencePlans cache[2];
+        return cache[no_alloc ? 1 : 0];
     }
 
     // Host scalars must be readable fp32 values of rank 0 for the key.
@@ -186,6 +190,107 @@ bool streamCapturing(FTrainStream stream) {
         return false;
     }
     return status != hipStreamCaptureStatusNone;
+}
+
+// A Plan as ftrainPlanCreate makes it, minus Plan::prepare: no Primitive
+// acquires device memory of its own.
+FTrainStatus createUnpreparedPlan(FTrainPlan* plan, FTrainArgs args) {
+    return guarded([&] {
+        const auto engine = globalHandle().find(args->args.key());
+        if (!engine) raise(FTRAIN_STATUS_INTERNAL_ERROR, "OpsEngine registered for Args is unavailable");
+        *plan = new FTrainPlanStruct{engine->createPlan(args->args)};
+    });
+}
+
+FTrainStatus executeConvenience(FTrainPlan plan, void* workspace, uint64_t workspace_bytes, FTrainStream stream,
+                                const DeviceScratch* scratch) {
+    if (scratch == nullptr) return ftrainPlanExecutePrimitive(plan, 0, workspace, workspace_bytes, stream);
+    uint64_t index = 0;
+    const FTrainStatus s = guarded([&] {
+        const uint64_t n = plan->plan.size();
+        while (index < n && plan->plan.scratchBytes(index) > scratch->bytes) ++index;
+        if (index == n)
+            raise(FTRAIN_STATUS_UNSUPPORTED,
+                  "ftrainGemmNoAlloc: every Primitive of the Plan needs more than the %llu-byte device scratch "
+                  "array (Primitive 0, %s, needs %llu bytes)",
+                  static_cast<unsigned long long>(scratch->bytes), plan->plan.primitiveName(0),
+                  static_cast<unsigned long long>(plan->plan.scratchBytes(0)));
+    });
+    if (s != FTRAIN_STATUS_SUCCESS) return s;
+    return ftrainPlanExecutePrimitive(plan, index, scratch->memory, scratch->bytes, stream);
+}
+
+// The convenience path behind ftrainGemm and ftrainGemmNoAlloc.  With
+// `scratch` null (ftrainGemm) the Plan is made by ftrainPlanCreate and its
+// Primitive 0 runs.  With `scratch` set (ftrainGemmNoAlloc) the Plan is made
+// without preparation, so nothing is allocated on the device, and the first
+// Primitive in rank order whose scratch need fits the library's device
+// scratch array runs with that array as its workspace.
+FTrainStatus convenienceGemm(const FTrainStorageView* const views[6], FTrainNumericType compute_type, void* workspace,
+                             uint64_t workspace_bytes, FTrainStream stream, const DeviceScratch* scratch) {
+    const FTrainStorageView &a = *views[0], &b = *views[1], &c = *views[2], &d = *views[3], &alpha = *views[4],
+                            &beta = *views[5];
+    // One Ops for the Gemm Pattern per process, built through the staged API
+    // (reference src/api/gemm_api.cpp:28-49).
+    struct Entry {
+        FTrainOps ops = nullptr;
+        FTrainTensorId a{}, b{}, c{}, d{}, alpha{}, beta{};
+        FTrainGemmOpId gemm{};
+        FTrainStatus status = FTRAIN_STATUS_SUCCESS;
+    };
+    static const Entry entry = [] {
+        Entry e;
+        FTrainPattern p = nullptr;
+        FTrainStatus s  = ftrainPatternCreate(&p);
+        for (FTrainTensorId* id : {&e.a, &e.b, &e.c, &e.alpha, &e.beta, &e.d})
+            if (s == FTRAIN_STATUS_SUCCESS) s = ftrainPatternAddTensor(p, id);
+        if (s == FTRAIN_STATUS_SUCCESS) s = ftrainPatternAddGemm(p, &e.gemm, e.a, e.b, e.c, e.d, e.alpha, e.beta);
+        if (s == FTRAIN_STATUS_SUCCESS) s = ftrainOpsCreate(&e.ops, p);
+        if (p != nullptr) ftrainPatternDestroy(p);
+        e.status = s;
+        return e;
+    }();
+    if (entry.status != FTRAIN_STATUS_SUCCESS) return entry.status;
+
+    const bool no_alloc               = scratch != nullptr;
+    const bool cacheable              = !selectionCacheDisabled() && ConveniencePlans::describable(views);
+    int device                        = -1;
+    std::vector<uint64_t> key;
+    if (cacheable && hipGetDevice(&device) == hipSuccess) {
+        key = ConveniencePlans::describe(views, compute_type, device, stream);
+        if (FTrainPlan cached = ConveniencePlans::local(no_alloc).find(key)) {
+            if (streamCapturing(stream)) ConveniencePlans::local(no_alloc).markFrontCaptured();
+            return executeConvenience(cached, workspace, workspace_bytes, stream, scratch);
+        }
+    } else {
+        (void)hipGetLastError();
+    }
+
+    FTrainArgs args = nullptr;
+    FTrainPlan plan = nullptr;
+    FTrainStatus s  = ftrainArgsCreate(&args, entry.ops);
+    const std::pair<FTrainTensorId, const FTrainStorageView*> ports[] = {
+        {entry.a, &a}, {entry.b, &b}, {entry.c, &c}, {entry.d, &d}, {entry.alpha, &alpha}, {entry.beta, &beta}};
+    for (const auto& port : ports)
+        if (s == FTRAIN_STATUS_SUCCESS) s = ftrainArgsSetTensor(args, port.first, *port.second);
+    if (s == FTRAIN_STATUS_SUCCESS) s = ftrainArgsSetGemm(args, entry.gemm, compute_type);
+    if (s == FTRAIN_STATUS_SUCCESS) s = no_alloc ? createUnpreparedPlan(&plan, args) : ftrainPlanCreate(&plan, args);
+    if (s == FTRAIN_STATUS_SUCCESS) s = executeConvenience(plan, workspace, workspace_bytes, stream, scratch);
+    // Keep the failing step's diagnostic across the clean-up calls.
+    const Result failure = s != FTRAIN_STATUS_SUCCESS ? lastResult() : Result{};
+    if (plan != nullptr) {
+        if (s == FTRAIN_STATUS_SUCCESS && !key.empty()) {
+            ConveniencePlans::local(no_alloc).insert(std::move(key), plan);  // the cache now owns it
+            if (streamCapturing(stream)) ConveniencePlans::local(no_alloc).markFrontCaptured();
+        } else if (s == FTRAIN_STATUS_SUCCESS && streamCapturing(stream)) {
+            retire(plan);
+        } else {
+            ftrainPlanDestroy(plan);
+        }
+    }
+    if (args != nullptr) ftrainArgsDestroy(args);
+    if (s != FTRAIN_STATUS_SUCCESS) lastResult() = failure;
+    return s;
 }
 
 }  // namespace
@@ -416,67 +521,19 @@ FTrainStatus ftrainGemm(FTrainStorageView a, FTrainStorageView b, FTrainStorageV
                         FTrainStorageView alpha, FTrainStorageView beta, FTrainNumericType compute_type,
                         void* workspace, uint64_t workspace_bytes, FTrainStream stream) {
     TraceRange trace("ftrainGemm");
-    // One Ops for the Gemm Pattern per process, built through the staged API
-    // (reference src/api/gemm_api.cpp:28-49).
-    struct Entry {
-        FTrainOps ops = nullptr;
-        FTrainTensorId a{}, b{}, c{}, d{}, alpha{}, beta{};
-        FTrainGemmOpId gemm{};
-        FTrainStatus status = FTRAIN_STATUS_SUCCESS;
-    };
-    static const Entry entry = [] {
-        Entry e;
-        FTrainPattern p = nullptr;
-        FTrainStatus s  = ftrainPatternCreate(&p);
-        for (FTrainTensorId* id : {&e.a, &e.b, &e.c, &e.alpha, &e.beta, &e.d})
-            if (s == FTRAIN_STATUS_SUCCESS) s = ftrainPatternAddTensor(p, id);
-        if (s == FTRAIN_STATUS_SUCCESS) s = ftrainPatternAddGemm(p, &e.gemm, e.a, e.b, e.c, e.d, e.alpha, e.beta);
-        if (s == FTRAIN_STATUS_SUCCESS) s = ftrainOpsCreate(&e.ops, p);
-        if (p != nullptr) ftrainPatternDestroy(p);
-        e.status = s;
-        return e;
-    }();
-    if (entry.status != FTRAIN_STATUS_SUCCESS) return entry.status;
-
     const FTrainStorageView* views[6] = {&a, &b, &c, &d, &alpha, &beta};
-    const bool cacheable              = !selectionCacheDisabled() && ConveniencePlans::describable(views);
-    int device                        = -1;
-    std::vector<uint64_t> key;
-    if (cacheable && hipGetDevice(&device) == hipSuccess) {
-        key = ConveniencePlans::describe(views, compute_type, device, stream);
-        if (FTrainPlan cached = ConveniencePlans::local().find(key)) {
-            if (streamCapturing(stream)) ConveniencePlans::local().markFrontCaptured();
-            return ftrainPlanExecutePrimitive(cached, 0, workspace, workspace_bytes, stream);
-        }
-    } else {
-        (void)hipGetLastError();
-    }
+    return convenienceGemm(views, compute_type, workspace, workspace_bytes, stream, nullptr);
+}
 
-    FTrainArgs args = nullptr;
-    FTrainPlan plan = nullptr;
-    FTrainStatus s  = ftrainArgsCreate(&args, entry.ops);
-    const std::pair<FTrainTensorId, const FTrainStorageView*> ports[] = {
-        {entry.a, &a}, {entry.b, &b}, {entry.c, &c}, {entry.d, &d}, {entry.alpha, &alpha}, {entry.beta, &beta}};
-    for (const auto& port : ports)
-        if (s == FTRAIN_STATUS_SUCCESS) s = ftrainArgsSetTensor(args, port.first, *port.second);
-    if (s == FTRAIN_STATUS_SUCCESS) s = ftrainArgsSetGemm(args, entry.gemm, compute_type);
-    if (s == FTRAIN_STATUS_SUCCESS) s = ftrainPlanCreate(&plan, args);
-    if (s == FTRAIN_STATUS_SUCCESS) s = ftrainPlanExecutePrimitive(plan, 0, workspace, workspace_bytes, stream);
-    // Keep the failing step's diagnostic across the clean-up calls.
-    const Result failure = s != FTRAIN_STATUS_SUCCESS ? lastResult() : Result{};
-    if (plan != nullptr) {
-        if (s == FTRAIN_STATUS_SUCCESS && !key.empty()) {
-            ConveniencePlans::local().insert(std::move(key), plan);  // the cache now owns it
-            if (streamCapturing(stream)) ConveniencePlans::local().markFrontCaptured();
-        } else if (s == FTRAIN_STATUS_SUCCESS && streamCapturing(stream)) {
-            retire(plan);
-        } else {
-            ftrainPlanDestroy(plan);
-        }
-    }
-    if (args != nullptr) ftrainArgsDestroy(args);
-    if (s != FTRAIN_STATUS_SUCCESS) lastResult() = failure;
-    return s;
+FTrainStatus ftrainGemmNoAlloc(FTrainStorageView a, FTrainStorageView b, FTrainStorageView c, FTrainStorageView d,
+                               FTrainStorageView alpha, FTrainStorageView beta, FTrainNumericType compute_type,
+                               FTrainStream stream) {
+    TraceRange trace("ftrainGemmNoAlloc");
+    DeviceScratch scratch{};
+    const FTrainStatus s = guarded([&] { scratch = deviceScratch(); });
+    if (s != FTRAIN_STATUS_SUCCESS) return s;
+    const FTrainStorageView* views[6] = {&a, &b, &c, &d, &alpha, &beta};
+    return convenienceGemm(views, compute_type, nullptr, 0, stream, &scratch);
 }
 
 }  // extern "C"

@@ -100,6 +100,7 @@ class Plan {
     FTrainDeviceId device() const noexcept { return device_; }
     const char* primitiveName(uint64_t index) const { return at(index).name(); }
     uint64_t requiredWorkspaceBytes(uint64_t index) const { return at(index).requiredWorkspaceBytes(); }
+    uint64_t scratchBytes(uint64_t index) const { return at(index).scratchBytes(); }
 
     // Runs every Primitive's prepare() (Primitive 0 as the default slot).
     void prepare();

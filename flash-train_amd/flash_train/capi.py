@@ -46,6 +46,10 @@ EXPORTED_SYMBOLS = (
     "ftrainPlanGetPrimitiveRequiredWorkspaceBytes", "ftrainPlanExecutePrimitive",
     "ftrainGemm",
 )
+# The reference's 29 entry points plus ftrainGemmNoAlloc, which has no
+# reference counterpart (for callers that cannot allocate device memory).
+REFERENCE_SYMBOLS = EXPORTED_SYMBOLS
+EXPORTED_SYMBOLS = REFERENCE_SYMBOLS + ("ftrainGemmNoAlloc",)
 
 
 class StorageView(ctypes.Structure):
@@ -100,6 +104,7 @@ def _declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         "ftrainPlanGetPrimitiveRequiredWorkspaceBytes": (st, [_H, c_uint64, POINTER(c_uint64)]),
         "ftrainPlanExecutePrimitive": (st, [_H, c_uint64, c_void_p, c_uint64, c_void_p]),
         "ftrainGemm": (st, [StorageView] * 6 + [c_uint8, c_void_p, c_uint64, c_void_p]),
+        "ftrainGemmNoAlloc": (st, [StorageView] * 6 + [c_uint8, c_void_p]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -340,6 +345,12 @@ def gemm_status(a: View, b: View, c: View, d: View, alpha: View, beta: View, com
     """ftrainGemm (the convenience entry point); returns the status."""
     return (l or lib()).ftrainGemm(a.sv, b.sv, c.sv, d.sv, alpha.sv, beta.sv, compute_type, workspace or None,
                                    workspace_bytes, stream or None)
+
+
+def gemm_no_alloc_status(a: View, b: View, c: View, d: View, alpha: View, beta: View, compute_type: int = FP32,
+                         stream: int = 0, l: Optional[ctypes.CDLL] = None) -> int:
+    """ftrainGemmNoAlloc (ftrainGemm with split-k partials in the library's device scratch array)."""
+    return (l or lib()).ftrainGemmNoAlloc(a.sv, b.sv, c.sv, d.sv, alpha.sv, beta.sv, compute_type, stream or None)
 
 
 def plan_for(a: torch.Tensor, b: torch.Tensor, c: Optional[torch.Tensor], d: torch.Tensor, alpha: float,

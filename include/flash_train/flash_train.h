@@ -27,6 +27,25 @@ FTRAIN_API FTrainStatus ftrainGemm(FTrainStorageView a, FTrainStorageView b, FTr
                                    FTrainStorageView alpha, FTrainStorageView beta, FTrainNumericType compute_type,
                                    void* workspace, uint64_t workspace_bytes, FTrainStream stream);
 
+/*
+ * ftrainGemm without device allocation.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.
+ *
+ * Same operands, result and errors as ftrainGemm, minus the workspace: a
+ * split-k Primitive keeps its partial tiles in the library's fixed device
+ * scratch array (32 MiB per GPU, held from library load until the process
+ * ends) and no call allocates or frees device memory.  The Primitive run is
+ * the first in the Plan's rank order whose partial tiles fit the array
+ * (Primitive 0 whenever it fits); UNSUPPORTED when none fits.  Every call on
+ * one GPU shares that GPU's array: calls that may overlap on one GPU (other
+ * streams, other threads) race and must be serialised by the caller.
+ * Nothing in the array needs to start at zero.
+ */
+FTRAIN_API FTrainStatus ftrainGemmNoAlloc(FTrainStorageView a, FTrainStorageView b, FTrainStorageView c,
+                                          FTrainStorageView d, FTrainStorageView alpha, FTrainStorageView beta,
+                                          FTrainNumericType compute_type, FTrainStream stream);
+
 #ifdef __cplusplus
 }
 #endif
