@@ -71,6 +71,7 @@ LIB_SOURCES = [
     "csrc/gemm/kernels_half_fp16_nt.hip",
     "csrc/gemm/kernels_half_fp16_tt.hip",
     "csrc/gemm/kernels_gemv_half.hip",
+    "csrc/gemm/kernels_deepk.hip",
     "csrc/api/c_api.cpp",
     "csrc/api/scratch.hip",
 ]

@@ -217,7 +217,9 @@ FTrainStatus executeConvenience(FTrainPlan plan, void* workspace, uint64_t works
                   static_cast<unsigned long long>(plan->plan.scratchBytes(0)));
     });
     if (s != FTRAIN_STATUS_SUCCESS) return s;
-    return ftrainPlanExecutePrimitive(plan, index, scratch->memory, scratch->bytes, stream);
+    // The scratch array's split-k arrival counters are 0 (zero at load, left
+    // zero by every launch), so no clearing launch is needed.
+    return guarded([&] { plan->plan.execute(index, scratch->memory, scratch->bytes, stream, true); });
 }
 
 // The convenience path behind ftrainGemm and ftrainGemmNoAlloc.  With

@@ -13,7 +13,7 @@ namespace {
 // The 16-bit efficiencies are set by hand so that the ranking matches measured timings from
 // 1024^3 to 8192^3 in every layout (the 64x64 tile loses to 128x128 from 1024^3 on, 128x128
 // to 256x256 from 3072^3 on) and in grouped MoE shapes with 8 and 64 experts.
-constexpr SplitKind N = SplitKind::kNone, P = SplitKind::kPartial;
+constexpr SplitKind N = SplitKind::kNone, P = SplitKind::kPartial, F = SplitKind::kFused;
 constexpr FTrainNumericType FP32 = FTRAIN_NUMERIC_TYPE_FP32, BF16 = FTRAIN_NUMERIC_TYPE_BF16,
                             FP16 = FTRAIN_NUMERIC_TYPE_FP16;
 constexpr VariantInfo kInfo[] = {
@@ -43,6 +43,7 @@ constexpr VariantInfo kInfo[] = {
     {"Fp32Gemv", kGemvRows, kGemvPassCols, 1, 1024, 1, true, N, true, false, false, 0, FP32, 256.0, 0},
     {"Fp32Gemv_SplitK", kGemvRows, kGemvCols, 1, 256, 8, true, P, true, false, false, 0, FP32, 256.0, 0},
     {"Fp32Gemv_Unaligned_SplitK", kGemvRows, kGemvCols, 1, 256, 8, false, P, true, false, false, 0, FP32, 256.0, 0},
+    {"Fp32Mfma16Gemm_64x64_DeepK", 64, 64, 32, 256, 1, true, F, false, false, false, 0.66, FP32, 256.0, 0.66},
     {"Fp32Gemm", 64, 64, 16, 256, 2, false, N, false, true, true, 0.2, FP32, 256.0, 0.2},
     {"Bf16MfmaGemm_256x256", 256, 256, 64, 512, 1, true, N, false, false, true, 0.6, BF16, 4096.0, 0.6},
     {"Bf16MfmaGemm_128x128", 128, 128, 64, 256, 2, true, N, false, false, true, 0.4, BF16, 4096.0, 0.4},

@@ -35,7 +35,16 @@ namespace {
 constexpr double kClockPerMicro = 2.4e3;  // peak engine clock (MHz)
 constexpr double kHbmBytesPerMicro = 8.0e6 * 0.8;  // sustained HBM bytes per microsecond
 constexpr double kLaunchMicros = 4.0;
-constexpr double kPoolMicros      = 2.0;  // stream-ordered workspace acquire + release
+constexpr double kPoolMicros      = 2.0;  // dependency gap before the reduction kernel (fitted)
+// The deep-k kernel (SplitKind::kFused): ramp of its single round, and the
+// tile's last workgroup storing, counting and gathering the partial tiles
+// (measured on MI355X: 3.7 us at 4 splits, 11-12 us at 16; the per-split
+// figure is set so that the kernel loses to the split-k tiles at 16 splits,
+// as measured: 64x1024x16384 33.9 against 31.1 us, 256x256x65536 89.8
+// against 80.0).
+constexpr double kFusedRampMicros     = 1.5;
+constexpr double kFusedGatherMicros   = 2.2;
+constexpr double kFusedPerSplitMicros = 0.9;
 // Fixed cost per round of resident workgroups (operand prologue, epilogue
 // stores, the ramp of the first stages); fitted with the catalog efficiencies.
 constexpr double kRoundMicros     = 8.2;
@@ -87,6 +96,13 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
         serial_us = 4.0 * m * n * (double(splits) + (has_c ? 2.0 : 1.0)) / kHbmBytesPerMicro;
         launch += kLaunchMicros + kPoolMicros;
     }
+    if (vi.split == SplitKind::kFused && splits > 1) {
+        // Partial tiles written and read once, plus the last workgroup's
+        // store / count / gather, after the tile's other workgroups.
+        const double tiles = double(ceilDiv(s.m, vi.bm) * ceilDiv(s.n, vi.bn));
+        bytes += 2.0 * 4.0 * tiles * vi.bm * vi.bn * double(splits);
+        serial_us = kFusedGatherMicros + kFusedPerSplitMicros * (double(splits) - 1.0);
+    }
     if (vi.gemv) {
         // Too few waves cannot reach the HBM peak; about four per CU do
         // (measured with the one-pass kernel: 1024 waves over 256 CUs stream
@@ -110,7 +126,8 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
     // SIMT FMAs run at half the matrix rate without packed FP32.
     const double cu_rate   = vi.flop_per_clk * kClockPerMicro * residentEfficiency(vi, per_cu) * (vi.simt ? 0.5 : 1.0);
     const double rounds    = double(ceilDiv(per_cu, uint64_t(vi.occupancy)));
-    const double compute   = double(per_cu) * 2.0 * vi.bm * vi.bn * depth / cu_rate + rounds * kRoundMicros;
+    const double per_round = vi.split == SplitKind::kFused ? kFusedRampMicros : kRoundMicros;
+    const double compute   = double(per_cu) * 2.0 * vi.bm * vi.bn * depth / cu_rate + rounds * per_round;
     return std::max(compute, bytes / kHbmBytesPerMicro) + serial_us + launch;
 }
 
@@ -122,7 +139,23 @@ uint32_t chooseSplits(Variant v, const GemmShape& s, int cus) {
     const uint64_t min_depth = vi.gemv ? kMinGemvDepth : kMinSplitDepth;
     uint64_t most            = std::min<uint64_t>(1024, s.k / min_depth);
     if (vi.split == SplitKind::kPartial && s.m * s.n > 0)
-        most = std::min<uint64_t>(most, kMaxPartialBytes / (s.m * s.n * sizeof(float)));
+        most = std::min<uint64_t>(most, (kMaxPartialBytes - kCounterBytes) / (s.m * s.n * sizeof(float)));
+    if (vi.split == SplitKind::kFused) {
+        // One split is a plain whole-k launch; more only while the partial
+        // tiles fit the cap.
+        const uint64_t tile_bytes = ceilDiv(s.m, vi.bm) * ceilDiv(s.n, vi.bn) * vi.bm * vi.bn * sizeof(float);
+        most = std::min<uint64_t>(most, (kMaxPartialBytes - kCounterBytes) / std::max<uint64_t>(tile_bytes, 1));
+        uint64_t best = 1;
+        double best_t = modelMicros(vi, s, false, cus, 1);
+        for (uint64_t sp = 2; sp <= most; sp *= 2) {
+            const double t = modelMicros(vi, s, false, cus, sp);
+            if (t < best_t * 0.999) {
+                best_t = t;
+                best   = sp;
+            }
+        }
+        return static_cast<uint32_t>(best);
+    }
     if (vi.gemv && most < 2) return 1;  // the skinny kernel also runs unsplit
     if (most < 2 || s.m == 0 || s.n == 0) return 0;
     // Smallest modelled time over powers of two in [2, most] (ties: fewer splits).

@@ -406,6 +406,7 @@ const void* kernelFor(Variant v, bool ta, bool tb) {
         case Variant::kGemvS: return reinterpret_cast<const void*>(&gemv_splitk<true, false>);
         case Variant::kGemvUS: return reinterpret_cast<const void*>(&gemv_splitk<false, false>);
         case Variant::kSimt: return reinterpret_cast<const void*>(&simt_gemm);
+        case Variant::kDeepK64x64: return deepkKernel();
         default: return layoutKernel<false, false>(v);
     }
 }

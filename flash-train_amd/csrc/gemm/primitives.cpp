@@ -119,6 +119,11 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
                   static_cast<unsigned long long>(partial_bytes_));
         }
         owned_.reset(q, [](void* x) { (void)hipFree(x); });
+        // The arrival counters start at 0; every launch leaves them 0.
+        if (hipMemset(q, 0, gemm::kCounterBytes) != hipSuccess) {
+            (void)hipGetLastError();
+            raise(FTRAIN_STATUS_INTERNAL_ERROR, "%s: clearing the split-k counters failed", info_->name);
+        }
     }
 
     Result isApplicable(const GemmProblem& p, const Constraints& constraints) const override {
@@ -165,6 +170,9 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
         if (info_->split == SplitKind::kPartial &&
             gemm::chooseSplits(v_, s, gemm::computeUnits(constraints.device())) == 0)
             return Result(FTRAIN_STATUS_UNSUPPORTED, "reduction depth too shallow to split");
+        if (info_->split == SplitKind::kFused &&
+            ceilDiv(s.m, info_->bm) * ceilDiv(s.n, info_->bn) > gemm::kMaxFusedTiles)
+            return Result(FTRAIN_STATUS_UNSUPPORTED, "more output tiles than the deep-k kernel's arrival counters");
         return Result{};
     }
 
@@ -219,8 +227,18 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
             grid_           = dim3(uint32_t(params_.tiles_m) * uint32_t(params_.tiles_n), 1, splits);
         }
         const uint64_t count = s.m * s.n;
+        if (info_->split == SplitKind::kFused) {
+            // One launch of tiles x splits workgroups (grid x); with splits >
+            // 1 the buffer holds the tiles' arrival counters, then the
+            // partial tiles.
+            const uint64_t tiles = uint64_t(params_.tiles_m) * uint64_t(params_.tiles_n);
+            grid_          = dim3(uint32_t(tiles * splits));
+            deepk_         = gemm::DeepKParams{params_, nullptr, nullptr, int32_t(splits)};
+            partial_bytes_ = splits > 1 ? gemm::kCounterBytes + uint64_t(splits) * tiles * info_->bm * info_->bn * sizeof(float) : 0;
+            fused_tiles_   = int32_t(tiles);
+        }
         if (info_->split == SplitKind::kPartial) {
-            partial_bytes_ = uint64_t(splits) * count * sizeof(float);
+            partial_bytes_ = gemm::kCounterBytes + uint64_t(splits) * count * sizeof(float);
             const int32_t cd_type = !cd_half ? gemm::kCdFp32
                                     : p.d().numericType() == FTRAIN_NUMERIC_TYPE_BF16 ? gemm::kCdBf16
                                                                                      : gemm::kCdFp16;
@@ -262,15 +280,45 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
                     raise(FTRAIN_STATUS_INVALID_ARGUMENT,
                           "%s requires a 16-byte aligned workspace of %llu bytes for its split-k partial tiles",
                           info_->name, static_cast<unsigned long long>(partial_bytes_));
-                params.d           = static_cast<float*>(ws);
-                half_params.d      = ws;
+                char* const partials = static_cast<char*>(ws) + gemm::kCounterBytes;
+                params.d           = reinterpret_cast<float*>(partials);
+                half_params.d      = partials;
                 ReduceParams red   = reduce_;
-                red.partials       = static_cast<const float*>(ws);
+                red.partials       = reinterpret_cast<const float*>(partials);
                 void* rargs[]      = {&red};
                 hipError_t e       = hipLaunchKernel(kernel_, grid_, block_, args, 0, r.stream);
                 if (e == hipSuccess)
                     e = hipLaunchKernel(gemm::reduceKernel(reduce_vec_), aux_grid_, dim3(256), rargs, 0, r.stream);
                 check(e, info_->name);
+                break;
+            }
+            case SplitKind::kFused: {
+                gemm::DeepKParams dp = deepk_;
+                void* dargs[]  = {&dp};
+                if (dp.splits > 1) {
+                    // Counters and partials in the buffer the kPartial case
+                    // would use.  A caller's workspace starts with arbitrary
+                    // contents: its counters are cleared first (a kernel,
+                    // not a memset, so the launch pair can be captured).
+                    const bool caller = r.workspace != nullptr && r.workspace_bytes >= partial_bytes_ &&
+                                        reinterpret_cast<uintptr_t>(r.workspace) % 16 == 0;
+                    void* ws = caller ? r.workspace : owned_.get();
+                    if (ws == nullptr)
+                        raise(FTRAIN_STATUS_INVALID_ARGUMENT,
+                              "%s requires a 16-byte aligned workspace of %llu bytes for its split-k partial tiles",
+                              info_->name, static_cast<unsigned long long>(partial_bytes_));
+                    dp.counters = static_cast<unsigned int*>(ws);
+                    dp.partials = reinterpret_cast<float*>(static_cast<char*>(ws) + gemm::kCounterBytes);
+                    if (caller && !r.counters_clear) {
+                        unsigned int* counters = dp.counters;
+                        int n                  = fused_tiles_;
+                        void* cargs[]          = {&counters, &n};
+                        check(hipLaunchKernel(gemm::deepkClearKernel(), dim3(uint32_t(ceilDiv(uint64_t(n), 256))),
+                                              dim3(256), cargs, 0, r.stream),
+                              info_->name);
+                    }
+                }
+                check(hipLaunchKernel(kernel_, grid_, block_, dargs, 0, r.stream), info_->name);
                 break;
             }
         }
@@ -298,6 +346,8 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
     HalfGemmParams half_params_{};
     WideParams wide_{};
     ReduceParams reduce_{};
+    gemm::DeepKParams deepk_{};
+    int32_t fused_tiles_ = 0;
     bool reduce_vec_        = false;
     uint64_t partial_bytes_ = 0;
     std::shared_ptr<void> owned_;  // split-k partials of Primitive 0 (shared by clones)

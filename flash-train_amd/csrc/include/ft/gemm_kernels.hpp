@@ -66,6 +66,17 @@ struct HalfGemmParams {
     int32_t cd_half;             // c and d hold the input type (else fp32)
 };
 
+// Parameters of the deep-k kernel (gemm/deepk_tile.hpp): the tile problem,
+// and for splits > 1 the partial slots (splits x tiles x 4096 floats) and
+// one arrival counter per output tile (0 when a launch starts; each launch
+// leaves them 0).
+struct DeepKParams {
+    GemmParams g;
+    float* partials;
+    unsigned int* counters;
+    int32_t splits;
+};
+
 // Grouped GEMM launch arguments: a device table of per-group parameters
 // (non-empty groups only) and each group's first workgroup, ascending.
 struct GroupedGemmArgs {
@@ -151,6 +162,11 @@ enum class Variant : int {
     // splitk_reduce in a fixed order.
     kGemvS,
     kGemvUS,
+    // Deep-k 64x64 tiles (v_mfma_f32_16x16x4_f32, 4 waves splitting k,
+    // operands streamed from global memory into registers), split-k reduced
+    // inside the launch by the last-arriving workgroup of each tile.
+    // Row-major a and b only.
+    kDeepK64x64,
     // General SIMT kernel with 64-bit indexing.
     kSimt,
     // bf16 and fp16 inputs, fp32 accumulation (v_mfma_f32_32x32x16_*):
@@ -178,6 +194,7 @@ constexpr int kHalfTiles = 4;
 enum class SplitKind : int {
     kNone,     // one workgroup owns each output tile's whole reduction
     kPartial,  // partial tiles to a workspace, then splitk_reduce (fixed order)
+    kFused,    // partial tiles to a workspace, summed by the tile's last workgroup in the same launch
 };
 
 struct VariantInfo {
@@ -198,6 +215,14 @@ struct VariantInfo {
 
 // Largest split-k workspace (partial tiles) a Primitive will use.
 constexpr uint64_t kMaxPartialBytes = 256ull << 20;
+
+// Every split-k buffer (a Plan's own, a caller's workspace, the device
+// scratch array) starts with this many bytes of per-tile arrival counters
+// for the kFused kernels; partial tiles follow.  The split kernels of every
+// kind leave the region alone, so a buffer shared by several Primitives
+// keeps its counters.
+constexpr uint64_t kCounterBytes = 16384;
+constexpr uint64_t kMaxFusedTiles = kCounterBytes / 4;
 
 const VariantInfo& info(Variant v);
 
@@ -252,5 +277,7 @@ const void* groupedHalfKernelFp16TN(int which);
 const void* groupedHalfKernelFp16NT(int which);
 const void* groupedHalfKernelFp16TT(int which);
 const void* reduceKernel(bool vec);      // split-k reduction (ReduceParams)
+const void* deepkKernel();              // kDeepK64x64 (DeepKParams)
+const void* deepkClearKernel();         // zeroes (unsigned*, int n) arrival counters
 
 }  // namespace ftrain::gemm

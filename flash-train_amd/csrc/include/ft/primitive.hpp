@@ -27,6 +27,10 @@ struct Resources {
     void* workspace;
     uint64_t workspace_bytes;
     FTrainStream stream;
+    // The workspace's split-k arrival counters are known to be 0 (the
+    // library's device scratch array: zero at load, left zero by every
+    // launch).  A caller's workspace has arbitrary contents.
+    bool counters_clear = false;
 };
 
 // Everything outside the Problem that can change a selection.  Encoded into
@@ -107,7 +111,9 @@ class Plan {
 
     // Device check (calling thread's device must be the Plan's), index check,
     // then the Primitive's workspace check and launch.
-    void execute(uint64_t index, void* workspace, uint64_t workspace_bytes, FTrainStream stream);
+    // `counters_clear`: see Resources.
+    void execute(uint64_t index, void* workspace, uint64_t workspace_bytes, FTrainStream stream,
+                 bool counters_clear = false);
 
   private:
     PrimitiveBase& at(uint64_t index) const;

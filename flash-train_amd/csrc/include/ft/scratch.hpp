@@ -14,11 +14,13 @@ struct DeviceScratch {
 };
 
 // Bytes of the array on every device (fixed at build time).
-constexpr uint64_t kDeviceScratchBytes = 32ull << 20;
+constexpr uint64_t kDeviceScratchBytes = 64ull << 20;
 
 // The array on the calling thread's current device.  The first call on a
 // device looks its address up (hipGetSymbolAddress, with that device
-// current) and keeps it; nothing is allocated.  INTERNAL_ERROR when HIP
+// current) and keeps it; nothing is allocated.  The array starts with the
+// split-k arrival counters (kCounterBytes, zero at load); every kernel
+// leaves them zero, and no kernel writes partial tiles over them.  INTERNAL_ERROR when HIP
 // fails.  Every use on one device shares the array: executions that
 // overlap on one device race.
 DeviceScratch deviceScratch();

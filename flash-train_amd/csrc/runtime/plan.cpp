@@ -31,13 +31,14 @@ PrimitiveBase& Plan::at(uint64_t index) const {
     return *primitives_[index];
 }
 
-void Plan::execute(uint64_t index, void* workspace, uint64_t workspace_bytes, FTrainStream stream) {
+void Plan::execute(uint64_t index, void* workspace, uint64_t workspace_bytes, FTrainStream stream,
+                   bool counters_clear) {
     const FTrainDeviceId current = getCurrentDeviceId();
     if (current != device_)
         raise(FTRAIN_STATUS_INVALID_ARGUMENT,
                         "Plan was created for device %d but the calling thread uses device %d", int(device_),
                         int(current));
-    at(index).execute(Resources{workspace, workspace_bytes, stream});
+    at(index).execute(Resources{workspace, workspace_bytes, stream, counters_clear});
 }
 
 }  // namespace ftrain

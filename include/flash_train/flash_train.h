@@ -34,7 +34,7 @@ FTRAIN_API FTrainStatus ftrainGemm(FTrainStorageView a, FTrainStorageView b, FTr
  *
  * Same operands, result and errors as ftrainGemm, minus the workspace: a
  * split-k Primitive keeps its partial tiles in the library's fixed device
- * scratch array (32 MiB per GPU, held from library load until the process
+ * scratch array (64 MiB per GPU, held from library load until the process
  * ends) and no call allocates or frees device memory.  The Primitive run is
  * the first in the Plan's rank order whose partial tiles fit the array
  * (Primitive 0 whenever it fits); UNSUPPORTED when none fits.  Every call on

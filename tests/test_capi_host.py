@@ -542,21 +542,23 @@ def test_strided_alignment_rules(tlib, tops):
 
 def test_split_k_primitives_report_their_partial_bytes(tlib, tops):
     """Without Plan preparation (the host hook skips it) every split-k
-    Primitive states its partial-tile bytes as required workspace: a whole
-    number of m x n fp32 slices, at least two, within the 256 MiB cap.  Whole-k
-    Primitives need none."""
+    Primitive states its workspace: 16 KiB of arrival counters, then a whole
+    number (at least two) of m x n fp32 partial slices (the _SplitK kernels)
+    or of 64 x 64 partial tiles per output tile (the _DeepK kernel), within
+    the 256 MiB cap.  Whole-k Primitives need none."""
     m, n, k = 64, 4096, 4096
     st, msg, plan = plan_status(tlib, tops, V([m, k]), V([k, n]), V([m, n], None), V([m, n]))
     assert st == c.SUCCESS, msg
     split = 0
     for i, name in enumerate(plan.names()):
         w = plan.workspace_bytes(i)
-        if name.endswith("SplitK"):
+        unit = m * n * 4 if name.endswith("SplitK") else 4096 * 4 * ((m + 63) // 64) * ((n + 63) // 64)
+        if name.endswith(("SplitK", "DeepK")):
             split += 1
-            assert w % (m * n * 4) == 0 and 2 <= w // (m * n * 4) and w <= 256 << 20, (name, w)
+            assert (w - 16384) % unit == 0 and 2 <= (w - 16384) // unit and w <= 256 << 20, (name, w)
         else:
             assert w == 0, (name, w)
-    assert split >= 2
+    assert split >= 3 and plan.names()[0] == "Fp32Mfma16Gemm_64x64_DeepK", plan.names()
     plan.close()
 
 
@@ -601,8 +603,8 @@ def test_finder_choices_for_the_baseline_configs(tlib):
     assert rank(tlib, 4096, 4096, 4096, with_c=True)[0].startswith("Fp32Mfma16Gemm_")
     # 2048^3: the 16x16 256x64 / 64x256 tiles (141.7 / 142.5) beat split-k (170+) and 256x128 (268).
     assert rank(tlib, 2048, 2048, 2048)[0] in ("Fp32Mfma16Gemm_256x64", "Fp32Mfma16Gemm_64x256")
-    # 1024^3: whole-k 64x64 (29.9) against the best split-k tile (38.5).
-    assert rank(tlib, 1024, 1024, 1024)[0] == "Fp32MfmaGemm_64x64"
+    # 1024^3: the deep-k tile unsplit (25.3) against whole-k 64x64 (29.9) and split-k (33.8+).
+    assert rank(tlib, 1024, 1024, 1024)[0] == "Fp32Mfma16Gemm_64x64_DeepK"
     # GEMV: the one-pass kernel (37.8 us) against split-k plus its reduction (47.6 us).
     assert rank(tlib, 1, 8192, 8192)[0] == "Fp32Gemv"
     # It also wins with 128 (1x4096x8192: 24.8 against 39.2 us) and 64 workgroups of 16 waves
@@ -610,10 +612,13 @@ def test_finder_choices_for_the_baseline_configs(tlib):
     assert rank(tlib, 1, 4096, 8192)[0] == "Fp32Gemv"
     assert rank(tlib, 2, 2048, 4096)[0] == "Fp32Gemv"
     assert rank(tlib, 1, 1024, 8192)[0] == "Fp32Gemv_SplitK"
-    # Deep or skinny: split-k on the 16x16 skinny tiles (88.3, 34.9, 33.6).
+    # Skinny: the deep-k tile with 4 splits reduced in the launch (28.9 / 30.7) against
+    # split-k plus a reduction (31.9 / 31.5).  Deep k with 16 or more splits: split-k
+    # tiles (256x256x65536: 80.0-88.7 against 89.8; 64x1024x16384: 31.1 against 33.9).
     assert rank(tlib, 256, 256, 65536)[0] == "Fp32Mfma16Gemm_256x64_SplitK"
-    assert rank(tlib, 64, 4096, 4096)[0] == "Fp32Mfma16Gemm_64x256_SplitK"
-    assert rank(tlib, 4096, 64, 4096)[0] == "Fp32Mfma16Gemm_256x64_SplitK"
+    assert rank(tlib, 64, 1024, 16384)[0] == "Fp32Mfma16Gemm_64x256_SplitK"
+    assert rank(tlib, 64, 4096, 4096)[0] == "Fp32Mfma16Gemm_64x64_DeepK"
+    assert rank(tlib, 4096, 64, 4096)[0] == "Fp32Mfma16Gemm_64x64_DeepK"
     # Odd sizes: no 128-bit variant applies.
     odd = rank(tlib, 127, 97, 33)
     assert odd and all(("Unaligned" in n) or n == "Fp32Gemm" for n in odd)

@@ -354,7 +354,7 @@ def test_caller_workspace_is_used_for_split_k(capi, ops, oracle):
     d = torch.empty(m, n, device="cuda")
     plan = capi.plan_for(a_h.cuda(), b_h.cuda(), None, d, 1.0, 0.0, ops)
     names = plan.names()
-    split = [i for i, nm in enumerate(names) if nm.endswith("_SplitK")]
+    split = [i for i, nm in enumerate(names) if nm.endswith(("_SplitK", "_DeepK"))]
     assert len(split) >= 2, names
     assert plan.workspace_bytes(0) == 0
     ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
@@ -364,7 +364,7 @@ def test_caller_workspace_is_used_for_split_k(capi, ops, oracle):
         if i == 0:
             assert need == 0
         else:
-            assert need > 0 and need % (m * n * 4) == 0, (names[i], need)
+            assert need > 16384, (names[i], need)  # arrival counters, then partial tiles
             assert plan.execute_status(i, s) == capi.INVALID_ARGUMENT
             assert "workspace" in capi.last_message()
             assert plan.execute_status(i, s, ws.data_ptr(), need - 1) == capi.INVALID_ARGUMENT
@@ -382,18 +382,20 @@ def test_split_k_is_deterministic(capi, ops):
     a, b = torch.randn(m, k, generator=g).cuda(), torch.randn(k, n, generator=g).cuda()
     d = torch.empty(m, n, device="cuda")
     plan = capi.plan_for(a, b, None, d, 1.0, 0.0, ops)
-    assert plan.name(0).endswith("_SplitK"), plan.names()
-    # Every MFMA split-k Primitive reduces its partial tiles in a fixed order.
+    assert plan.name(0).endswith(("_SplitK", "_DeepK")), plan.names()
+    # Every MFMA split-k Primitive reduces its partial tiles in a fixed order;
+    # the deep-k kernel's last-arriving workgroup too, whichever one it is
+    # (more runs: the arrival order changes from run to run).
     s = torch.cuda.current_stream().cuda_stream
-    split = [i for i, nm in enumerate(plan.names()) if nm.endswith("_SplitK") and "Mfma" in nm]
-    assert len(split) >= 4, plan.names()
+    split = [i for i, nm in enumerate(plan.names()) if nm.endswith(("_SplitK", "_DeepK")) and "Mfma" in nm]
+    assert len(split) >= 4 and any(plan.name(i).endswith("_DeepK") for i in split), plan.names()
     for i in split:
         outs = []
-        for _ in range(3):
+        for _ in range(12 if plan.name(i).endswith("_DeepK") else 3):
             plan.execute(i, s)
             torch.cuda.synchronize()
             outs.append(d.clone())
-        assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2]), plan.name(i)
+        assert all(torch.equal(outs[0], o) for o in outs[1:]), plan.name(i)
 
 
 def test_skinny_gemv_is_deterministic(capi, ops, oracle):
@@ -417,7 +419,7 @@ def test_skinny_gemv_is_deterministic(capi, ops, oracle):
             plan.execute(i, s)
             torch.cuda.synchronize()
             outs.append(d.clone())
-        assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2]), plan.name(i)
+        assert all(torch.equal(outs[0], o) for o in outs[1:]), plan.name(i)
         rep = oracle.tolerance_check(outs[0].cpu().numpy(), ref, k)
         assert rep["ok"], (plan.name(i), rep)
 
@@ -451,3 +453,43 @@ def test_one_pass_gemv(capi, ops, oracle, m, n, k, col_a):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
     rep = oracle.tolerance_check(outs[0].cpu().numpy(), ref, k)
     assert rep["ok"], rep
+
+
+@pytest.mark.parametrize("m,n,k,with_c", [
+    (64, 4096, 4096, False),    # BASELINE 5a shape: 4 splits reduced in the launch
+    (4096, 64, 4096, True),     # 5b shape, with c
+    (100, 200, 4100, True),     # m, n edge tiles, a k tail of 4 (k % 32 != 0)
+    (8, 36, 12, False),         # one tile, a k tail only (no whole slice)
+    (130, 260, 16388, False),   # many splits, every edge
+    (256, 256, 65536, True),    # BASELINE 5c shape with c
+])
+def test_deep_k_kernel(capi, ops, oracle, m, n, k, with_c):
+    """Fp32Mfma16Gemm_64x64_DeepK on edges and tails, with its partials in the
+    Plan's own buffer and in a caller workspace full of garbage (the arrival
+    counters are cleared before the launch); repeated runs are bit-identical
+    whichever workgroup of a tile arrives last."""
+    g = torch.Generator().manual_seed(m + n + k)
+    a_h, b_h = torch.randn(m, k, generator=g), torch.randn(k, n, generator=g)
+    c_h = torch.randn(m, n, generator=g) if with_c else None
+    alpha, beta = 0.75, (-1.5 if with_c else 0.0)
+    ref = oracle.gemm_f64(a_h, b_h, c_h, alpha, beta)
+    d = torch.empty(m, n, device="cuda")
+    plan = capi.plan_for(a_h.cuda(), b_h.cuda(), None if c_h is None else c_h.cuda(), d, alpha, beta, ops)
+    names = plan.names()
+    i = names.index("Fp32Mfma16Gemm_64x64_DeepK")
+    s = torch.cuda.current_stream().cuda_stream
+    need = plan.workspace_bytes(i)
+    ws = torch.full((max(need, 16) // 4 + 64,), -1, dtype=torch.int32, device="cuda")  # counters read 0xffffffff
+    outs = []
+    for run in range(6):
+        d.fill_(float("nan"))
+        if need and run % 2:
+            plan.execute(i, s, ws.data_ptr(), ws.numel() * 4)
+        else:
+            plan.execute(i, s)
+        torch.cuda.synchronize()
+        outs.append(d.clone())
+    rep = oracle.tolerance_check(outs[0].cpu().numpy(), ref, k)
+    assert rep["ok"], (names[i], need, rep)
+    assert rep["max_abs_err"] <= 1e-2 * rep["bound"], rep  # far inside the bar, not just under it
+    assert all(torch.equal(outs[0], o) for o in outs[1:]), names[i]

@@ -34,8 +34,10 @@ def rnd(shape, seed):
 
 @pytest.mark.parametrize("shape,want,workspace,warm", [
     ((1024, 1024, 1024), "", False, True),
-    ((64, 4096, 4096), "_SplitK", True, True),     # partials in the caller's workspace
-    ((64, 4096, 4096), "_SplitK", False, False),   # partials in the Plan's own buffer, first execution captured
+    ((64, 4096, 4096), "_DeepK", True, True),      # partials in the caller's workspace (counters cleared first)
+    ((64, 4096, 4096), "_DeepK", False, False),    # partials in the Plan's own buffer, first execution captured
+    ((64, 1024, 16384), "_SplitK", True, True),    # the split-k kernel + reduction pair
+    ((64, 1024, 16384), "_SplitK", False, False),
 ])
 def test_plan_replays_in_a_hip_graph(capi, oracle, shape, want, workspace, warm):
     m, n, k = shape
@@ -43,17 +45,19 @@ def test_plan_replays_in_a_hip_graph(capi, oracle, shape, want, workspace, warm)
     d = torch.empty(m, n, device="cuda")
     plan = capi.plan_for(a, b, c, d, 1.5, -0.5)
     name = plan.name(0)
-    assert name.endswith(want) if want else not name.endswith("_SplitK"), plan.names()
+    idx = next((i for i, nm in enumerate(plan.names()) if nm.endswith(want)), None) if want else 0
+    assert idx is not None, plan.names()
+    name = plan.name(idx)
     ws = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
     wsa = (ws.data_ptr(), ws.numel()) if workspace else (0, 0)
     side = torch.cuda.Stream()
     if warm:
         with torch.cuda.stream(side):
-            plan.execute(0, side.cuda_stream, *wsa)  # warm-up outside the capture
+            plan.execute(idx, side.cuda_stream, *wsa)  # warm-up outside the capture
         torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=side):
-        plan.execute(0, side.cuda_stream, *wsa)
+        plan.execute(idx, side.cuda_stream, *wsa)
     for rep in range(3):
         a.copy_(rnd((m, k), 10 + rep).cuda())
         d.fill_(float("nan"))
