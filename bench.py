@@ -214,6 +214,87 @@ def run_grouped(args, a_h, b_h, c_h, cfg) -> None:
     }), flush=True)
 
 
+# BASELINE configurations timed after the headline (BASELINE.json configs[0..4]):
+# name -> steps on one cached Plan (configs[3] asks for 100 iterations per MLP shape).
+CONFIG_STEPS = {
+    "readme_128x96x64": 200,
+    "square_4096_beta": 50,
+    "mlp_fwd": 100,
+    "mlp_dgrad": 100,
+    "skinny_64x4096x4096": 200,
+    "skinny_4096x64x4096": 200,
+    "splitk_256x256x65536": 200,
+    "gemv_1x8192x8192": 200,
+    "odd_127x97x33": 200,
+}
+
+
+def time_steps(plan, index: int, stream, steps: int, warmup: int) -> dict:
+    """Per-step HIP events on the launch stream: mean and median step time (ms)."""
+    import torch
+
+    h = stream.cuda_stream
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            plan.execute(index, h)
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        ev[0].record(stream)
+        for i in range(steps):
+            plan.execute(index, h)
+            ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+    per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+    return {"mean_ms": ev[0].elapsed_time(ev[-1]) / steps, "median_ms": per[steps // 2]}
+
+
+def parity_rows(oracle, a_h, b_h, c_h, cfg, d, rows_wanted: int = 64) -> dict:
+    """fp64 check of sampled rows (all rows when m is small) against the north-star bar, and how far
+    inside it the result is (a subtle pipeline slip would show as a ratio far above the usual 1e-3)."""
+    import numpy as np
+    import torch
+
+    m = cfg["m"]
+    rows = np.arange(m) if m <= rows_wanted else np.sort(np.random.default_rng(1).choice(m, size=rows_wanted, replace=False))
+    ref = oracle.sampled_rows_f64(a_h.float(), b_h.float(), c_h, cfg["alpha"], cfg["beta"], rows)
+    rep = oracle.tolerance_check(d[torch.as_tensor(rows).cuda()].cpu().numpy(), ref, cfg["k"])
+    ratio = rep["max_abs_err"] / rep["bound"] if rep["bound"] > 0 else 0.0
+    return {"rows_checked": int(len(rows)), "max_abs_err": rep["max_abs_err"], "bound": rep["bound"],
+            "err_over_bound": ratio, "ok": bool(rep["ok"] and ratio <= 1e-2)}
+
+
+def run_config(name: str, steps: int) -> dict:
+    """One BASELINE config on one cached Plan (Primitive 0): median step time, rate, roofline, parity."""
+    import torch
+
+    import flash_train.capi as capi
+    from oracle import oracle
+
+    a_h, b_h, c_h, cfg = oracle.seeded_inputs(name)
+    m, n, k = cfg["m"], cfg["n"], cfg["k"]
+    a, b = a_h.cuda(), b_h.cuda()
+    c = c_h.cuda() if c_h is not None else None
+    d = torch.empty(m, n, device="cuda")
+    plan = capi.plan_for(a, b, c, d, cfg["alpha"], cfg["beta"])
+    t = time_steps(plan, 0, torch.cuda.Stream(), steps, warmup=max(3, steps // 20))
+    ms = t["median_ms"]
+    flops = 2.0 * m * n * k
+    alg_bytes = 4.0 * (m * k + k * n + m * n * (2 if c is not None else 1))
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbs = alg_bytes / (ms * 1e-3) / 1e9
+    hbm_bound = flops / alg_bytes < FP32_MATRIX_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+    out = {"workload": name, "m": m, "n": n, "k": k, "c": c is not None, "primitive": plan.name(0),
+           "steps": steps, "median_ms": round(ms, 5), "mean_ms": round(t["mean_ms"], 5),
+           "tflops": round(tflops, 3), "gbs": round(gbs, 1),
+           "roofline": {"bound": "hbm" if hbm_bound else "mfma",
+                        "frac": round(gbs / HBM_PEAK_GBS if hbm_bound else tflops / FP32_MATRIX_PEAK_TFLOPS, 4),
+                        "traffic": traffic_from_profiles(name)},
+           "parity": parity_rows(oracle, a_h, b_h, c_h, cfg, d)}
+    del a, b, c, d, plan
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -231,6 +312,8 @@ def main() -> None:
     ap.add_argument("--grouped", type=int, default=0, metavar="E",
                     help="grouped GEMM (GroupedABCDGemm): the workload's m rows split unevenly over E experts, "
                          "each with its own k x n weight (mixture-of-experts forward)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other BASELINE configs (the `configs` key of the JSON line)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 device copies of 256 MiB (the known-size kernel that scales the PMC "
                          "FETCH_SIZE / WRITE_SIZE counters into bytes)")
@@ -341,9 +424,18 @@ def main() -> None:
         "roofline": roofline,
         "plan_overhead": overhead,
         "parity": {"rows_checked": int(len(rows)), "max_abs_err": rep["max_abs_err"], "bound": rep["bound"],
-                   "ok": rep["ok"]},
+                   "err_over_bound": rep["max_abs_err"] / rep["bound"] if rep["bound"] > 0 else 0.0,
+                   "ok": bool(rep["ok"] and rep["max_abs_err"] <= 1e-2 * rep["bound"])},
         "wall_s_timed": round(wall, 3),
     }
+    if not args.no_configs and not half and args.layout == "nn" and args.workload == "square_8192":
+        del a, b, c, d, plan
+        torch.cuda.empty_cache()
+        configs = []
+        for name, steps in CONFIG_STEPS.items():
+            log(f"config {name}")
+            configs.append(run_config(name, steps))
+        result["configs"] = configs
     if not args.no_cpu and not half:
         result["cpu_baseline"] = cpu_baseline(a_h, b_h, cfg["alpha"], cfg["beta"], args.cpu_budget)
         result["cpu_torch_matmul"] = torch_cpu_matmul(a_h, b_h, min(args.cpu_budget, 5.0))

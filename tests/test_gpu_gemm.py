@@ -284,23 +284,38 @@ def test_baseline_config_full_check(capi, ops, oracle, name):
         torch.cuda.synchronize()
         rep = oracle.tolerance_check(d.cpu().numpy(), ref, cfg["k"])
         assert rep["ok"], (name, pname, rep)
+        # Far inside the bar, not just under it: a dropped or repeated k slice
+        # or a misplaced partial tile lands near or above it.
+        assert rep["max_abs_err"] <= 1e-2 * rep["bound"], (name, pname, rep)
 
 
-@pytest.mark.parametrize("name", ["square_4096_beta", "square_8192", "mlp_fwd", "mlp_dgrad"])
-def test_baseline_config_sampled_rows(capi, ops, oracle, name):
-    """Large configs: fp64 reference on 64 seeded rows x all columns (primitive 0)."""
+@pytest.mark.parametrize("name,every", [("square_4096_beta", True), ("square_8192", False), ("mlp_fwd", False),
+                                        ("mlp_dgrad", True)])
+def test_baseline_config_sampled_rows(capi, ops, oracle, name, every):
+    """Large configs: fp64 reference on 64 seeded rows x all columns.  Primitive 0
+    everywhere; every Primitive of the Plan on the deepest config (MLP dgrad, k =
+    14336) and on the one with c (4096^3, beta 0.5), so a Primitive another box,
+    an environment filter or a Finder change could promote is checked at full
+    size too.  Each result must also sit far inside the bar (1e-2 of it)."""
     a_h, b_h, c_h, cfg = oracle.seeded_inputs(name)
     rows = np.sort(np.random.default_rng(2026).choice(cfg["m"], size=64, replace=False))
     ref = oracle.sampled_rows_f64(a_h, b_h, c_h, cfg["alpha"], cfg["beta"], rows)
     d = torch.empty(cfg["m"], cfg["n"], device="cuda")
     plan = capi.plan_for(a_h.cuda(), b_h.cuda(), c_h.cuda() if c_h is not None else None, d, cfg["alpha"],
                          cfg["beta"], ops)
-    print(name, plan.names())
+    names = plan.names()
+    print(name, names)
+    for i in (range(len(names)) if every else [0]):
+        d.fill_(float("nan"))
+        plan.execute(i, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        got = d[torch.as_tensor(rows).cuda()].cpu().numpy()
+        rep = oracle.tolerance_check(got, ref, cfg["k"])
+        assert rep["ok"], (name, names[i], rep)
+        assert rep["max_abs_err"] <= 1e-2 * rep["bound"], (name, names[i], rep)
+        assert not torch.isnan(d).any().item(), (name, names[i], "left part of d unwritten")
     plan.execute(0, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
-    got = d[torch.as_tensor(rows).cuda()].cpu().numpy()
-    rep = oracle.tolerance_check(got, ref, cfg["k"])
-    assert rep["ok"], (name, plan.name(0), rep)
     # Size-independent property over the whole output: row sums equal a @ (b @ 1).
     ones = torch.ones(cfg["n"], 1, dtype=torch.float64)
     row_sums = d.double().cpu() @ ones
