@@ -20,11 +20,11 @@ constexpr VariantInfo kInfo[] = {
     {"Fp32Mfma16Gemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, true, 0.905, FP32, 256.0, 0.905},
     {"Fp32Mfma16Gemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, true, 0.73, FP32, 256.0, 0.73},
     {"Fp32Mfma16Gemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, true, 0.895, FP32, 256.0, 0.855},
-    {"Fp32Mfma16Gemm_256x128_SplitK", 256, 128, 16, 256, 2, true, P, false, false, true, 0.855, FP32, 256.0, 0.82},
+    {"Fp32Mfma16Gemm_256x128_SplitK", 256, 128, 16, 256, 2, true, P, false, false, true, 0.90, FP32, 256.0, 0.87},
     {"Fp32Mfma16Gemm_128x256", 128, 256, 16, 256, 2, true, N, false, false, true, 0.895, FP32, 256.0, 0.855},
-    {"Fp32Mfma16Gemm_64x256", 64, 256, 16, 256, 2, true, N, false, false, true, 0.865, FP32, 256.0, 0.915},
+    {"Fp32Mfma16Gemm_64x256", 64, 256, 16, 256, 2, true, N, false, false, true, 0.845, FP32, 256.0, 0.83},
     {"Fp32Mfma16Gemm_64x256_SplitK", 64, 256, 16, 256, 2, true, P, false, false, true, 0.80, FP32, 256.0, 0.85},
-    {"Fp32Mfma16Gemm_256x64", 256, 64, 16, 256, 2, true, N, false, false, true, 0.87, FP32, 256.0, 0.915},
+    {"Fp32Mfma16Gemm_256x64", 256, 64, 16, 256, 2, true, N, false, false, true, 0.85, FP32, 256.0, 0.83},
     {"Fp32Mfma16Gemm_256x64_SplitK", 256, 64, 16, 256, 2, true, P, false, false, true, 0.86, FP32, 256.0, 0.82},
     {"Fp32MfmaGemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, false, 0.86, FP32, 256.0, 0.86},
     {"Fp32MfmaGemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, false, 0.74, FP32, 256.0, 0.74},

@@ -45,6 +45,7 @@ constexpr double kPoolMicros      = 2.0;  // dependency gap before the reduction
 constexpr double kFusedRampMicros     = 1.5;
 constexpr double kFusedGatherMicros   = 2.2;
 constexpr double kFusedPerSplitMicros = 0.9;
+constexpr double kFusedStoreMicros    = 2.0;  // per round: a split workgroup's partial store and count
 // Fixed cost per round of resident workgroups (operand prologue, epilogue
 // stores, the ramp of the first stages); fitted with the catalog efficiencies.
 constexpr double kRoundMicros     = 8.2;
@@ -126,7 +127,10 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
     // SIMT FMAs run at half the matrix rate without packed FP32.
     const double cu_rate   = vi.flop_per_clk * kClockPerMicro * residentEfficiency(vi, per_cu) * (vi.simt ? 0.5 : 1.0);
     const double rounds    = double(ceilDiv(per_cu, uint64_t(vi.occupancy)));
-    const double per_round = vi.split == SplitKind::kFused ? kFusedRampMicros : kRoundMicros;
+    // The deep-k kernel runs one workgroup per CU: each round pays the ramp
+    // and, when split, its workgroups' partial-tile stores and arrival.
+    const double per_round = vi.split != SplitKind::kFused ? kRoundMicros
+                             : kFusedRampMicros + (splits > 1 ? kFusedStoreMicros : 0.0);
     const double compute   = double(per_cu) * 2.0 * vi.bm * vi.bn * depth / cu_rate + rounds * per_round;
     return std::max(compute, bytes / kHbmBytesPerMicro) + serial_us + launch;
 }
