@@ -115,7 +115,8 @@ def main() -> None:
         f"Dominant kernel `{a.title}`: **{kernel_us:.1f} µs** per timed step "
         f"({flops / kernel_us / 1e6:.1f} TFLOP/s, {100 * flops / kernel_us / 1e6 / FP32_PEAK:.1f}% of {FP32_PEAK}). "
         f"`bench.py` in the same profiled run (HIP events on the launch stream over the {steps} steps): "
-        f"**{step_us:.1f} µs** per step, primitive `{cfg['primitive']}`.",
+        f"**{step_us:.1f} µs** per step, primitive `{cfg['primitive']}`. Algorithmic bytes over the kernel time: "
+        f"{alg / kernel_us / 1e3:.1f} GB/s ({100 * alg / kernel_us / 1e3 / 8000:.1f}% of 8 TB/s).",
         "",
         "## HBM traffic and counters per dispatch (PMC)", "",
         "| FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes (scaled) | Algorithmic bytes | Ratio | MFMA busy | LDS bank conflicts / LDS active |",
