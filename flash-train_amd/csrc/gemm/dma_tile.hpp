@@ -1,0 +1,335 @@
+// BF16 / FP16 256x256 whole-tile kernel whose operands reach LDS by DMA
+// (global_load_lds_dwordx4) instead of through registers.  Device code only;
+// the per-type translation units kernels_half_dma_*.hip instantiate it.
+//
+// d = alpha * (a @ b) + beta * c, the same contract as the register-staged
+// tiles of half_tile.hpp (fp32 accumulation; c and d in fp32 or the input
+// type; with a null c the beta term is dropped).  Applicability, checked on
+// the host: m and n multiples of 256, k a multiple of 64, a and b 16-byte
+// aligned with leading dimensions multiples of 8 elements.
+//
+// Workgroup: 4 waves (one per SIMD), each a 128x128 block of the tile, as
+// 4x4 v_mfma_f32_32x32x16 blocks:
+//   A operand: lane l holds A[row l % 32][8 consecutive k]
+//   B operand: lane l holds B[the same 8 k][col l % 32]
+//   result   : lane l, register r holds D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]
+// In k-step s (16 k) lane half h = l / 32 takes k 16 s + 8 h .. 16 s + 8 h + 7.
+//
+// Stage = 64 k of both operands, 32 KiB each; two LDS stages (128 KiB).
+// One DMA instruction moves 64 lanes x 16 bytes into 1 KiB of LDS at
+// M0 + 16 * lane, each lane from its own global address, so a stage takes 32
+// instructions per operand, 8 per wave.  Each covers whole 128-byte lines:
+//   k-contiguous operand (row-major a, column-major b): 8 rows x 64 k, LDS
+//     [256 rows][64 k], 16-byte chunk c of row r at slot c ^ ((r >> 1) & 7);
+//     read with ds_read_b128 (one per operand);
+//   transposed operand (column-major a, row-major b): 2 k rows x 256, LDS
+//     [64 k][256], chunk c of k row kr at slot c ^ (4 (kr & 3)); read with
+//     ds_read_b64_tr_b16 (two per operand).
+// Both swizzles keep the reads free of bank conflicts (SQ_LDS_BANK_CONFLICT
+// reads 0 on MI355X).
+//
+// Pipeline of stage st in buffer X (stage st + 1 in Y), per wave:
+//   half 1: MFMAs on k 0..31 (registers) while reading k 32..63 of X;
+//   wait for this wave's LDS reads and DMAs, barrier: every wave is done
+//     with X, and stage st + 1 has landed in Y;
+//   half 2: MFMAs on k 32..63 while reading k 0..31 of Y and issuing the
+//     DMA of stage st + 2 into X.
+// A DMA has one stage of MFMAs (2048 MFMA cycles per wave) to land.  The
+// DMA is issued from inline assembly with M0 set in the same statement, so
+// the compiler's wait-count bookkeeping never sees it: every wait on it is
+// the explicit vmcnt in this file.  The compiler does not otherwise use M0
+// in this kernel (no LDS DMA builtins, no indexed register access: every
+// loop is unrolled).
+//
+// Measured (bf16 8192^3, fp32 d, same box and session): row-major a and b
+// 881 us against 994 us for the register-staged 256x256 tile; row-major a,
+// column-major b 875 against 916 us.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "ft/gemm_kernels.hpp"
+
+namespace ftrain::gemm::ddev {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+using u16 = unsigned short;
+
+constexpr int kTile = 256, kStageK = 64;
+constexpr int kStageElems = kTile * kStageK;  // one operand, one stage: 32 KiB
+
+template <bool BF16>
+__device__ __forceinline__ floatx16 mfma(u32x4 a, u32x4 b, floatx16 acc) {
+    if constexpr (BF16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       acc, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(halfx8, a), __builtin_bit_cast(halfx8, b),
+                                                      acc, 0, 0, 0);
+}
+
+template <bool BF16>
+__device__ __forceinline__ float to_float(u16 v) {
+    if constexpr (BF16)
+        return __builtin_bit_cast(float, static_cast<unsigned int>(v) << 16);
+    else
+        return static_cast<float>(__builtin_bit_cast(_Float16, v));
+}
+
+template <bool BF16>
+__device__ __forceinline__ u16 from_float(float v) {
+    if constexpr (BF16)
+        return __builtin_bit_cast(u16, static_cast<__bf16>(v));
+    else
+        return __builtin_bit_cast(u16, static_cast<_Float16>(v));
+}
+
+// 1 KiB DMA: lane l copies 16 bytes from sbase + voff(l) to LDS byte address lds + 16 l.
+__device__ __forceinline__ void dma_1k(unsigned voff, const void* sbase, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(sbase)
+                 : "memory", "m0");
+}
+
+// Output tile of workgroup `bid`: consecutive ids go to the 8 XCDs in turn,
+// so each XCD gets a contiguous run of tile ids, walked in bands of 8 tile
+// rows (a band's a panels stay in that XCD's L2 while its b panels stream).
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int tiles = tiles_m * tiles_n;
+    const int per   = tiles >> 3;
+    int t           = bid;
+    if (bid < (per << 3)) t = (bid & 7) * per + (bid >> 3);
+    constexpr int kBand = 8;
+    const int band_span = kBand * tiles_n;
+    const int band      = t / band_span;
+    const int first_m   = band * kBand;
+    const int band_rows = min(tiles_m - first_m, kBand);
+    const int within    = t - band * band_span;
+    tm                  = first_m + within % band_rows;
+    tn                  = within / band_rows;
+}
+
+// One operand's staging: where each DMA reads and how a wave reads its
+// MFMA operands back.  TR: the operand is transposed in memory (k rows).
+template <bool TR>
+struct Operand {
+    const char* base;  // tile origin (element 0 of its first row / k row)
+    unsigned voff;     // this lane's byte offset inside a DMA block
+    int64_t ld;        // leading dimension, elements
+
+    __device__ __forceinline__ void init(const u16* m, int64_t ld_, int origin, int wave, int lane) {
+        ld = ld_;
+        if constexpr (TR) {
+            // Block q = wave + 4 j holds k rows 2q, 2q + 1 (lane: row 2q + lane / 32); slot lane % 32
+            // holds 8-element chunk (lane % 32) ^ (4 (kr & 3)).  kr & 3 does not depend on j.
+            const int kr = 2 * wave + (lane >> 5), chunk = (lane & 31) ^ (4 * (kr & 3));
+            base         = reinterpret_cast<const char*>(m + origin);
+            voff         = static_cast<unsigned>((kr * ld + 8 * chunk) * 2);
+        } else {
+            // Block q = wave + 4 j holds rows 8q .. 8q + 7 (lane: row 8q + lane / 8); slot lane % 8
+            // holds k chunk (lane % 8) ^ ((row >> 1) & 7), which does not depend on j.
+            const int row = 8 * wave + (lane >> 3), chunk = (lane & 7) ^ ((row >> 1) & 7);
+            base          = reinterpret_cast<const char*>(m + (size_t)origin * ld);
+            voff          = static_cast<unsigned>((row * ld + 8 * chunk) * 2);
+        }
+    }
+    // DMA j (0..7) of this wave for stage st into the stage buffer at LDS byte address lds.
+    __device__ __forceinline__ void dma(int st, int j, unsigned lds, int wave) const {
+        const size_t off = TR ? ((size_t)st * kStageK + 8 * j) * ld : (size_t)32 * j * ld + (size_t)st * kStageK;
+        dma_1k(voff, base + off * 2, lds + (wave + 4 * j) * 1024);
+    }
+};
+
+template <bool BF16, bool TA, bool TB>
+__global__ __launch_bounds__(256, 1) void half_gemm_dma(HalfGemmParams p) {
+    constexpr bool A_TR = TA, B_TR = !TB;
+    __shared__ __attribute__((aligned(1024))) u16 As0[kStageElems];
+    __shared__ __attribute__((aligned(1024))) u16 Bs0[kStageElems];
+    __shared__ __attribute__((aligned(1024))) u16 As1[kStageElems];
+    __shared__ __attribute__((aligned(1024))) u16 Bs1[kStageElems];
+    const int tid = threadIdx.x, lane = tid & 63, li = lane & 31, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wrow = (wave >> 1) * 128, wcol = (wave & 1) * 128;
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * kTile, n0 = tn * kTile;
+    const int nst = p.k / kStageK;
+
+    Operand<A_TR> opa;
+    Operand<B_TR> opb;
+    opa.init(static_cast<const u16*>(p.a), p.lda, m0, wave, lane);
+    opb.init(static_cast<const u16*>(p.b), p.ldb, n0, wave, lane);
+    const unsigned la0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)As0;
+    const unsigned lb0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)Bs0;
+    const unsigned la1 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)As1;
+    const unsigned lb1 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)Bs1;
+
+    // Operand of k-step ks (0..3 in the stage) for rows (or columns) x .. x + 31.
+    const int tr_k = (lane & 15) >> 2, tr_x = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    auto rd_k = [&](const u16* T, int x, int ks) {  // k-contiguous
+        const int row = x + li, pos = (2 * ks + h) ^ ((row >> 1) & 7);
+        return *reinterpret_cast<const u32x4*>(T + row * kStageK + 8 * pos);
+    };
+    // Transposed: within each 16 lanes, lane 4j + e reads elements x + tr_x .. + 3 of k row kk + j;
+    // lane 4e + i receives element i of lanes e, 4 + e, 8 + e, 12 + e, i.e. 4 consecutive k of
+    // column x + lane % 32.  Part `part` covers k 16 ks + 8 h + 4 part .. + 3.
+    auto rd_t = [&](const u16* T, int x, int ks, int part) {
+        const int k = 16 * ks + 8 * h + 4 * part + tr_k, n = x + tr_x;
+        const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4i16*)(T + k * kTile + 8 * ((n >> 3) ^ (4 * (k & 3))) + (n & 7)));
+        return __builtin_bit_cast(u32x2, v);
+    };
+
+    floatx16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    // Operands of one half stage (32 k): [k-step][block].
+    u32x4 fa0[2][4], fb0[2][4], fa1[2][4], fb1[2][4];
+    constexpr int NRA = A_TR ? 16 : 8, NRB = B_TR ? 16 : 8, NR = NRA + NRB;
+    // LDS read r (0 .. NR-1) of half `hf`, ordered k-step major (A then B within a k-step), into (ga, gb).
+    auto read_one = [&](u32x4 (&ga)[2][4], u32x4 (&gb)[2][4], const u16* As, const u16* Bs, int hf, int r) {
+        const int s = r / (NR / 2), q = r % (NR / 2), ks = 2 * hf + s;
+        if (q < NRA / 2) {
+            if constexpr (A_TR) {
+                const u32x2 v = rd_t(As, wrow + 32 * (q >> 1), ks, q & 1);
+                ga[s][q >> 1][2 * (q & 1)]     = v[0];
+                ga[s][q >> 1][2 * (q & 1) + 1] = v[1];
+            } else {
+                ga[s][q] = rd_k(As, wrow + 32 * q, ks);
+            }
+        } else {
+            const int u = q - NRA / 2;
+            if constexpr (B_TR) {
+                const u32x2 v = rd_t(Bs, wcol + 32 * (u >> 1), ks, u & 1);
+                gb[s][u >> 1][2 * (u & 1)]     = v[0];
+                gb[s][u >> 1][2 * (u & 1) + 1] = v[1];
+            } else {
+                gb[s][u] = rd_k(Bs, wcol + 32 * u, ks);
+            }
+        }
+    };
+    // 32 MFMAs on (fa, fb); the NR reads of half hf of (As, Bs) into (ga, gb) and, with a true
+    // with_dma, the 16 DMAs of stage dma_st into (la, lb) are spread between them in a fixed order.
+    auto run_half = [&](u32x4 (&fa)[2][4], u32x4 (&fb)[2][4], u32x4 (&ga)[2][4], u32x4 (&gb)[2][4], const u16* As,
+                    const u16* Bs, int hf, auto with_dma, int dma_st, unsigned la, unsigned lb) {
+#pragma unroll
+        for (int t = 0; t < 32; ++t) {
+            acc[(t >> 2) & 3][t & 3] = mfma<BF16>(fa[t >> 4][(t >> 2) & 3], fb[t >> 4][t & 3], acc[(t >> 2) & 3][t & 3]);
+#pragma unroll
+            for (int r = 0; r < NR; ++r)
+                if ((r * 32) / NR == t) read_one(ga, gb, As, Bs, hf, r);
+            if constexpr (decltype(with_dma)::value) {
+                if (t & 1) {
+                    const int u = t >> 1;
+                    if (u & 1)
+                        opb.dma(dma_st, u >> 1, lb, wave);
+                    else
+                        opa.dma(dma_st, u >> 1, la, wave);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto read_half = [&](u32x4 (&ga)[2][4], u32x4 (&gb)[2][4], const u16* As, const u16* Bs, int hf) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) read_one(ga, gb, As, Bs, hf, r);
+    };
+
+    // Prologue: stages 0 and 1 in flight (8 + 8 DMAs per wave each); wait for stage 0.
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        opa.dma(0, j, la0, wave);
+        opb.dma(0, j, lb0, wave);
+    }
+    const int st1 = min(1, nst - 1);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        opa.dma(st1, j, la1, wave);
+        opb.dma(st1, j, lb1, wave);
+    }
+    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+    read_half(fa0, fb0, As0, Bs0, 0);
+
+    // Stages past the last reload the last one (harmless: nothing reads them).
+#define FT_DMA_PHASE(XA, XB, YA, YB, LXA, LXB, ST)                               \
+    run_half(fa0, fb0, fa1, fb1, XA, XB, 1, std::false_type{}, 0, 0u, 0u);                          \
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory"); \
+    run_half(fa1, fb1, fa0, fb0, YA, YB, 0, std::true_type{}, min((ST) + 2, nst - 1), LXA, LXB);
+    int st = 0;
+    for (; st + 1 < nst; st += 2) {
+        FT_DMA_PHASE(As0, Bs0, As1, Bs1, la0, lb0, st)
+        FT_DMA_PHASE(As1, Bs1, As0, Bs0, la1, lb1, st + 1)
+    }
+    // An odd stage count ends with one more stage in buffer 0 (a separate copy: leaving the
+    // loop between its two phases costs the register allocator the fragment double buffer).
+    if (st < nst) {
+        FT_DMA_PHASE(As0, Bs0, As1, Bs1, la0, lb0, st)
+    }
+#undef FT_DMA_PHASE
+    // The workgroup's LDS must not be released with a DMA still writing it.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    const float alpha = p.alpha, beta = p.beta;
+    auto epilogue = [&](auto c_tag, auto half_tag) {
+        constexpr bool HAS_C = decltype(c_tag)::value;
+        constexpr bool HALF  = decltype(half_tag)::value;
+#pragma unroll
+        for (int bi = 0; bi < 4; ++bi)
+#pragma unroll
+            for (int bj = 0; bj < 4; ++bj) {
+                const int col = n0 + wcol + 32 * bj + li;
+                float cv[16];
+                if constexpr (HAS_C) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const size_t ci = (size_t)(m0 + wrow + 32 * bi + 8 * (r / 4) + 4 * h + (r % 4)) * p.ldc + col;
+                        cv[r] = HALF ? to_float<BF16>(static_cast<const u16*>(p.c)[ci]) : static_cast<const float*>(p.c)[ci];
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const size_t di = (size_t)(m0 + wrow + 32 * bi + 8 * (r / 4) + 4 * h + (r % 4)) * p.ldd + col;
+                    float out       = alpha * acc[bi][bj][r];
+                    if constexpr (HAS_C) out += beta * cv[r];
+                    if constexpr (HALF)
+                        __builtin_nontemporal_store(from_float<BF16>(out), static_cast<u16*>(p.d) + di);
+                    else
+                        __builtin_nontemporal_store(out, static_cast<float*>(p.d) + di);
+                }
+            }
+    };
+    if (p.c != nullptr) {
+        if (p.cd_half)
+            epilogue(std::true_type{}, std::true_type{});
+        else
+            epilogue(std::true_type{}, std::false_type{});
+    } else {
+        if (p.cd_half)
+            epilogue(std::false_type{}, std::true_type{});
+        else
+            epilogue(std::false_type{}, std::false_type{});
+    }
+}
+
+// Kernel for one input type and operand orientation (ta: column-major a, tb: column-major b).
+template <bool BF16>
+const void* dmaKernel(bool ta, bool tb) {
+    if (ta) return tb ? reinterpret_cast<const void*>(&half_gemm_dma<BF16, true, true>)
+                      : reinterpret_cast<const void*>(&half_gemm_dma<BF16, true, false>);
+    return tb ? reinterpret_cast<const void*>(&half_gemm_dma<BF16, false, true>)
+              : reinterpret_cast<const void*>(&half_gemm_dma<BF16, false, false>);
+}
+
+}  // namespace ftrain::gemm::ddev

@@ -180,6 +180,10 @@ enum class Variant : int {
     kFp16Mfma128x128,
     kFp16Mfma128x128S,
     kFp16Mfma64x64U,
+    // bf16 / fp16 256x256 whole tiles with operands staged into LDS by DMA
+    // (global_load_lds_dwordx4): m, n multiples of 256, k a multiple of 64.
+    kBf16MfmaDma256x256,
+    kFp16MfmaDma256x256,
     // One-pass skinny-m kernels (m <= 8, row-major b) for bf16 / fp16 inputs.
     kBf16Gemv,
     kFp16Gemv,
@@ -258,6 +262,9 @@ const void* halfKernelFp16NN(int tile);
 const void* halfKernelFp16TN(int tile);
 const void* halfKernelFp16NT(int tile);
 const void* halfKernelFp16TT(int tile);
+// The DMA-staged 256x256 tiles per input type and operand orientation.
+const void* dmaKernelBf16(bool ta, bool tb);
+const void* dmaKernelFp16(bool ta, bool tb);
 // Grouped kernels: element type (FTRAIN_NUMERIC_TYPE_FP32 / BF16 / FP16),
 // tile (0 = 128x128 with 16-byte loads, 1 = 64x64 per-element, 2 = the
 // family's large tile: fp32 16x16x4 256x128, bf16/fp16 256x256; 3 = fp32

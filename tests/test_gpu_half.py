@@ -105,6 +105,41 @@ def test_half_every_primitive(capi, ops, oracle, kind, cd, la, lb, m, n, k, pad)
 
 @pytest.mark.parametrize("kind", ["bf16", "fp16"])
 @pytest.mark.parametrize("cd", ["fp32", "same"])
+@pytest.mark.parametrize("la,lb", list(itertools.product((False, True), (False, True))))
+@pytest.mark.parametrize("m,n,k,pad,with_c", [(256, 256, 64, 8, True), (512, 256, 192, 8, False),
+                                              (256, 512, 1024, 0, True)])
+def test_half_dma_tile(capi, ops, oracle, kind, cd, la, lb, m, n, k, pad, with_c):
+    # Whole 256x256 tiles with LDS staging by DMA: one stage (k = 64), an odd stage count (the
+    # tail copy of the pipeline) and a long even one, every operand orientation, NaN past each
+    # leading dimension's used extent.
+    names = run_case(capi, ops, oracle, kind, kind if cd == "same" else "fp32", m, n, k, la, lb, pad=pad,
+                     with_c=with_c, seed=k + pad)
+    assert f"{kind.capitalize()}MfmaGemm_256x256_Dma" in names, names
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+def test_half_dma_tile_exact_and_repeatable(capi, ops, kind):
+    # Integer inputs in [-8, 8] (exact in fp32 for this k): the DMA tile equals the integer
+    # product bit for bit, on a run after another shape (so the LDS held other data) and twice.
+    g = np.random.default_rng(5)
+    m, n, k = 512, 256, 320
+    a = g.integers(-8, 9, (m, k)).astype(np.float32)
+    b = g.integers(-8, 9, (k, n)).astype(np.float32)
+    exact = (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32)
+    at = torch.from_numpy(a).to(DT[kind]).cuda()
+    bt = torch.from_numpy(b).to(DT[kind]).cuda()
+    d = torch.empty(m, n, device="cuda")
+    plan = capi.plan_for(at, bt, None, d, 1.0, 0.0, ops)
+    i = plan.names().index(f"{kind.capitalize()}MfmaGemm_256x256_Dma")
+    for _ in range(2):
+        d.fill_(float("nan"))
+        plan.execute(i, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(d.cpu().numpy(), exact)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+@pytest.mark.parametrize("cd", ["fp32", "same"])
 @pytest.mark.parametrize("m,n,k,pad", [(1, 8192, 8192, 0), (2, 200, 1000, 8), (1, 64, 8, 0), (2, 4096, 2056, 0),
                                        (3, 64, 64, 0), (4, 128, 1024, 8), (5, 64, 64, 0)])
 def test_half_one_pass_gemv(capi, ops, oracle, kind, cd, m, n, k, pad):
