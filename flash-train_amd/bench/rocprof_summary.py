@@ -30,6 +30,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(os.path.dirname(HERE))
 FP32_PEAK = 157.3
+HALF_PEAK = 2500.0  # dense bf16 / fp16 MFMA, TFLOP/s
 
 
 def rows(path: str) -> list:
@@ -76,7 +77,9 @@ def main() -> None:
     cfg = bj["config"]
     m, n, k = cfg["m"], cfg["n"], cfg["k"]
     flops = 2.0 * m * n * k
-    alg = 4.0 * (m * k + k * n + m * n * (2 if cfg.get("c") else 1))
+    half = bj.get("dtype") in ("bf16", "fp16")
+    peak = HALF_PEAK if half else FP32_PEAK
+    alg = (2.0 if half else 4.0) * (m * k + k * n) + 4.0 * m * n * (2 if cfg.get("c") else 1)
     fetch = counters(os.path.join(a.dir, "F", "run_counter_collection.csv"), a.kernel)["FETCH_SIZE"]
     write = counters(os.path.join(a.dir, "W", "run_counter_collection.csv"), a.kernel)["WRITE_SIZE"]
     mc = counters(os.path.join(a.dir, "M", "run_counter_collection.csv"), a.kernel)
@@ -113,7 +116,7 @@ def main() -> None:
     lines += [
         "",
         f"Dominant kernel `{a.title}`: **{kernel_us:.1f} µs** per timed step "
-        f"({flops / kernel_us / 1e6:.1f} TFLOP/s, {100 * flops / kernel_us / 1e6 / FP32_PEAK:.1f}% of {FP32_PEAK}). "
+        f"({flops / kernel_us / 1e6:.1f} TFLOP/s, {100 * flops / kernel_us / 1e6 / peak:.1f}% of {peak}). "
         f"`bench.py` in the same profiled run (HIP events on the launch stream over the {steps} steps): "
         f"**{step_us:.1f} µs** per step, primitive `{cfg['primitive']}`. Algorithmic bytes over the kernel time: "
         f"{alg / kernel_us / 1e3:.1f} GB/s ({100 * alg / kernel_us / 1e3 / 8000:.1f}% of 8 TB/s).",
