@@ -441,7 +441,25 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
 template <int BM, int BN, int BK, int WM, int WN, int SPLIT, bool TA, bool TB, int MINB = 1, bool SIMPLE = false,
           int BAND = 4>
 __global__ __launch_bounds__(WM* WN * 64, MINB) void mfma16_gemm(GemmParams p) {
-    mfma16_gemm_tile<BM, BN, BK, WM, WN, SPLIT, TA, TB, MINB, SIMPLE, BAND>(p, blockIdx.x, blockIdx.z);
+    int bid = blockIdx.x, z = blockIdx.z;
+    if constexpr (SPLIT != kWhole) {
+        // Workgroups are dispatched in grid order (x fastest) and dealt to the 8 XCDs in turn, so
+        // the tiles of one k split would land on different XCDs and each fetch the split's
+        // shared operand slice into its own L2.  Renumber: the s-th workgroup on XCD x takes
+        // work item x * (total / 8) + s, items ordered split-major, so each XCD runs whole splits
+        // and every tile of a split reuses the slice from the same L2.
+        const int tiles = gridDim.x, total = tiles * gridDim.z;
+        // The tile index t is then handed to tile_of as the id whose XCD spreading yields t
+        // back, so the tiles a workgroup walks stay in tile_of's band order.
+        if ((total & 7) == 0) {
+            const int lin = blockIdx.x + tiles * blockIdx.z;
+            const int w   = (lin & 7) * (total >> 3) + (lin >> 3);
+            z             = w / tiles;
+            const int t   = w - z * tiles, per = tiles >> 3;
+            bid           = t < (per << 3) ? ((t % per) << 3) + t / per : t;
+        }
+    }
+    mfma16_gemm_tile<BM, BN, BK, WM, WN, SPLIT, TA, TB, MINB, SIMPLE, BAND>(p, bid, z);
 }
 
 // Index of the group that owns workgroup `bid`: the last g with
