@@ -1,12 +1,16 @@
-// BF16 / FP16 256x256 whole-tile kernel whose operands reach LDS by DMA
-// (global_load_lds_dwordx4) instead of through registers.  Device code only;
-// the per-type translation units kernels_half_dma_*.hip instantiate it.
+// BF16 / FP16 256x256 tile kernel whose operands reach LDS by DMA
+// (global_load_lds_dwordx4) instead of through registers, plain and grouped.
+// Device code only; the per-type translation units kernels_half_dma_*.hip
+// instantiate it.
 //
 // d = alpha * (a @ b) + beta * c, the same contract as the register-staged
 // tiles of half_tile.hpp (fp32 accumulation; c and d in fp32 or the input
 // type; with a null c the beta term is dropped).  Applicability, checked on
-// the host: m and n multiples of 256, k a multiple of 64, a and b 16-byte
-// aligned with leading dimensions multiples of 8 elements.
+// the host: k a multiple of 64 (no k tail: a DMA cannot zero-fill), a and b
+// 16-byte aligned with leading dimensions multiples of 8 elements and below
+// 2^23, c and d leading dimensions below 2^21 (32-bit offsets), contiguous
+// extents multiples of 8; m and n are free (edge tiles clamp their loads and
+// drop their out-of-matrix stores).
 //
 // Workgroup: 4 waves (one per SIMD), each a 128x128 block of the tile, as
 // 4x4 v_mfma_f32_32x32x16 blocks:
@@ -65,6 +69,9 @@ typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 using u16 = unsigned short;
 
 constexpr int kTile = 256, kStageK = 64;
+// Word 3 of a raw (untyped, stride 0) buffer resource on gfx9 parts: 32-bit data format, the range
+// check against num_records on every access.
+constexpr int kBufferConfig = 0x00020000;
 constexpr int kStageElems = kTile * kStageK;  // one operand, one stage: 32 KiB
 
 template <bool BF16>
@@ -117,39 +124,57 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
     tn                  = within / band_rows;
 }
 
-// One operand's staging: where each DMA reads and how a wave reads its
-// MFMA operands back.  TR: the operand is transposed in memory (k rows).
+// One operand's staging: where each DMA reads.  TR: the operand is
+// transposed in memory (k rows, its m or n extent contiguous).  Rows (or
+// columns) past the matrix edge are clamped onto its last row (column
+// group): they read valid memory and feed only outputs the epilogue does not
+// store.
 template <bool TR>
 struct Operand {
     const char* base;  // tile origin (element 0 of its first row / k row)
-    unsigned voff;     // this lane's byte offset inside a DMA block
     int64_t ld;        // leading dimension, elements
+    unsigned voff;     // TR: this lane's byte offset inside every DMA block
+    unsigned r8;       // k-contiguous: this lane's row inside DMA block 0
+    unsigned chunk16;  // k-contiguous: byte offset of this lane's 16-byte k chunk
+    unsigned last;     // k-contiguous: last row of the tile inside the matrix
+    unsigned ld2;      // k-contiguous: row stride in bytes (below 2^24)
 
-    __device__ __forceinline__ void init(const u16* m, int64_t ld_, int origin, int wave, int lane) {
+    // origin: the tile's first row (column); extent: rows (columns) in the matrix.
+    __device__ __forceinline__ void init(const u16* m, int64_t ld_, int origin, int extent, int wave, int lane) {
         ld = ld_;
         if constexpr (TR) {
             // Block q = wave + 4 j holds k rows 2q, 2q + 1 (lane: row 2q + lane / 32); slot lane % 32
-            // holds 8-element chunk (lane % 32) ^ (4 (kr & 3)).  kr & 3 does not depend on j.
+            // holds 8-element chunk (lane % 32) ^ (4 (kr & 3)).  kr & 3 does not depend on j.  The
+            // extent is a multiple of 8, so a clamped chunk is a whole one.
             const int kr = 2 * wave + (lane >> 5), chunk = (lane & 31) ^ (4 * (kr & 3));
-            base         = reinterpret_cast<const char*>(m + origin);
-            voff         = static_cast<unsigned>((kr * ld + 8 * chunk) * 2);
+            const int col = min(origin + 8 * chunk, extent - 8) - origin;
+            base          = reinterpret_cast<const char*>(m + origin);
+            voff          = static_cast<unsigned>((kr * ld + col) * 2);
         } else {
             // Block q = wave + 4 j holds rows 8q .. 8q + 7 (lane: row 8q + lane / 8); slot lane % 8
             // holds k chunk (lane % 8) ^ ((row >> 1) & 7), which does not depend on j.
-            const int row = 8 * wave + (lane >> 3), chunk = (lane & 7) ^ ((row >> 1) & 7);
-            base          = reinterpret_cast<const char*>(m + (size_t)origin * ld);
-            voff          = static_cast<unsigned>((row * ld + 8 * chunk) * 2);
+            r8      = 8 * wave + (lane >> 3);
+            chunk16 = 16 * ((lane & 7) ^ ((r8 >> 1) & 7));
+            last    = static_cast<unsigned>(min(extent - 1 - origin, kTile - 1));
+            ld2     = static_cast<unsigned>(2 * ld);
+            base    = reinterpret_cast<const char*>(m + (size_t)origin * ld);
         }
     }
     // DMA j (0..7) of this wave for stage st into the stage buffer at LDS byte address lds.
     __device__ __forceinline__ void dma(int st, int j, unsigned lds, int wave) const {
-        const size_t off = TR ? ((size_t)st * kStageK + 8 * j) * ld : (size_t)32 * j * ld + (size_t)st * kStageK;
-        dma_1k(voff, base + off * 2, lds + (wave + 4 * j) * 1024);
+        if constexpr (TR) {
+            dma_1k(voff, base + ((size_t)st * kStageK + 8 * j) * ld * 2, lds + (wave + 4 * j) * 1024);
+        } else {
+            // Row 32 j + r8 of the tile, clamped to the matrix (255 * ld2 < 2^32).
+            const unsigned row = min(r8 + 32u * j, last);
+            dma_1k(row * ld2 + chunk16, base + (size_t)st * kStageK * 2, lds + (wave + 4 * j) * 1024);
+        }
     }
 };
 
+// Output tile `bid` of p (tile_of order); the whole workgroup calls it.
 template <bool BF16, bool TA, bool TB>
-__global__ __launch_bounds__(256, 1) void half_gemm_dma(HalfGemmParams p) {
+__device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int bid) {
     constexpr bool A_TR = TA, B_TR = !TB;
     __shared__ __attribute__((aligned(1024))) u16 As0[kStageElems];
     __shared__ __attribute__((aligned(1024))) u16 Bs0[kStageElems];
@@ -159,14 +184,15 @@ __global__ __launch_bounds__(256, 1) void half_gemm_dma(HalfGemmParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wrow = (wave >> 1) * 128, wcol = (wave & 1) * 128;
     int tm, tn;
-    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    tile_of(bid, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * kTile, n0 = tn * kTile;
+    const int M = p.m, N = p.n;
     const int nst = p.k / kStageK;
 
     Operand<A_TR> opa;
     Operand<B_TR> opb;
-    opa.init(static_cast<const u16*>(p.a), p.lda, m0, wave, lane);
-    opb.init(static_cast<const u16*>(p.b), p.ldb, n0, wave, lane);
+    opa.init(static_cast<const u16*>(p.a), p.lda, m0, M, wave, lane);
+    opb.init(static_cast<const u16*>(p.b), p.ldb, n0, N, wave, lane);
     const unsigned la0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)As0;
     const unsigned lb0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)Bs0;
     const unsigned la1 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)As1;
@@ -282,32 +308,66 @@ __global__ __launch_bounds__(256, 1) void half_gemm_dma(HalfGemmParams p) {
     // The workgroup's LDS must not be released with a DMA still writing it.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+    // Epilogue through buffer loads and stores relative to the tile's corner.  The byte offset of
+    // an element splits into a per-lane part (4 h rows and lane column li) in the VGPR offset and
+    // a wave-uniform part (block, register) in the scalar offset.  An element outside the matrix
+    // (edge tiles: a grouped GEMM's last rows, any m or n not a multiple of 256) gets the lane
+    // offset 2^31, past the buffer's size (at most 2^31 - 1 bytes), so its c load returns 0 and
+    // its store is dropped by the hardware range check: no branches, one copy for whole and edge
+    // tiles.  ldc, ldd below 2^21 (checked on the host) keep every sum below 2^32.
     const float alpha = p.alpha, beta = p.beta;
     auto epilogue = [&](auto c_tag, auto half_tag) {
         constexpr bool HAS_C = decltype(c_tag)::value;
         constexpr bool HALF  = decltype(half_tag)::value;
+        constexpr unsigned ES = HALF ? 2 : 4;
+        const unsigned ldd = static_cast<unsigned>(p.ldd), ldc = static_cast<unsigned>(p.ldc);
+        const int rows_left = M - m0, cols_left = N - n0;
+        auto span = [&](uint64_t ld) {  // bytes from the tile's corner to the matrix's last element
+            const uint64_t b = ((uint64_t)(rows_left - 1) * ld + (uint64_t)cols_left) * ES;
+            return static_cast<int>(b < 0x7FFFFFFFull ? b : 0x7FFFFFFFull);
+        };
+        const __amdgpu_buffer_rsrc_t dres = __builtin_amdgcn_make_buffer_rsrc(
+            static_cast<char*>(p.d) + ((size_t)m0 * p.ldd + n0) * ES, 0, span(p.ldd), kBufferConfig);
+        __amdgpu_buffer_rsrc_t cres = dres;
+        if constexpr (HAS_C)
+            cres = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<char*>(static_cast<const char*>(p.c)) + ((size_t)m0 * p.ldc + n0) * ES, 0, span(p.ldc),
+                kBufferConfig);
+        const unsigned lane_d = (4 * h * ldd + li) * ES, lane_c = (4 * h * ldc + li) * ES;
+        constexpr unsigned kOut = 0x80000000u;
 #pragma unroll
         for (int bi = 0; bi < 4; ++bi)
 #pragma unroll
             for (int bj = 0; bj < 4; ++bj) {
-                const int col = n0 + wcol + 32 * bj + li;
+                const int col    = wcol + 32 * bj;  // wave-uniform block column
+                const bool colok = col + li < cols_left;
                 float cv[16];
                 if constexpr (HAS_C) {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const size_t ci = (size_t)(m0 + wrow + 32 * bi + 8 * (r / 4) + 4 * h + (r % 4)) * p.ldc + col;
-                        cv[r] = HALF ? to_float<BF16>(static_cast<const u16*>(p.c)[ci]) : static_cast<const float*>(p.c)[ci];
+                        const int row0 = wrow + 32 * bi + 8 * (r / 4) + (r % 4);  // row of lane half 0
+                        const bool ok  = colok && 4 * h < rows_left - row0;
+                        const int so   = static_cast<int>((row0 * ldc + col) * ES);
+                        if constexpr (HALF)
+                            cv[r] = to_float<BF16>(
+                                static_cast<u16>(__builtin_amdgcn_raw_buffer_load_b16(cres, ok ? lane_c : kOut, so, 0)));
+                        else
+                            cv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(cres, ok ? lane_c : kOut, so, 0));
                     }
                 }
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const size_t di = (size_t)(m0 + wrow + 32 * bi + 8 * (r / 4) + 4 * h + (r % 4)) * p.ldd + col;
-                    float out       = alpha * acc[bi][bj][r];
+                    const int row0 = wrow + 32 * bi + 8 * (r / 4) + (r % 4);
+                    const bool ok  = colok && 4 * h < rows_left - row0;
+                    const int so   = static_cast<int>((row0 * ldd + col) * ES);
+                    float out      = alpha * acc[bi][bj][r];
                     if constexpr (HAS_C) out += beta * cv[r];
+                    // Non-temporal (aux 2): d is not read again here.
                     if constexpr (HALF)
-                        __builtin_nontemporal_store(from_float<BF16>(out), static_cast<u16*>(p.d) + di);
+                        __builtin_amdgcn_raw_buffer_store_b16(from_float<BF16>(out), dres, ok ? lane_d : kOut, so, 2);
                     else
-                        __builtin_nontemporal_store(out, static_cast<float*>(p.d) + di);
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, out), dres, ok ? lane_d : kOut,
+                                                              so, 2);
                 }
             }
     };
@@ -324,7 +384,41 @@ __global__ __launch_bounds__(256, 1) void half_gemm_dma(HalfGemmParams p) {
     }
 }
 
+template <bool BF16, bool TA, bool TB>
+__global__ __launch_bounds__(256, 1) void half_gemm_dma(HalfGemmParams p) {
+    half_gemm_dma_tile<BF16, TA, TB>(p, blockIdx.x);
+}
+
+// Grouped GEMM over a device table of per-group parameters: the workgroup's
+// group is the last one whose first tile id is at most its own.  Group starts
+// are multiples of 8, so the group-local id keeps the hardware id's XCD;
+// ids past the group's tiles are padding and exit at once (before any
+// barrier, the whole workgroup).
+template <bool BF16, bool TA, bool TB>
+__global__ __launch_bounds__(256, 1) void grouped_half_gemm_dma(GroupedHalfArgs g) {
+    const int bid = blockIdx.x;
+    int lo = 0, hi = g.groups - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (g.tile_start[mid] <= bid)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    const HalfGemmParams p = g.params[lo];
+    const int local        = bid - g.tile_start[lo];
+    if (local >= p.tiles_m * p.tiles_n) return;
+    half_gemm_dma_tile<BF16, TA, TB>(p, local);
+}
+
 // Kernel for one input type and operand orientation (ta: column-major a, tb: column-major b).
+template <bool BF16>
+const void* groupedDmaKernel(bool ta, bool tb) {
+    if (ta) return tb ? reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, true, true>)
+                      : reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, true, false>);
+    return tb ? reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, false, true>)
+              : reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, false, false>);
+}
 template <bool BF16>
 const void* dmaKernel(bool ta, bool tb) {
     if (ta) return tb ? reinterpret_cast<const void*>(&half_gemm_dma<BF16, true, true>)

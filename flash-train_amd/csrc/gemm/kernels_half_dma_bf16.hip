@@ -5,4 +5,6 @@ namespace ftrain::gemm {
 
 const void* dmaKernelBf16(bool ta, bool tb) { return ddev::dmaKernel<true>(ta, tb); }
 
+const void* groupedDmaKernelBf16(bool ta, bool tb) { return ddev::groupedDmaKernel<true>(ta, tb); }
+
 }  // namespace ftrain::gemm

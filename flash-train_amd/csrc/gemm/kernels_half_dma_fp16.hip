@@ -5,4 +5,6 @@ namespace ftrain::gemm {
 
 const void* dmaKernelFp16(bool ta, bool tb) { return ddev::dmaKernel<false>(ta, tb); }
 
+const void* groupedDmaKernelFp16(bool ta, bool tb) { return ddev::groupedDmaKernel<false>(ta, tb); }
+
 }  // namespace ftrain::gemm

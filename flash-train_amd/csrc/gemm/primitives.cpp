@@ -166,11 +166,11 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
                     return Result(FTRAIN_STATUS_UNSUPPORTED, "a matrix address is not 16-byte aligned");
         }
         if ((v_ == Variant::kBf16MfmaDma256x256 || v_ == Variant::kFp16MfmaDma256x256) &&
-            (s.k == 0 || s.m % 256 != 0 || s.n % 256 != 0 || s.k % 64 != 0 || g.lda >= (int64_t(1) << 26) ||
-             g.ldb >= (int64_t(1) << 26)))
+            (s.k == 0 || s.k % 64 != 0 || g.lda >= (int64_t(1) << 23) || g.ldb >= (int64_t(1) << 23) ||
+             g.ldc >= (int64_t(1) << 21) || g.ldd >= (int64_t(1) << 21)))
             return Result(FTRAIN_STATUS_UNSUPPORTED,
-                          "needs m, n multiples of 256, k a positive multiple of 64 and leading dimensions below 2^26 "
-                          "(whole DMA tiles, 32-bit lane offsets)");
+                          "needs k a positive multiple of 64, leading dimensions of a and b below 2^23 and of c and d "
+                          "below 2^21 (DMA stages, 32-bit offsets)");
         if (info_->gemv && s.m > uint64_t(info_->bm))
             return Result(FTRAIN_STATUS_UNSUPPORTED, "m exceeds the skinny-kernel row limit");
         if (info_->split == SplitKind::kPartial &&

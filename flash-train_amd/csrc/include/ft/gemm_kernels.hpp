@@ -180,8 +180,8 @@ enum class Variant : int {
     kFp16Mfma128x128,
     kFp16Mfma128x128S,
     kFp16Mfma64x64U,
-    // bf16 / fp16 256x256 whole tiles with operands staged into LDS by DMA
-    // (global_load_lds_dwordx4): m, n multiples of 256, k a multiple of 64.
+    // bf16 / fp16 256x256 tiles with operands staged into LDS by DMA
+    // (global_load_lds_dwordx4): k a multiple of 64, any m and n.
     kBf16MfmaDma256x256,
     kFp16MfmaDma256x256,
     // One-pass skinny-m kernels (m <= 8, row-major b) for bf16 / fp16 inputs.
@@ -265,6 +265,8 @@ const void* halfKernelFp16TT(int tile);
 // The DMA-staged 256x256 tiles per input type and operand orientation.
 const void* dmaKernelBf16(bool ta, bool tb);
 const void* dmaKernelFp16(bool ta, bool tb);
+const void* groupedDmaKernelBf16(bool ta, bool tb);
+const void* groupedDmaKernelFp16(bool ta, bool tb);
 // Grouped kernels: element type (FTRAIN_NUMERIC_TYPE_FP32 / BF16 / FP16),
 // tile (0 = 128x128 with 16-byte loads, 1 = 64x64 per-element, 2 = the
 // family's large tile: fp32 16x16x4 256x128, bf16/fp16 256x256; 3 = fp32

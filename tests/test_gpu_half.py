@@ -107,11 +107,13 @@ def test_half_every_primitive(capi, ops, oracle, kind, cd, la, lb, m, n, k, pad)
 @pytest.mark.parametrize("cd", ["fp32", "same"])
 @pytest.mark.parametrize("la,lb", list(itertools.product((False, True), (False, True))))
 @pytest.mark.parametrize("m,n,k,pad,with_c", [(256, 256, 64, 8, True), (512, 256, 192, 8, False),
-                                              (256, 512, 1024, 0, True)])
+                                              (256, 512, 1024, 0, True), (296, 520, 128, 8, True),
+                                              (40, 24, 64, 0, False)])
 def test_half_dma_tile(capi, ops, oracle, kind, cd, la, lb, m, n, k, pad, with_c):
-    # Whole 256x256 tiles with LDS staging by DMA: one stage (k = 64), an odd stage count (the
-    # tail copy of the pipeline) and a long even one, every operand orientation, NaN past each
-    # leading dimension's used extent.
+    # The 256x256 tile with LDS staging by DMA: one stage (k = 64), an odd stage count (the tail
+    # copy of the pipeline), a long even one, edge tiles in m and n (loads clamped, stores
+    # checked) and a matrix smaller than one tile; every operand orientation, NaN past each
+    # leading dimension's used extent, 7.0 around d (nothing written outside it).
     names = run_case(capi, ops, oracle, kind, kind if cd == "same" else "fp32", m, n, k, la, lb, pad=pad,
                      with_c=with_c, seed=k + pad)
     assert f"{kind.capitalize()}MfmaGemm_256x256_Dma" in names, names

@@ -81,7 +81,7 @@ def test_large_groups_take_the_large_tiles(tlib):
     assert plan.names()[0] == "GroupedFp32Mfma16Gemm_128x256"
     st, msg, plan = moe_abcd(tlib, rows, k=4096, n=14336, a_type=c.BF16)
     assert st == c.SUCCESS, msg
-    assert plan.names()[0] == "GroupedBf16MfmaGemm_256x256"
+    assert plan.names()[0] == "GroupedBf16MfmaGemm_256x256_Dma"
 
 
 def test_disabled_grouped_finder_falls_back_to_registration_order():
@@ -109,11 +109,15 @@ def test_unaligned_groups_take_the_per_element_tile(tlib):
 def test_half_types_select_their_variants(tlib):
     st, msg, plan = moe_abcd(tlib, [64, 32], a_type=c.BF16)
     assert st == c.SUCCESS, msg
-    assert sorted(plan.names()) == sorted(["GroupedBf16MfmaGemm_256x256", "GroupedBf16MfmaGemm_128x128",
-                                           "GroupedBf16MfmaGemm_64x64_Unaligned"])
+    assert sorted(plan.names()) == sorted(["GroupedBf16MfmaGemm_256x256_Dma", "GroupedBf16MfmaGemm_256x256",
+                                           "GroupedBf16MfmaGemm_128x128", "GroupedBf16MfmaGemm_64x64_Unaligned"])
     st, msg, plan = moe_abcd(tlib, [64, 32], a_type=c.FP16, d_type=c.FP16)
     assert st == c.SUCCESS, msg
-    assert all(n.startswith("GroupedFp16") for n in plan.names()) and len(plan) == 3
+    assert all(n.startswith("GroupedFp16") for n in plan.names()) and len(plan) == 4
+    # k not a multiple of 64: the DMA tile (whole 64-k stages) steps aside.
+    st, msg, plan = moe_abcd(tlib, [64, 32], k=72, a_type=c.BF16)
+    assert st == c.SUCCESS, msg
+    assert "GroupedBf16MfmaGemm_256x256_Dma" not in plan.names() and len(plan) == 3
 
 
 def test_group_shape_mismatch_is_invalid(tlib):
