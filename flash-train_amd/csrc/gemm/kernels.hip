@@ -287,6 +287,40 @@ __global__ __launch_bounds__(256) void splitk_reduce(ReduceParams p) {
     }
 }
 
+// The same reduction with one thread per output unit, summing the slices in
+// increasing z: for outputs with enough units to fill the chip on their own
+// (the 16-thread form leaves 15 of 16 threads idle at two splits).
+template <bool VEC>
+__global__ __launch_bounds__(256) void splitk_reduce_wide(ReduceParams p) {
+    using V               = std::conditional_t<VEC, floatx4, float>;
+    const uint64_t units  = VEC ? p.count / 4 : p.count;
+    const V* __restrict__ W = reinterpret_cast<const V*>(p.partials);
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < units; i += (uint64_t)gridDim.x * 256) {
+        V s = W[i];
+#pragma unroll 4
+        for (int z = 1; z < p.splits; ++z) s += W[(uint64_t)z * units + i];
+        if constexpr (VEC) {
+            const uint64_t row_vecs = p.n / 4;
+            const uint64_t r = i / row_vecs, c = 4 * (i - r * row_vecs);
+            const float* C = static_cast<const float*>(p.c);
+            floatx4 out;
+            if (C != nullptr) {
+                const floatx4 cv = *reinterpret_cast<const floatx4*>(C + r * p.ldc + c);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) out[j] = p.alpha * s[j] + p.beta * cv[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) out[j] = p.alpha * s[j] + 0.f;
+            }
+            *reinterpret_cast<floatx4*>(static_cast<float*>(p.d) + r * p.ldd + c) = out;
+        } else {
+            const uint64_t r = i / p.n, c = i - r * p.n;
+            const float out = p.alpha * s + (p.c != nullptr ? p.beta * load_cd(p.c, r * p.ldc + c, p.cd_type) : 0.f);
+            store_cd(p.d, r * p.ldd + c, p.cd_type, out);
+        }
+    }
+}
+
 // ----------------------------------------------------------------------------
 // General SIMT kernel: 64x64 tiles, 4x4 outputs per thread, 64-bit indices,
 // grid-stride over tiles.  Any shape, 4-byte alignment, any element strides
@@ -432,7 +466,10 @@ const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool t
     return table[t][o](which);
 }
 
-const void* reduceKernel(bool vec) {
+const void* reduceKernel(bool vec, bool wide) {
+    if (wide)
+        return vec ? reinterpret_cast<const void*>(&splitk_reduce_wide<true>)
+                   : reinterpret_cast<const void*>(&splitk_reduce_wide<false>);
     return vec ? reinterpret_cast<const void*>(&splitk_reduce<true>) : reinterpret_cast<const void*>(&splitk_reduce<false>);
 }
 

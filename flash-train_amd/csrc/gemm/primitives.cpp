@@ -250,10 +250,16 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
                                                                                      : gemm::kCdFp16;
             reduce_ = ReduceParams{nullptr, g.c, g.d, alpha, beta, count, s.n, g.ldc, g.ldd, int32_t(splits), cd_type};
             // isApplicable guaranteed n, ldc, ldd % 4 == 0 and 16-byte bases
-            // for the fp32 vec variants; the half variants reduce per element.
-            reduce_vec_ = info_->vec && !half_;
-            // splitk_reduce: 16 output units per block (16 threads each).
-            aux_grid_ = dim3(static_cast<uint32_t>(std::min<uint64_t>(ceilDiv(reduce_vec_ ? count / 4 : count, 16), 65535)));
+            // for the fp32 vec variants; the half variants reduce four at a
+            // time when c and d are fp32 and meet the same conditions.
+            const auto a16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+            reduce_vec_ = info_->vec && (!half_ || (!cd_half && s.n % 4 == 0 && g.ldd % 4 == 0 && a16(g.d) &&
+                                                    (g.c == nullptr || (g.ldc % 4 == 0 && a16(g.c)))));
+            const uint64_t units = reduce_vec_ ? count / 4 : count;
+            reduce_wide_         = units >= gemm::kWideReduceUnits;
+            // splitk_reduce: 16 output units per block (16 threads each); the
+            // wide form 256 units per block.
+            aux_grid_ = dim3(static_cast<uint32_t>(std::min<uint64_t>(ceilDiv(units, reduce_wide_ ? 256 : 16), 65535)));
         }
     }
 
@@ -294,7 +300,7 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
                 void* rargs[]      = {&red};
                 hipError_t e       = hipLaunchKernel(kernel_, grid_, block_, args, 0, r.stream);
                 if (e == hipSuccess)
-                    e = hipLaunchKernel(gemm::reduceKernel(reduce_vec_), aux_grid_, dim3(256), rargs, 0, r.stream);
+                    e = hipLaunchKernel(gemm::reduceKernel(reduce_vec_, reduce_wide_), aux_grid_, dim3(256), rargs, 0, r.stream);
                 check(e, info_->name);
                 break;
             }
@@ -355,6 +361,7 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
     gemm::DeepKParams deepk_{};
     int32_t fused_tiles_ = 0;
     bool reduce_vec_        = false;
+    bool reduce_wide_       = false;
     uint64_t partial_bytes_ = 0;
     std::shared_ptr<void> owned_;  // split-k partials of Primitive 0 (shared by clones)
 };

@@ -285,7 +285,10 @@ const void* groupedHalfKernelFp16NN(int which);
 const void* groupedHalfKernelFp16TN(int which);
 const void* groupedHalfKernelFp16NT(int which);
 const void* groupedHalfKernelFp16TT(int which);
-const void* reduceKernel(bool vec);      // split-k reduction (ReduceParams)
+// Split-k reduction (ReduceParams); wide: one thread per output unit (outputs
+// with at least kWideReduceUnits units), else 16 threads per unit.
+const void* reduceKernel(bool vec, bool wide);
+constexpr uint64_t kWideReduceUnits = 256 * 1024;
 const void* deepkKernel();              // kDeepK64x64 (DeepKParams)
 const void* deepkClearKernel();         // zeroes (unsigned*, int n) arrival counters
 

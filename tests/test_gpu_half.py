@@ -119,6 +119,15 @@ def test_half_dma_tile(capi, ops, oracle, kind, cd, la, lb, m, n, k, pad, with_c
     assert f"{kind.capitalize()}MfmaGemm_256x256_Dma" in names, names
 
 
+@pytest.mark.parametrize("cd", ["fp32", "same"])
+def test_half_split_k_wide_reduction(capi, ops, oracle, cd):
+    # 384x4096 outputs at k = 4096: the split-k tile's reduction runs one thread per output unit
+    # (four fp32 values with fp32 c and d, one with a bf16 d); every Primitive of the Plan.
+    names = run_case(capi, ops, oracle, "bf16", "bf16" if cd == "same" else "fp32", 384, 4096, 4096, False, False,
+                     seed=9)
+    assert "Bf16MfmaGemm_128x128_SplitK" in names, names
+
+
 @pytest.mark.parametrize("kind", ["bf16", "fp16"])
 def test_half_dma_tile_exact_and_repeatable(capi, ops, kind):
     # Integer inputs in [-8, 8] (exact in fp32 for this k): the DMA tile equals the integer
