@@ -18,6 +18,7 @@ constexpr SplitKind N = SplitKind::kNone, P = SplitKind::kPartial, F = SplitKind
 constexpr FTrainNumericType FP32 = FTRAIN_NUMERIC_TYPE_FP32, BF16 = FTRAIN_NUMERIC_TYPE_BF16,
                             FP16 = FTRAIN_NUMERIC_TYPE_FP16;
 constexpr VariantInfo kInfo[] = {
+    {"Fp32Mfma16Gemm_256x256_Dma", 256, 256, 32, 256, 1, true, N, false, false, false, 0.96, FP32, 256.0, 0.96},
     {"Fp32Mfma16Gemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, true, 0.905, FP32, 256.0, 0.905},
     {"Fp32Mfma16Gemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, true, 0.73, FP32, 256.0, 0.73},
     {"Fp32Mfma16Gemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, true, 0.895, FP32, 256.0, 0.855},

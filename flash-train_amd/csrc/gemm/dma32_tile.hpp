@@ -1,0 +1,273 @@
+// FP32 256x256 tile kernel (v_mfma_f32_16x16x4_f32) whose operands reach
+// LDS by DMA (global_load_lds_dwordx4), for row-major a and b.  Device code
+// only; kernels_dma32.hip instantiates it.
+//
+// d = alpha * (a @ b) + beta * c (the reference's formula,
+// src/primitive/hygon/gemm/fp32_gemm.hip:18-31: the beta term dropped for a
+// null c, always evaluated otherwise).  Applicability, checked on the host:
+// m and n multiples of 256, k a multiple of 32, 16-byte aligned a, b, c, d
+// with leading dimensions multiples of 4, a's and b's below 2^22 elements
+// (32-bit lane offsets).
+//
+// Workgroup: 4 waves (one per SIMD), each a 128x128 block of 8x8 MFMA blocks
+// (16x16 outputs, 256 accumulators per lane):
+//   A operand: lane l holds A[row l % 16][k slot g = l / 16]
+//   B operand: lane l holds B[k slot g][col l % 16]
+//   result   : lane l, register r holds D[row 4 g + r][col l % 16]
+// Within a stage of 32 k, lane group g takes k = 8 g + s at k-step s
+// (s = 0..7), so a lane's A values for four k-steps are one 128-bit LDS read.
+// Column interleave: block bj, MFMA column j is wave-tile column
+// (bj / 4) * 64 + 4 j + bj % 4, so one 128-bit read of four adjacent columns
+// at one k serves four blocks, and each epilogue store writes four adjacent
+// columns.
+//
+// Stage = 32 k of both operands, 32 KiB each; two stages (128 KiB).  One DMA
+// instruction moves 64 lanes x 16 bytes into 1 KiB of LDS at M0 + 16 * lane:
+//   A [256 rows][32 k]: a DMA covers 8 rows (whole 128-byte lines); 16-byte
+//     chunk c of row r sits at slot c ^ h(r), h(r) = bit 2 of r | bit 3 of r
+//     shifted to bit 2, so the 32 lanes of a half-wave (16 rows, two chunks
+//     two apart) hit 32 distinct 16-byte bank groups;
+//   B [32 k][256 cols]: a DMA covers one k row (1 KiB); chunk c of k row kr
+//     sits at slot c ^ (16 * ((kr >> 3) & 1)), separating the two k rows a
+//     half-wave reads.
+//
+// Pipeline per stage st (buffer X; stage st + 1 in Y), per wave: k-steps
+// 0..3 from registers while reading k-steps 4..7 of X; wait for this wave's
+// LDS reads and DMAs, barrier (every wave is done with X, stage st + 1 has
+// landed in Y); k-steps 4..7 while reading k-steps 0..3 of Y and issuing the
+// DMA of stage st + 2 into X.  One barrier per 512 MFMAs (16384 MFMA cycles).
+// The DMA is issued from inline assembly with M0 set in the same statement;
+// every wait on it is an explicit vmcnt in this file, and the compiler has
+// no other use of M0 here (no LDS DMA builtins, no indexed register access).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "ft/gemm_kernels.hpp"
+
+namespace ftrain::gemm::d32 {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTile = 256, kStageK = 32;
+constexpr int kStageFloats = kTile * kStageK;  // one operand, one stage: 32 KiB
+
+__device__ __forceinline__ void dma_1k(unsigned voff, const void* sbase, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(sbase)
+                 : "memory", "m0");
+}
+
+// Output tile of workgroup `bid`: the 8 XCDs take contiguous runs of tile
+// ids (hardware ids are dealt to XCDs in turn), walked in bands of 4 tile
+// rows.
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int tiles = tiles_m * tiles_n;
+    const int per   = tiles >> 3;
+    int t           = bid;
+    if (bid < (per << 3)) t = (bid & 7) * per + (bid >> 3);
+    constexpr int kBand = 4;
+    const int band_span = kBand * tiles_n;
+    const int band      = t / band_span;
+    const int first_m   = band * kBand;
+    const int band_rows = min(tiles_m - first_m, kBand);
+    const int within    = t - band * band_span;
+    tm                  = first_m + within % band_rows;
+    tn                  = within / band_rows;
+}
+
+__device__ __forceinline__ int a_swz(int row) { return ((row >> 2) & 1) | (((row >> 3) & 1) << 2); }
+
+__global__ __launch_bounds__(256, 1) void fp32_gemm_dma(GemmParams p) {
+    __shared__ __attribute__((aligned(1024))) float As0[kStageFloats];
+    __shared__ __attribute__((aligned(1024))) float Bs0[kStageFloats];
+    __shared__ __attribute__((aligned(1024))) float As1[kStageFloats];
+    __shared__ __attribute__((aligned(1024))) float Bs1[kStageFloats];
+    const int tid = threadIdx.x, lane = tid & 63, j16 = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wrow = (wave >> 1) * 128, wcol = (wave & 1) * 128;
+    int tm, tn;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * kTile, n0 = tn * kTile;
+    const int nst = p.k / kStageK;
+    const int64_t lda = p.lda, ldb = p.ldb;
+
+    // DMA sources.  A block q = wave + 4 j: rows 8q .. 8q + 7 (lane: row 8q + lane / 8), slot
+    // lane % 8 holds chunk (lane % 8) ^ h(row); h does not depend on j (32 j leaves bits 2, 3).
+    const int ar = 8 * wave + (lane >> 3);
+    const unsigned aoff = static_cast<unsigned>((ar * lda + 4 * ((lane & 7) ^ a_swz(ar))) * 4);
+    const char* abase   = reinterpret_cast<const char*>(p.a + (size_t)m0 * lda);
+    // B block q = wave + 4 j: k row q (lane: slot lane), chunk lane ^ (16 ((q >> 3) & 1)).
+    const char* bbase = reinterpret_cast<const char*>(p.b + n0);
+    const unsigned boff0 = static_cast<unsigned>(4 * 4 * lane);
+    const unsigned boff1 = static_cast<unsigned>(4 * 4 * (lane ^ 16));
+    auto dma_a = [&](int st, int j, unsigned lds) {
+        dma_1k(aoff, abase + ((size_t)32 * j * lda + (size_t)st * kStageK) * 4, lds + (wave + 4 * j) * 1024);
+    };
+    auto dma_b = [&](int st, int j, unsigned lds) {
+        const int q = wave + 4 * j;
+        dma_1k(((q >> 3) & 1) ? boff1 : boff0, bbase + ((size_t)st * kStageK + q) * ldb * 4, lds + q * 1024);
+    };
+    const unsigned la0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) float*)As0;
+    const unsigned lb0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) float*)Bs0;
+    const unsigned la1 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) float*)As1;
+    const unsigned lb1 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) float*)Bs1;
+
+    // A operands of half hf (k-steps 4 hf .. 4 hf + 3) for block row bi: A[row][8 g + 4 hf .. + 3].
+    auto rd_a = [&](const float* T, int bi, int hf) {
+        const int row = wrow + 16 * bi + j16, c = 2 * g + hf;
+        return *reinterpret_cast<const floatx4*>(T + row * kStageK + 4 * (c ^ a_swz(row)));
+    };
+    // B operands of k-step s for column run cc (blocks 4 cc .. 4 cc + 3): B[8 g + s][4 cols].
+    auto rd_b = [&](const float* T, int s, int cc) {
+        const int kr = 8 * g + s, c = (wcol >> 2) + 16 * cc + j16;
+        return *reinterpret_cast<const floatx4*>(T + kr * kTile + 4 * (c ^ (16 * ((kr >> 3) & 1))));
+    };
+
+    floatx4 acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // Operands of one half stage: fa[bi] (4 k-steps), fb[s][cc].
+    floatx4 fa0[8], fb0[4][2], fa1[8], fb1[4][2];
+    // Read r (0..15) of half hf: 8 A reads, then 8 B reads (k-step major).
+    auto read_one = [&](floatx4 (&ga)[8], floatx4 (&gb)[4][2], const float* As, const float* Bs, int hf, int r) {
+        if (r < 8)
+            ga[r] = rd_a(As, r, hf);
+        else
+            gb[(r - 8) >> 1][(r - 8) & 1] = rd_b(Bs, 4 * hf + ((r - 8) >> 1), (r - 8) & 1);
+    };
+    // 256 MFMAs of one half stage on (fa, fb), k-step major, in 32 slots of 8 (one block row at
+    // one k-step); the 16 reads into (ga, gb) follow the even slots, and with a true with_dma the
+    // 16 DMAs of stage dma_st the odd ones.  The scheduling groups pin that order (left to
+    // itself the scheduler bunched the reads at the end of the half: 0.929-0.937 of peak at
+    // 8192^3 against 0.962-0.964).
+    auto run_half = [&](floatx4 (&fa)[8], floatx4 (&fb)[4][2], floatx4 (&ga)[8], floatx4 (&gb)[4][2],
+                        const float* As, const float* Bs, int hf, auto with_dma, int dma_st, unsigned la,
+                        unsigned lb) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+#pragma unroll
+            for (int bi = 0; bi < 8; ++bi) {
+#pragma unroll
+                for (int bj = 0; bj < 8; ++bj)
+                    acc[bi][bj] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[bi][s], fb[s][bj >> 2][bj & 3], acc[bi][bj],
+                                                                      0, 0, 0);
+                const int u = 8 * s + bi;
+                // Read r at slot 2 r: the 16 reads spread over all 32 slots of 8 MFMAs.
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (2 * r == u) read_one(ga, gb, As, Bs, hf, r);
+                // Keep each slot's 8 MFMAs, then its read, in that order.
+                __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+                if ((u & 1) == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                if constexpr (decltype(with_dma)::value) {
+                    if (u & 1) {
+                        const int v = u >> 1;
+                        if (v & 1)
+                            dma_b(dma_st, v >> 1, lb);
+                        else
+                            dma_a(dma_st, v >> 1, la);
+                    }
+                }
+            }
+        }
+    };
+    auto read_half = [&](floatx4 (&ga)[8], floatx4 (&gb)[4][2], const float* As, const float* Bs, int hf) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) read_one(ga, gb, As, Bs, hf, r);
+    };
+
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        dma_a(0, j, la0);
+        dma_b(0, j, lb0);
+    }
+    const int st1 = min(1, nst - 1);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        dma_a(st1, j, la1);
+        dma_b(st1, j, lb1);
+    }
+    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+    read_half(fa0, fb0, As0, Bs0, 0);
+
+    // Stages past the last reload the last one (nothing reads them).  The operand sets rotate by
+    // copying (f1 -> f0 after each half); the allocator coalesces the copies, where alternating
+    // the two sets by reference kept both live in separate registers and spilled.
+    auto rotate = [&] {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) fa0[i] = fa1[i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            fb0[i][0] = fb1[i][0];
+            fb0[i][1] = fb1[i][1];
+        }
+    };
+#define FT_DMA32_PHASE(XA, XB, YA, YB, LXA, LXB, ST)                                              \
+    run_half(fa0, fb0, fa1, fb1, XA, XB, 1, std::false_type{}, 0, 0u, 0u);                        \
+    rotate();                                                                                     \
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");         \
+    run_half(fa0, fb0, fa1, fb1, YA, YB, 0, std::true_type{}, min((ST) + 2, nst - 1), LXA, LXB);  \
+    rotate();
+    int st = 0;
+    for (; st + 1 < nst; st += 2) {
+        FT_DMA32_PHASE(As0, Bs0, As1, Bs1, la0, lb0, st)
+        FT_DMA32_PHASE(As1, Bs1, As0, Bs0, la1, lb1, st + 1)
+    }
+    if (st < nst) {
+        FT_DMA32_PHASE(As0, Bs0, As1, Bs1, la0, lb0, st)
+    }
+#undef FT_DMA32_PHASE
+    // The workgroup's LDS must not be released with a DMA still writing it.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // Epilogue, one row block at a time: block (bi, bj) register r is D[row 16 bi + 4 g + r][col
+    // (bj / 4) * 64 + 4 j16 + bj % 4]; c of row block bi + 1 is loaded while bi is written.
+    const float alpha = p.alpha, beta = p.beta;
+    const int col = n0 + wcol + 4 * j16;
+    auto run = [&](auto c_tag) {
+        constexpr bool HAS_C = decltype(c_tag)::value;
+        floatx4 cv[HAS_C ? 2 : 1][4][2];
+        auto load_c = [&](int bi, floatx4 (&dst)[4][2]) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + wrow + 16 * bi + 4 * g + r;
+#pragma unroll
+                for (int q = 0; q < 2; ++q)
+                    dst[r][q] = *reinterpret_cast<const floatx4*>(p.c + (size_t)row * p.ldc + col + 64 * q);
+            }
+        };
+        if constexpr (HAS_C) load_c(0, cv[0]);
+#pragma unroll
+        for (int bi = 0; bi < 8; ++bi) {
+            if constexpr (HAS_C)
+                if (bi + 1 < 8) load_c(bi + 1, cv[(bi + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + wrow + 16 * bi + 4 * g + r;
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    floatx4 out;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        out[t] = alpha * acc[bi][4 * q + t][r];
+                        if constexpr (HAS_C) out[t] += beta * cv[HAS_C ? bi & 1 : 0][r][q][t];
+                    }
+                    *reinterpret_cast<floatx4*>(p.d + (size_t)row * p.ldd + col + 64 * q) = out;
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    if (p.c != nullptr)
+        run(std::true_type{});
+    else
+        run(std::false_type{});
+}
+
+}  // namespace ftrain::gemm::d32

@@ -592,11 +592,11 @@ def rank(tlib, m, n, k, addr=FAKE, with_c=False, device=0, ab_type=c.FP32):
 
 def test_finder_choices_for_the_baseline_configs(tlib):
     # Best of 3 interleaved passes over every applicable Primitive, MI355X, N(0,1) inputs (us):
-    # 8192^3: Fp32Mfma16Gemm_256x256 7771, _128x256 7811, _256x128 7834, Fp32MfmaGemm_128x128 7921.
-    # MLP fwd: _128x256 13620, _256x128 13655, _256x256 13673 (all within 0.4%).
-    assert rank(tlib, 8192, 8192, 8192)[0] == "Fp32Mfma16Gemm_256x256"
-    assert rank(tlib, 16384, 14336, 4096)[0] in ("Fp32Mfma16Gemm_256x256", "Fp32Mfma16Gemm_128x256",
-                                                  "Fp32Mfma16Gemm_256x128")
+    # 8192^3: Fp32Mfma16Gemm_256x256 7771, _128x256 7811, _256x128 7834, Fp32MfmaGemm_128x128 7921;
+    # the DMA-staged 256x256 tile 7250-7290 (U(-1,1) inputs).
+    # MLP fwd: _128x256 13620, _256x128 13655, _256x256 13673 (all within 0.4%); DMA tile 12700.
+    assert rank(tlib, 8192, 8192, 8192)[0] == "Fp32Mfma16Gemm_256x256_Dma"
+    assert rank(tlib, 16384, 14336, 4096)[0] == "Fp32Mfma16Gemm_256x256_Dma"
     assert rank(tlib, 16384, 4096, 14336)[0].startswith("Fp32Mfma16Gemm_")
     # 6144^3: the 32x32 128x128 tile 3361, the 16x16 256x64 tile 3442, 256x256 tiles 4373 (2.25 per CU).
     assert rank(tlib, 6144, 6144, 6144)[0] == "Fp32MfmaGemm_128x128"

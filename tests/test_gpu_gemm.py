@@ -508,3 +508,50 @@ def test_deep_k_kernel(capi, ops, oracle, m, n, k, with_c):
     assert rep["ok"], (names[i], need, rep)
     assert rep["max_abs_err"] <= 1e-2 * rep["bound"], rep  # far inside the bar, not just under it
     assert all(torch.equal(outs[0], o) for o in outs[1:]), names[i]
+
+
+@pytest.mark.parametrize("m,n,k,with_c,pad", [
+    (256, 256, 32, False, 0),     # one stage
+    (512, 256, 96, True, 4),      # an odd stage count (the pipeline's tail copy), padded rows
+    (256, 512, 1024, True, 0),    # a long even run
+    (768, 1024, 2080, False, 8),  # 12 tiles, 65 stages
+])
+def test_fp32_dma_tile(capi, ops, oracle, m, n, k, with_c, pad):
+    """Fp32Mfma16Gemm_256x256_Dma (operands staged into LDS by DMA) on whole tiles: one, odd and
+    long stage counts, row strides padded past the used extent with NaN (a read out of a row
+    fails the check), twice in a row bit for bit."""
+    g = torch.Generator().manual_seed(m + n + k)
+    a_h, b_h = torch.randn(m, k, generator=g), torch.randn(k, n, generator=g)
+    c_h = torch.randn(m, n, generator=g) if with_c else None
+    alpha, beta = 1.25, (0.5 if with_c else 0.0)
+    ref = oracle.gemm_f64(a_h, b_h, c_h, alpha, beta)
+    a_s = torch.full((m, k + pad), float("nan")); a_s[:, :k] = a_h
+    b_s = torch.full((k, n + pad), float("nan")); b_s[:, :n] = b_h
+    a_d, b_d = a_s.cuda()[:, :k], b_s.cuda()[:, :n]
+    d = torch.empty(m, n, device="cuda")
+    plan = capi.plan_for(a_d, b_d, None if c_h is None else c_h.cuda(), d, alpha, beta, ops)
+    names = plan.names()
+    i = names.index("Fp32Mfma16Gemm_256x256_Dma")
+    outs = []
+    for _ in range(2):
+        d.fill_(float("nan"))
+        plan.execute(i, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        outs.append(d.clone())
+    rep = oracle.tolerance_check(outs[0].cpu().numpy(), ref, k)
+    assert rep["ok"], (names[i], rep)
+    assert rep["max_abs_err"] <= 1e-2 * rep["bound"], rep
+    assert torch.equal(outs[0], outs[1])
+
+
+def test_fp32_dma_tile_skips_other_layouts_and_edges(capi, ops):
+    a = torch.zeros(256, 64, device="cuda")
+    b = torch.zeros(64, 256, device="cuda")
+    d = torch.empty(256, 256, device="cuda")
+    assert "Fp32Mfma16Gemm_256x256_Dma" in capi.plan_for(a, b, None, d, 1.0, 0.0, ops).names()
+    # column-major b, an n edge, a k tail: the whole-tile row-major kernel does not apply
+    assert "Fp32Mfma16Gemm_256x256_Dma" not in capi.plan_for(a, b.t().contiguous().t(), None, d, 1.0, 0.0, ops).names()
+    d2 = torch.empty(256, 200, device="cuda")
+    assert "Fp32Mfma16Gemm_256x256_Dma" not in capi.plan_for(a, b[:, :200], None, d2, 1.0, 0.0, ops).names()
+    a3 = torch.zeros(256, 48, device="cuda")
+    assert "Fp32Mfma16Gemm_256x256_Dma" not in capi.plan_for(a3, b[:48], None, d, 1.0, 0.0, ops).names()
