@@ -24,9 +24,7 @@
 // Stage = 32 k of both operands, 32 KiB each; two stages (128 KiB).  One DMA
 // instruction moves 64 lanes x 16 bytes into 1 KiB of LDS at M0 + 16 * lane:
 //   A [256 rows][32 k]: a DMA covers 8 rows (whole 128-byte lines); 16-byte
-//     chunk c of row r sits at slot c ^ h(r), h(r) = bit 2 of r | bit 3 of r
-//     shifted to bit 2, so the 32 lanes of a half-wave (16 rows, two chunks
-//     two apart) hit 32 distinct 16-byte bank groups;
+//     chunk c of row r sits at slot c ^ h(r) (a_swz below);
 //   B [32 k][256 cols]: a DMA covers one k row (1 KiB); chunk c of k row kr
 //     sits at slot c ^ (16 * ((kr >> 3) & 1)), separating the two k rows a
 //     half-wave reads.
@@ -77,7 +75,12 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
     tn                  = within / band_rows;
 }
 
-__device__ __forceinline__ int a_swz(int row) { return ((row >> 2) & 1) | (((row >> 3) & 1) << 2); }
+// Chunk swizzle of A: row bits 2, 1, 3 to chunk bits 0, 1, 2.  Reads run 16 lanes (16 consecutive
+// rows, one chunk) at a time over 64 banks: rows of one parity get 8 distinct chunks; the 32
+// lanes of a half-wave (two chunks two apart) also cover 128 banks.
+__device__ __forceinline__ int a_swz(int row) {
+    return ((row >> 2) & 1) | (((row >> 1) & 1) << 1) | (((row >> 3) & 1) << 2);
+}
 
 __global__ __launch_bounds__(256, 1) void fp32_gemm_dma(GemmParams p) {
     __shared__ __attribute__((aligned(1024))) float As0[kStageFloats];
@@ -94,7 +97,7 @@ __global__ __launch_bounds__(256, 1) void fp32_gemm_dma(GemmParams p) {
     const int64_t lda = p.lda, ldb = p.ldb;
 
     // DMA sources.  A block q = wave + 4 j: rows 8q .. 8q + 7 (lane: row 8q + lane / 8), slot
-    // lane % 8 holds chunk (lane % 8) ^ h(row); h does not depend on j (32 j leaves bits 2, 3).
+    // lane % 8 holds chunk (lane % 8) ^ h(row); h does not depend on j (32 j leaves bits 1-3).
     const int ar = 8 * wave + (lane >> 3);
     const unsigned aoff = static_cast<unsigned>((ar * lda + 4 * ((lane & 7) ^ a_swz(ar))) * 4);
     const char* abase   = reinterpret_cast<const char*>(p.a + (size_t)m0 * lda);
