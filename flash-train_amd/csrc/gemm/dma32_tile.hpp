@@ -1,13 +1,14 @@
 // FP32 256x256 tile kernel (v_mfma_f32_16x16x4_f32) whose operands reach
 // LDS by DMA (global_load_lds_dwordx4), for row-major a and b.  Device code
-// only; kernels_dma32.hip instantiates it.
+// only; kernels_dma32.hip instantiates it (plain and grouped).
 //
 // d = alpha * (a @ b) + beta * c (the reference's formula,
 // src/primitive/hygon/gemm/fp32_gemm.hip:18-31: the beta term dropped for a
 // null c, always evaluated otherwise).  Applicability, checked on the host:
-// m and n multiples of 256, k a multiple of 32, 16-byte aligned a, b, c, d
-// with leading dimensions multiples of 4, a's and b's below 2^22 elements
-// (32-bit lane offsets).
+// k a positive multiple of 32, n a multiple of 4, 16-byte aligned a, b, c, d
+// with leading dimensions multiples of 4, a's and b's below 2^22 elements and
+// c's and d's below 2^21 (32-bit offsets); m and n are free otherwise (edge
+// tiles clamp their loads and drop their out-of-matrix stores).
 //
 // Workgroup: 4 waves (one per SIMD), each a 128x128 block of 8x8 MFMA blocks
 // (16x16 outputs, 256 accumulators per lane):
@@ -48,8 +49,12 @@
 namespace ftrain::gemm::d32 {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 256, kStageK = 32;
+// Word 3 of a raw (untyped, stride 0) buffer resource on gfx9 parts: 32-bit data format, the range
+// check against num_records on every access.
+constexpr int kBufferConfig = 0x00020000;
 constexpr int kStageFloats = kTile * kStageK;  // one operand, one stage: 32 KiB
 
 __device__ __forceinline__ void dma_1k(unsigned voff, const void* sbase, unsigned lds) {
@@ -82,7 +87,8 @@ __device__ __forceinline__ int a_swz(int row) {
     return ((row >> 2) & 1) | (((row >> 1) & 1) << 1) | (((row >> 3) & 1) << 2);
 }
 
-__global__ __launch_bounds__(256, 1) void fp32_gemm_dma(GemmParams p) {
+// Output tile `bid` of p (tile_of order); the whole workgroup calls it.
+__device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid) {
     __shared__ __attribute__((aligned(1024))) float As0[kStageFloats];
     __shared__ __attribute__((aligned(1024))) float Bs0[kStageFloats];
     __shared__ __attribute__((aligned(1024))) float As1[kStageFloats];
@@ -91,22 +97,29 @@ __global__ __launch_bounds__(256, 1) void fp32_gemm_dma(GemmParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wrow = (wave >> 1) * 128, wcol = (wave & 1) * 128;
     int tm, tn;
-    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+    tile_of(bid, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * kTile, n0 = tn * kTile;
+    const int M = p.m, N = p.n;
     const int nst = p.k / kStageK;
     const int64_t lda = p.lda, ldb = p.ldb;
 
     // DMA sources.  A block q = wave + 4 j: rows 8q .. 8q + 7 (lane: row 8q + lane / 8), slot
     // lane % 8 holds chunk (lane % 8) ^ h(row); h does not depend on j (32 j leaves bits 1-3).
-    const int ar = 8 * wave + (lane >> 3);
-    const unsigned aoff = static_cast<unsigned>((ar * lda + 4 * ((lane & 7) ^ a_swz(ar))) * 4);
-    const char* abase   = reinterpret_cast<const char*>(p.a + (size_t)m0 * lda);
-    // B block q = wave + 4 j: k row q (lane: slot lane), chunk lane ^ (16 ((q >> 3) & 1)).
-    const char* bbase = reinterpret_cast<const char*>(p.b + n0);
-    const unsigned boff0 = static_cast<unsigned>(4 * 4 * lane);
-    const unsigned boff1 = static_cast<unsigned>(4 * 4 * (lane ^ 16));
+    // Rows past the matrix are clamped onto its last row (they feed only outputs that are not
+    // stored); 255 rows of lda < 2^22 keep the lane offset below 2^32.
+    const unsigned ar      = 8 * wave + (lane >> 3);
+    const unsigned achunk  = 16 * ((lane & 7) ^ a_swz(ar));
+    const unsigned alast   = static_cast<unsigned>(min(M - 1 - m0, kTile - 1));
+    const unsigned lda4    = static_cast<unsigned>(4 * lda);
+    const char* abase      = reinterpret_cast<const char*>(p.a + (size_t)m0 * lda);
+    // B block q = wave + 4 j: k row q (lane: slot lane), chunk lane ^ (16 ((q >> 3) & 1)); a chunk
+    // past n is clamped onto the last whole one (n % 4 == 0).
+    const char* bbase    = reinterpret_cast<const char*>(p.b + n0);
+    const unsigned boff0 = static_cast<unsigned>(4 * (min(n0 + 4 * lane, N - 4) - n0));
+    const unsigned boff1 = static_cast<unsigned>(4 * (min(n0 + 4 * (lane ^ 16), N - 4) - n0));
     auto dma_a = [&](int st, int j, unsigned lds) {
-        dma_1k(aoff, abase + ((size_t)32 * j * lda + (size_t)st * kStageK) * 4, lds + (wave + 4 * j) * 1024);
+        const unsigned row = min(ar + 32u * j, alast);
+        dma_1k(row * lda4 + achunk, abase + (size_t)st * kStageK * 4, lds + (wave + 4 * j) * 1024);
     };
     auto dma_b = [&](int st, int j, unsigned lds) {
         const int q = wave + 4 * j;
@@ -229,19 +242,42 @@ __global__ __launch_bounds__(256, 1) void fp32_gemm_dma(GemmParams p) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
     // Epilogue, one row block at a time: block (bi, bj) register r is D[row 16 bi + 4 g + r][col
-    // (bj / 4) * 64 + 4 j16 + bj % 4]; c of row block bi + 1 is loaded while bi is written.
+    // (bj / 4) * 64 + 4 j16 + bj % 4], four adjacent columns per 128-bit access; c of row block
+    // bi + 1 is loaded while bi is written.  Buffer accesses relative to the tile's corner: the
+    // lane part of the offset (4 g rows, 4 j16 columns) in the VGPR offset, the block part in the
+    // scalar offset.  An element outside the matrix gets the lane offset 2^31, past the buffer's
+    // size (at most 2^31 - 1 bytes), so its c load returns 0 and its store is dropped; ldc and
+    // ldd below 2^21 keep every sum below 2^32.
     const float alpha = p.alpha, beta = p.beta;
-    const int col = n0 + wcol + 4 * j16;
+    const int rows_left = M - m0, cols_left = N - n0;
+    auto span = [&](uint64_t ld) {
+        const uint64_t b = ((uint64_t)(rows_left - 1) * ld + (uint64_t)cols_left) * 4;
+        return static_cast<int>(b < 0x7FFFFFFFull ? b : 0x7FFFFFFFull);
+    };
+    const __amdgpu_buffer_rsrc_t dres =
+        __builtin_amdgcn_make_buffer_rsrc(p.d + (size_t)m0 * p.ldd + n0, 0, span(p.ldd), kBufferConfig);
+    const unsigned ldd = static_cast<unsigned>(p.ldd), ldc = static_cast<unsigned>(p.ldc);
+    constexpr unsigned kOut = 0x80000000u;
+    const unsigned lane_d = (4 * g * ldd + 4 * j16) * 4, lane_c = (4 * g * ldc + 4 * j16) * 4;
     auto run = [&](auto c_tag) {
         constexpr bool HAS_C = decltype(c_tag)::value;
+        __amdgpu_buffer_rsrc_t cres = dres;
+        if constexpr (HAS_C)
+            cres = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.c) + (size_t)m0 * p.ldc + n0, 0,
+                                                     span(p.ldc), kBufferConfig);
         floatx4 cv[HAS_C ? 2 : 1][4][2];
         auto load_c = [&](int bi, floatx4 (&dst)[4][2]) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int row = m0 + wrow + 16 * bi + 4 * g + r;
+                const int row0 = wrow + 16 * bi + r;  // row of lane group 0
 #pragma unroll
-                for (int q = 0; q < 2; ++q)
-                    dst[r][q] = *reinterpret_cast<const floatx4*>(p.c + (size_t)row * p.ldc + col + 64 * q);
+                for (int q = 0; q < 2; ++q) {
+                    const int c0  = wcol + 64 * q;
+                    const bool ok = 4 * g < rows_left - row0 && c0 + 4 * j16 < cols_left;
+                    dst[r][q]     = __builtin_bit_cast(
+                        floatx4, __builtin_amdgcn_raw_buffer_load_b128(cres, ok ? lane_c : kOut,
+                                                                       static_cast<int>((row0 * ldc + c0) * 4), 0));
+                }
             }
         };
         if constexpr (HAS_C) load_c(0, cv[0]);
@@ -249,28 +285,52 @@ __global__ __launch_bounds__(256, 1) void fp32_gemm_dma(GemmParams p) {
         for (int bi = 0; bi < 8; ++bi) {
             if constexpr (HAS_C)
                 if (bi + 1 < 8) load_c(bi + 1, cv[(bi + 1) & 1]);
-            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int row = m0 + wrow + 16 * bi + 4 * g + r;
+                const int row0 = wrow + 16 * bi + r;
 #pragma unroll
                 for (int q = 0; q < 2; ++q) {
+                    const int c0  = wcol + 64 * q;
+                    const bool ok = 4 * g < rows_left - row0 && c0 + 4 * j16 < cols_left;
                     floatx4 out;
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
                         out[t] = alpha * acc[bi][4 * q + t][r];
                         if constexpr (HAS_C) out[t] += beta * cv[HAS_C ? bi & 1 : 0][r][q][t];
                     }
-                    *reinterpret_cast<floatx4*>(p.d + (size_t)row * p.ldd + col + 64 * q) = out;
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, out), dres, ok ? lane_d : kOut,
+                                                           static_cast<int>((row0 * ldd + c0) * 4), 0);
                 }
             }
-            __builtin_amdgcn_sched_barrier(0);
         }
     };
     if (p.c != nullptr)
         run(std::true_type{});
     else
         run(std::false_type{});
+}
+
+__global__ __launch_bounds__(256, 1) void fp32_gemm_dma(GemmParams p) { fp32_gemm_dma_tile(p, blockIdx.x); }
+
+// Grouped GEMM over a device table of per-group parameters: the workgroup's
+// group is the last one whose first tile id is at most its own.  Group starts
+// are multiples of 8, so the group-local id keeps the hardware id's XCD; ids
+// past the group's tiles are padding and exit at once (the whole workgroup,
+// before any barrier).
+__global__ __launch_bounds__(256, 1) void grouped_fp32_gemm_dma(GroupedGemmArgs g) {
+    const int bid = blockIdx.x;
+    int lo = 0, hi = g.groups - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (g.tile_start[mid] <= bid)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    const GemmParams p = g.params[lo];
+    const int local    = bid - g.tile_start[lo];
+    if (local >= p.tiles_m * p.tiles_n) return;
+    fp32_gemm_dma_tile(p, local);
 }
 
 }  // namespace ftrain::gemm::d32

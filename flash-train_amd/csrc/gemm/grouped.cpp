@@ -280,6 +280,7 @@ struct GroupedVariant {
 // Registration order is also the fallback order when the GroupedCost Finder
 // is disabled: largest tiles first.
 constexpr GroupedVariant kGroupedVariants[] = {
+    {"GroupedFp32Mfma16Gemm_256x256_Dma", FTRAIN_NUMERIC_TYPE_FP32, 4, gemm::Variant::kMfma16Dma256x256},
     {"GroupedFp32Mfma16Gemm_256x128", FTRAIN_NUMERIC_TYPE_FP32, 2, gemm::Variant::kMfma16_256x128},
     {"GroupedFp32Mfma16Gemm_128x256", FTRAIN_NUMERIC_TYPE_FP32, 3, gemm::Variant::kMfma16_128x256},
     {"GroupedFp32MfmaGemm_128x128", FTRAIN_NUMERIC_TYPE_FP32, 0, gemm::Variant::kMfma128x128},
@@ -362,6 +363,12 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
                               !aligned(l.c, 16) || !aligned(l.d, 16)))
                     return Result(FTRAIN_STATUS_UNSUPPORTED, "a group's c or d does not fit 128-bit stores");
             }
+            if (v_->tile == gemm::Variant::kMfma16Dma256x256 &&
+                (l.ta || l.tb || l.shape.k == 0 || l.shape.k % 32 != 0 || l.lda >= (int64_t(1) << 22) ||
+                 l.ldb >= (int64_t(1) << 22) || l.ldc >= (int64_t(1) << 21) || l.ldd >= (int64_t(1) << 21)))
+                return Result(FTRAIN_STATUS_UNSUPPORTED,
+                              "a group is not row-major a and b with k a positive multiple of 32 and leading dimensions "
+                              "that fit 32-bit offsets (fp32 DMA tiles)");
             if ((v_->tile == gemm::Variant::kBf16MfmaDma256x256 || v_->tile == gemm::Variant::kFp16MfmaDma256x256) &&
                 (l.shape.k == 0 || l.shape.k % 64 != 0 || l.lda >= (int64_t(1) << 23) || l.ldb >= (int64_t(1) << 23) ||
                  l.ldc >= (int64_t(1) << 21) || l.ldd >= (int64_t(1) << 21)))

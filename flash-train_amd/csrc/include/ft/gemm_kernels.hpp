@@ -123,9 +123,9 @@ constexpr int kGemvHalfRows = 4;
 enum class Variant : int {
     // v_mfma_f32_16x16x4_f32 256x256 tiles, 4 waves of 128x128 (one per
     // SIMD), 128-bit loads, every operand orientation; whole-k and split-k.
-    // fp32 256x256 whole tiles with operands staged into LDS by DMA
+    // fp32 256x256 tiles with operands staged into LDS by DMA
     // (global_load_lds_dwordx4), v_mfma_f32_16x16x4_f32: row-major a and b,
-    // m and n multiples of 256, k a multiple of 32.
+    // k a multiple of 32, any m and n.
     kMfma16Dma256x256,
     kMfma16_256x256,
     kMfma16_256x256S,
@@ -268,6 +268,7 @@ const void* halfKernelFp16NT(int tile);
 const void* halfKernelFp16TT(int tile);
 // The DMA-staged 256x256 tiles per input type and operand orientation.
 const void* dma32Kernel();
+const void* groupedDma32Kernel();
 const void* dmaKernelBf16(bool ta, bool tb);
 const void* dmaKernelFp16(bool ta, bool tb);
 const void* groupedDmaKernelBf16(bool ta, bool tb);

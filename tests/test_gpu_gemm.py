@@ -515,11 +515,14 @@ def test_deep_k_kernel(capi, ops, oracle, m, n, k, with_c):
     (512, 256, 96, True, 4),      # an odd stage count (the pipeline's tail copy), padded rows
     (256, 512, 1024, True, 0),    # a long even run
     (768, 1024, 2080, False, 8),  # 12 tiles, 65 stages
+    (300, 200, 64, True, 4),      # edge tiles in m and n (clamped loads, dropped stores)
+    (40, 24, 32, False, 0),       # smaller than one tile
 ])
 def test_fp32_dma_tile(capi, ops, oracle, m, n, k, with_c, pad):
-    """Fp32Mfma16Gemm_256x256_Dma (operands staged into LDS by DMA) on whole tiles: one, odd and
-    long stage counts, row strides padded past the used extent with NaN (a read out of a row
-    fails the check), twice in a row bit for bit."""
+    """Fp32Mfma16Gemm_256x256_Dma (operands staged into LDS by DMA): one, odd and long stage
+    counts, edge tiles, row strides padded past the used extent with NaN (a read out of a row
+    fails the check), d inside a 7.0-filled store (nothing written outside it), twice in a row
+    bit for bit."""
     g = torch.Generator().manual_seed(m + n + k)
     a_h, b_h = torch.randn(m, k, generator=g), torch.randn(k, n, generator=g)
     c_h = torch.randn(m, n, generator=g) if with_c else None
@@ -528,30 +531,32 @@ def test_fp32_dma_tile(capi, ops, oracle, m, n, k, with_c, pad):
     a_s = torch.full((m, k + pad), float("nan")); a_s[:, :k] = a_h
     b_s = torch.full((k, n + pad), float("nan")); b_s[:, :n] = b_h
     a_d, b_d = a_s.cuda()[:, :k], b_s.cuda()[:, :n]
-    d = torch.empty(m, n, device="cuda")
+    d_s = torch.full((m + 1, n + pad), 7.0, device="cuda")
+    d = d_s[:m, :n]
     plan = capi.plan_for(a_d, b_d, None if c_h is None else c_h.cuda(), d, alpha, beta, ops)
     names = plan.names()
     i = names.index("Fp32Mfma16Gemm_256x256_Dma")
+    keep = torch.ones_like(d_s, dtype=torch.bool)
+    keep[:m, :n] = False
     outs = []
     for _ in range(2):
         d.fill_(float("nan"))
         plan.execute(i, torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
         outs.append(d.clone())
+        assert torch.all(d_s[keep] == 7.0), "wrote outside d"
     rep = oracle.tolerance_check(outs[0].cpu().numpy(), ref, k)
     assert rep["ok"], (names[i], rep)
     assert rep["max_abs_err"] <= 1e-2 * rep["bound"], rep
     assert torch.equal(outs[0], outs[1])
 
 
-def test_fp32_dma_tile_skips_other_layouts_and_edges(capi, ops):
+def test_fp32_dma_tile_skips_other_layouts_and_k_tails(capi, ops):
     a = torch.zeros(256, 64, device="cuda")
     b = torch.zeros(64, 256, device="cuda")
     d = torch.empty(256, 256, device="cuda")
     assert "Fp32Mfma16Gemm_256x256_Dma" in capi.plan_for(a, b, None, d, 1.0, 0.0, ops).names()
-    # column-major b, an n edge, a k tail: the whole-tile row-major kernel does not apply
+    # column-major b and a k tail (k % 32 != 0): the row-major, whole-stage kernel does not apply
     assert "Fp32Mfma16Gemm_256x256_Dma" not in capi.plan_for(a, b.t().contiguous().t(), None, d, 1.0, 0.0, ops).names()
-    d2 = torch.empty(256, 200, device="cuda")
-    assert "Fp32Mfma16Gemm_256x256_Dma" not in capi.plan_for(a, b[:, :200], None, d2, 1.0, 0.0, ops).names()
     a3 = torch.zeros(256, 48, device="cuda")
     assert "Fp32Mfma16Gemm_256x256_Dma" not in capi.plan_for(a3, b[:48], None, d, 1.0, 0.0, ops).names()
