@@ -20,34 +20,39 @@ constexpr SplitKind N = SplitKind::kNone, P = SplitKind::kPartial, F = SplitKind
 constexpr FTrainNumericType FP32 = FTRAIN_NUMERIC_TYPE_FP32, BF16 = FTRAIN_NUMERIC_TYPE_BF16,
                             FP16 = FTRAIN_NUMERIC_TYPE_FP16;
 constexpr VariantInfo kInfo[] = {
-    {"Fp32Mfma16Gemm_256x256_Dma", 256, 256, 32, 256, 1, true, N, false, false, false, 0.96, FP32, 256.0, 0.96},
-    {"Fp32Mfma16Gemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, true, 0.909, FP32, 256.0, 0.909},
-    {"Fp32Mfma16Gemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, true, 0.832, FP32, 256.0, 0.832},
-    {"Fp32Mfma16Gemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, true, 0.899, FP32, 256.0, 0.83},
-    {"Fp32Mfma16Gemm_256x128_SplitK", 256, 128, 16, 256, 2, true, P, false, false, true, 0.88, FP32, 256.0, 0.842},
-    {"Fp32Mfma16Gemm_128x256", 128, 256, 16, 256, 2, true, N, false, false, true, 0.897, FP32, 256.0, 0.826},
-    {"Fp32Mfma16Gemm_64x256", 64, 256, 16, 256, 2, true, N, false, false, true, 0.867, FP32, 256.0, 0.794},
-    {"Fp32Mfma16Gemm_64x256_SplitK", 64, 256, 16, 256, 2, true, P, false, false, true, 0.83, FP32, 256.0, 0.761},
-    {"Fp32Mfma16Gemm_256x64", 256, 64, 16, 256, 2, true, N, false, false, true, 0.872, FP32, 256.0, 0.796},
-    {"Fp32Mfma16Gemm_256x64_SplitK", 256, 64, 16, 256, 2, true, P, false, false, true, 0.85, FP32, 256.0, 0.851},
-    {"Fp32MfmaGemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, false, 0.857, FP32, 256.0, 0.857},
-    {"Fp32MfmaGemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, false, 0.84, FP32, 256.0, 0.84},
-    {"Fp32MfmaGemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, false, 0.858, FP32, 256.0, 0.792},
-    {"Fp32MfmaGemm_128x128", 128, 128, 16, 256, 3, true, N, false, false, true, 0.886, FP32, 256.0, 0.762},
-    {"Fp32MfmaGemm_128x128_SplitK", 128, 128, 16, 256, 3, true, P, false, false, true, 0.897, FP32, 256.0, 0.761},
-    {"Fp32MfmaGemm_64x256", 64, 256, 16, 256, 2, true, N, false, false, false, 0.795, FP32, 256.0, 0.64},
-    {"Fp32MfmaGemm_64x256_SplitK", 64, 256, 16, 256, 2, true, P, false, false, false, 0.78, FP32, 256.0, 0.671},
-    {"Fp32MfmaGemm_256x64", 256, 64, 16, 256, 2, true, N, false, false, false, 0.819, FP32, 256.0, 0.744},
-    {"Fp32MfmaGemm_256x64_SplitK", 256, 64, 16, 256, 2, true, P, false, false, false, 0.765, FP32, 256.0, 0.734},
-    {"Fp32MfmaGemm_64x64", 64, 64, 16, 256, 4, true, N, false, false, true, 0.739, FP32, 256.0, 0.604},
-    {"Fp32MfmaGemm_64x64_SplitK", 64, 64, 16, 256, 4, true, P, false, false, true, 0.718, FP32, 256.0, 0.33},
+    {"Fp32Mfma16Gemm_256x256_Dma", 256, 256, 32, 256, 1, true, N, false, false, false, 0.942, FP32, 256.0, 0.942},
+    {"Fp32Mfma16Gemm_256x256_Dma_SplitK", 256, 256, 32, 256, 1, true, P, false, false, false, 0.937, FP32, 256.0, 0.937},
+    {"Fp32Mfma16Gemm_128x128_Dma", 128, 128, 32, 256, 2, true, N, false, false, false, 0.962, FP32, 256.0, 0.975},
+    {"Fp32Mfma16Gemm_128x128_Dma_SplitK", 128, 128, 32, 256, 2, true, P, false, false, false, 0.957, FP32, 256.0, 0.891},
+    {"Fp32Mfma16Gemm_64x256_Dma_SplitK", 64, 256, 32, 256, 2, true, P, false, false, false, 0.964, FP32, 256.0, 0.855},
+    {"Fp32Mfma16Gemm_256x64_Dma_SplitK", 256, 64, 32, 256, 2, true, P, false, false, false, 0.986, FP32, 256.0, 0.976},
+    {"Fp32Mfma16Gemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, true, 0.905, FP32, 256.0, 0.905},
+    {"Fp32Mfma16Gemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, true, 0.828, FP32, 256.0, 0.828},
+    {"Fp32Mfma16Gemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, true, 0.894, FP32, 256.0, 0.824},
+    {"Fp32Mfma16Gemm_256x128_SplitK", 256, 128, 16, 256, 2, true, P, false, false, true, 0.886, FP32, 256.0, 0.819},
+    {"Fp32Mfma16Gemm_128x256", 128, 256, 16, 256, 2, true, N, false, false, true, 0.893, FP32, 256.0, 0.825},
+    {"Fp32Mfma16Gemm_64x256", 64, 256, 16, 256, 2, true, N, false, false, true, 0.866, FP32, 256.0, 0.795},
+    {"Fp32Mfma16Gemm_64x256_SplitK", 64, 256, 16, 256, 2, true, P, false, false, true, 0.826, FP32, 256.0, 0.801},
+    {"Fp32Mfma16Gemm_256x64", 256, 64, 16, 256, 2, true, N, false, false, true, 0.872, FP32, 256.0, 0.778},
+    {"Fp32Mfma16Gemm_256x64_SplitK", 256, 64, 16, 256, 2, true, P, false, false, true, 0.832, FP32, 256.0, 0.742},
+    {"Fp32MfmaGemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, false, 0.856, FP32, 256.0, 0.856},
+    {"Fp32MfmaGemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, false, 0.838, FP32, 256.0, 0.838},
+    {"Fp32MfmaGemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, false, 0.856, FP32, 256.0, 0.796},
+    {"Fp32MfmaGemm_128x128", 128, 128, 16, 256, 3, true, N, false, false, true, 0.878, FP32, 256.0, 0.752},
+    {"Fp32MfmaGemm_128x128_SplitK", 128, 128, 16, 256, 3, true, P, false, false, true, 0.871, FP32, 256.0, 0.82},
+    {"Fp32MfmaGemm_64x256", 64, 256, 16, 256, 2, true, N, false, false, false, 0.792, FP32, 256.0, 0.64},
+    {"Fp32MfmaGemm_64x256_SplitK", 64, 256, 16, 256, 2, true, P, false, false, false, 0.789, FP32, 256.0, 0.667},
+    {"Fp32MfmaGemm_256x64", 256, 64, 16, 256, 2, true, N, false, false, false, 0.821, FP32, 256.0, 0.741},
+    {"Fp32MfmaGemm_256x64_SplitK", 256, 64, 16, 256, 2, true, P, false, false, false, 0.782, FP32, 256.0, 0.721},
+    {"Fp32MfmaGemm_64x64", 64, 64, 16, 256, 4, true, N, false, false, true, 0.731, FP32, 256.0, 0.61},
+    {"Fp32MfmaGemm_64x64_SplitK", 64, 64, 16, 256, 4, true, P, false, false, true, 0.71, FP32, 256.0, 0.508},
     {"Fp32MfmaGemm_128x128_Unaligned", 128, 128, 16, 256, 2, false, N, false, false, true, 0.654, FP32, 256.0, 0.658},
-    {"Fp32MfmaGemm_128x128_Unaligned_SplitK", 128, 128, 16, 256, 2, false, P, false, false, true, 0.703, FP32, 256.0, 0.64},
-    {"Fp32MfmaGemm_64x64_Unaligned", 64, 64, 16, 256, 4, false, N, false, false, true, 0.678, FP32, 256.0, 0.504},
+    {"Fp32MfmaGemm_128x128_Unaligned_SplitK", 128, 128, 16, 256, 2, false, P, false, false, true, 0.693, FP32, 256.0, 0.651},
+    {"Fp32MfmaGemm_64x64_Unaligned", 64, 64, 16, 256, 4, false, N, false, false, true, 0.678, FP32, 256.0, 0.469},
     {"Fp32Gemv", kGemvRows, kGemvPassCols, 1, 1024, 1, true, N, true, false, false, 0, FP32, 256.0, 0},
     {"Fp32Gemv_SplitK", kGemvRows, kGemvCols, 1, 256, 8, true, P, true, false, false, 0, FP32, 256.0, 0},
     {"Fp32Gemv_Unaligned_SplitK", kGemvRows, kGemvCols, 1, 256, 8, false, P, true, false, false, 0, FP32, 256.0, 0},
-    {"Fp32Mfma16Gemm_64x64_DeepK", 64, 64, 32, 256, 1, true, F, false, false, false, 0.655, FP32, 256.0, 0.655},
+    {"Fp32Mfma16Gemm_64x64_DeepK", 64, 64, 32, 256, 1, true, F, false, false, false, 0.704, FP32, 256.0, 0.704},
     {"Fp32Gemm", 64, 64, 16, 256, 2, false, N, false, true, true, 0.2, FP32, 256.0, 0.2},
     {"Bf16MfmaGemm_256x256", 256, 256, 64, 512, 1, true, N, false, false, true, 0.6, BF16, 4096.0, 0.6},
     {"Bf16MfmaGemm_128x128", 128, 128, 64, 256, 2, true, N, false, false, true, 0.4, BF16, 4096.0, 0.4},

@@ -1,17 +1,20 @@
-// FP32 256x256 tile kernel (v_mfma_f32_16x16x4_f32) whose operands reach
-// LDS by DMA (global_load_lds_dwordx4), for row-major a and b.  Device code
-// only; kernels_dma32.hip instantiates it (plain and grouped).
+// FP32 tile kernels (v_mfma_f32_16x16x4_f32) whose operands reach LDS by DMA
+// (global_load_lds_dwordx4), for row-major a and b: 256x256 (4 waves of
+// 128x128, one workgroup per CU) and 64x256 / 256x64 / 128x128 (4 waves of
+// 64x64, two workgroups per CU), whole-k or split-k.  Device code only;
+// kernels_dma32.hip instantiates them (plain and grouped).
 //
 // d = alpha * (a @ b) + beta * c (the reference's formula,
 // src/primitive/hygon/gemm/fp32_gemm.hip:18-31: the beta term dropped for a
-// null c, always evaluated otherwise).  Applicability, checked on the host:
-// k a positive multiple of 32, n a multiple of 4, 16-byte aligned a, b, c, d
-// with leading dimensions multiples of 4, a's and b's below 2^22 elements and
-// c's and d's below 2^21 (32-bit offsets); m and n are free otherwise (edge
-// tiles clamp their loads and drop their out-of-matrix stores).
+// null c, always evaluated otherwise); the split-k form writes each split's
+// raw partial tile to slice z of the workspace (dense m x n) and
+// splitk_reduce forms d.  Applicability, checked on the host: k a positive
+// multiple of 32, n a multiple of 4, 16-byte aligned a, b, c, d with leading
+// dimensions multiples of 4, a's and b's below 2^22 elements and c's and d's
+// below 2^21 (32-bit offsets); m and n are free otherwise (edge tiles clamp
+// their loads and drop their out-of-matrix stores).
 //
-// Workgroup: 4 waves (one per SIMD), each a 128x128 block of 8x8 MFMA blocks
-// (16x16 outputs, 256 accumulators per lane):
+// Wave tile: TM x TN blocks of 16x16 outputs:
 //   A operand: lane l holds A[row l % 16][k slot g = l / 16]
 //   B operand: lane l holds B[k slot g][col l % 16]
 //   result   : lane l, register r holds D[row 4 g + r][col l % 16]
@@ -22,22 +25,23 @@
 // at one k serves four blocks, and each epilogue store writes four adjacent
 // columns.
 //
-// Stage = 32 k of both operands, 32 KiB each; two stages (128 KiB).  One DMA
-// instruction moves 64 lanes x 16 bytes into 1 KiB of LDS at M0 + 16 * lane:
-//   A [256 rows][32 k]: a DMA covers 8 rows (whole 128-byte lines); 16-byte
+// Stage = 32 k of both operands (BM x 32 and 32 x BN floats); two stages.
+// One DMA instruction moves 64 lanes x 16 bytes into 1 KiB of LDS at
+// M0 + 16 * lane:
+//   A [BM rows][32 k]: a DMA covers 8 rows (whole 128-byte lines); 16-byte
 //     chunk c of row r sits at slot c ^ h(r) (a_swz below);
-//   B [32 k][256 cols]: a DMA covers one k row (1 KiB); chunk c of k row kr
-//     sits at slot c ^ (16 * ((kr >> 3) & 1)), separating the two k rows a
-//     half-wave reads.
+//   B [32 k][BN cols]: a DMA covers 256 / BN k rows; for BN >= 128 chunk c of
+//     k row kr sits at slot c ^ (16 * ((kr >> 3) & 1)), separating the two k
+//     rows a half-wave reads (a 64-wide row has no second half to swap with).
 //
 // Pipeline per stage st (buffer X; stage st + 1 in Y), per wave: k-steps
 // 0..3 from registers while reading k-steps 4..7 of X; wait for this wave's
 // LDS reads and DMAs, barrier (every wave is done with X, stage st + 1 has
 // landed in Y); k-steps 4..7 while reading k-steps 0..3 of Y and issuing the
-// DMA of stage st + 2 into X.  One barrier per 512 MFMAs (16384 MFMA cycles).
-// The DMA is issued from inline assembly with M0 set in the same statement;
-// every wait on it is an explicit vmcnt in this file, and the compiler has
-// no other use of M0 here (no LDS DMA builtins, no indexed register access).
+// DMA of stage st + 2 into X.  The DMA is issued from inline assembly with
+// M0 set in the same statement; every wait on it is an explicit vmcnt in
+// this file, and the compiler has no other use of M0 here (no LDS DMA
+// builtins, no indexed register access).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -51,11 +55,10 @@ namespace ftrain::gemm::d32 {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kTile = 256, kStageK = 32;
+constexpr int kStageK = 32;
 // Word 3 of a raw (untyped, stride 0) buffer resource on gfx9 parts: 32-bit data format, the range
 // check against num_records on every access.
 constexpr int kBufferConfig = 0x00020000;
-constexpr int kStageFloats = kTile * kStageK;  // one operand, one stage: 32 KiB
 
 __device__ __forceinline__ void dma_1k(unsigned voff, const void* sbase, unsigned lds) {
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(sbase)
@@ -87,43 +90,78 @@ __device__ __forceinline__ int a_swz(int row) {
     return ((row >> 2) & 1) | (((row >> 1) & 1) << 1) | (((row >> 3) & 1) << 2);
 }
 
-// Output tile `bid` of p (tile_of order); the whole workgroup calls it.
-__device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid) {
-    __shared__ __attribute__((aligned(1024))) float As0[kStageFloats];
-    __shared__ __attribute__((aligned(1024))) float Bs0[kStageFloats];
-    __shared__ __attribute__((aligned(1024))) float As1[kStageFloats];
-    __shared__ __attribute__((aligned(1024))) float Bs1[kStageFloats];
+// Output tile `bid`, k split z of p; the whole workgroup calls it.
+template <int BM, int BN, int WM, int WN, bool SPLIT>
+__device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid, int z) {
+    static_assert(WM * WN == 4, "4 waves");
+    constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 16, TN = WTN / 16, NC = TN / 4;
+    static_assert(TN % 4 == 0 && TM >= 1, "column runs of four blocks");
+    constexpr int DA = BM / 32;        // A DMAs per wave per stage (8-row blocks)
+    constexpr int RB = 256 / BN;       // k rows per B DMA
+    constexpr int DB = 8 / RB;         // B DMAs per wave per stage
+    constexpr int ND = DA + DB;        // DMAs per wave per stage
+    constexpr int CPR = BN / 4;        // 16-byte chunks per B k row
+    constexpr bool BSWZ = CPR >= 32;   // B k rows have a second half to swap
+    constexpr int NR = TM + 4 * NC;    // LDS reads per wave per half stage
+    constexpr int SLOTS = 4 * TM;      // groups of TN MFMAs per half stage
+    constexpr int A_FLOATS = BM * kStageK, B_FLOATS = kStageK * BN;
+
+    __shared__ __attribute__((aligned(1024))) float As0[A_FLOATS];
+    __shared__ __attribute__((aligned(1024))) float Bs0[B_FLOATS];
+    __shared__ __attribute__((aligned(1024))) float As1[A_FLOATS];
+    __shared__ __attribute__((aligned(1024))) float Bs1[B_FLOATS];
     const int tid = threadIdx.x, lane = tid & 63, j16 = lane & 15, g = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wrow = (wave >> 1) * 128, wcol = (wave & 1) * 128;
+    const int wrow = (wave / WN) * WTM, wcol = (wave % WN) * WTN;
     int tm, tn;
     tile_of(bid, p.tiles_m, p.tiles_n, tm, tn);
-    const int m0 = tm * kTile, n0 = tn * kTile;
+    const int m0 = tm * BM, n0 = tn * BN;
     const int M = p.m, N = p.n;
-    const int nst = p.k / kStageK;
+    const int kbeg = SPLIT ? z * p.k_chunk : 0;
+    const int kend = SPLIT ? min(p.k, kbeg + p.k_chunk) : p.k;
+    const int nst  = (kend - kbeg) / kStageK;
     const int64_t lda = p.lda, ldb = p.ldb;
 
     // DMA sources.  A block q = wave + 4 j: rows 8q .. 8q + 7 (lane: row 8q + lane / 8), slot
     // lane % 8 holds chunk (lane % 8) ^ h(row); h does not depend on j (32 j leaves bits 1-3).
     // Rows past the matrix are clamped onto its last row (they feed only outputs that are not
     // stored); 255 rows of lda < 2^22 keep the lane offset below 2^32.
-    const unsigned ar      = 8 * wave + (lane >> 3);
-    const unsigned achunk  = 16 * ((lane & 7) ^ a_swz(ar));
-    const unsigned alast   = static_cast<unsigned>(min(M - 1 - m0, kTile - 1));
-    const unsigned lda4    = static_cast<unsigned>(4 * lda);
-    const char* abase      = reinterpret_cast<const char*>(p.a + (size_t)m0 * lda);
-    // B block q = wave + 4 j: k row q (lane: slot lane), chunk lane ^ (16 ((q >> 3) & 1)); a chunk
-    // past n is clamped onto the last whole one (n % 4 == 0).
-    const char* bbase    = reinterpret_cast<const char*>(p.b + n0);
-    const unsigned boff0 = static_cast<unsigned>(4 * (min(n0 + 4 * lane, N - 4) - n0));
-    const unsigned boff1 = static_cast<unsigned>(4 * (min(n0 + 4 * (lane ^ 16), N - 4) - n0));
+    const unsigned ar     = 8 * wave + (lane >> 3);
+    const unsigned achunk = 16 * ((lane & 7) ^ a_swz(ar));
+    const unsigned alast  = static_cast<unsigned>(min(M - 1 - m0, BM - 1));
+    const unsigned lda4   = static_cast<unsigned>(4 * lda);
+    const char* abase     = reinterpret_cast<const char*>(p.a + (size_t)m0 * lda + kbeg);
+    // B block q = wave + 4 j: k rows RB q .. RB q + RB - 1 (lane: row RB q + lane / CPR), slot
+    // lane % CPR holds chunk (lane % CPR) ^ swizzle; a chunk past n is clamped onto the last whole
+    // one (n % 4 == 0).  x = the swizzle bit of the block's k rows.
+    const char* bbase = reinterpret_cast<const char*>(p.b + (size_t)kbeg * ldb + n0);
+    auto boff = [&](int x) {
+        const int kr = lane / CPR, chunk = (lane % CPR) ^ (x ? 16 : 0);
+        return static_cast<unsigned>((kr * ldb + (min(n0 + 4 * chunk, N - 4) - n0)) * 4);
+    };
+    const unsigned boff0 = boff(0), boff1 = BSWZ ? boff(1) : boff0;
     auto dma_a = [&](int st, int j, unsigned lds) {
         const unsigned row = min(ar + 32u * j, alast);
         dma_1k(row * lda4 + achunk, abase + (size_t)st * kStageK * 4, lds + (wave + 4 * j) * 1024);
     };
     auto dma_b = [&](int st, int j, unsigned lds) {
-        const int q = wave + 4 * j;
-        dma_1k(((q >> 3) & 1) ? boff1 : boff0, bbase + ((size_t)st * kStageK + q) * ldb * 4, lds + q * 1024);
+        const int q = wave + 4 * j, kr0 = RB * q;
+        dma_1k(BSWZ && ((kr0 >> 3) & 1) ? boff1 : boff0, bbase + ((size_t)st * kStageK + kr0) * ldb * 4,
+               lds + q * 1024);
+    };
+    // DMA d (0 .. ND - 1) of a stage: A and B alternate while both have some left.
+    auto dma_one = [&](int st, int d, unsigned la, unsigned lb) {
+        constexpr int PAIRS = DA < DB ? DA : DB;
+        if (d < 2 * PAIRS) {
+            if (d & 1)
+                dma_b(st, d >> 1, lb);
+            else
+                dma_a(st, d >> 1, la);
+        } else if (DA > DB) {
+            dma_a(st, d - PAIRS, la);
+        } else {
+            dma_b(st, d - PAIRS, lb);
+        }
     };
     const unsigned la0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) float*)As0;
     const unsigned lb0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) float*)Bs0;
@@ -138,108 +176,103 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid)
     // B operands of k-step s for column run cc (blocks 4 cc .. 4 cc + 3): B[8 g + s][4 cols].
     auto rd_b = [&](const float* T, int s, int cc) {
         const int kr = 8 * g + s, c = (wcol >> 2) + 16 * cc + j16;
-        return *reinterpret_cast<const floatx4*>(T + kr * kTile + 4 * (c ^ (16 * ((kr >> 3) & 1))));
+        return *reinterpret_cast<const floatx4*>(T + kr * BN + 4 * (BSWZ ? c ^ (16 * ((kr >> 3) & 1)) : c));
     };
 
-    floatx4 acc[8][8];
+    floatx4 acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     // Operands of one half stage: fa[bi] (4 k-steps), fb[s][cc].
-    floatx4 fa0[8], fb0[4][2], fa1[8], fb1[4][2];
-    // Read r (0..15) of half hf: 8 A reads, then 8 B reads (k-step major).
-    auto read_one = [&](floatx4 (&ga)[8], floatx4 (&gb)[4][2], const float* As, const float* Bs, int hf, int r) {
-        if (r < 8)
+    floatx4 fa0[TM], fb0[4][NC], fa1[TM], fb1[4][NC];
+    // Read r (0 .. NR - 1) of half hf: TM A reads, then the B reads (k-step major).
+    auto read_one = [&](floatx4 (&ga)[TM], floatx4 (&gb)[4][NC], const float* As, const float* Bs, int hf, int r) {
+        if (r < TM)
             ga[r] = rd_a(As, r, hf);
         else
-            gb[(r - 8) >> 1][(r - 8) & 1] = rd_b(Bs, 4 * hf + ((r - 8) >> 1), (r - 8) & 1);
+            gb[(r - TM) / NC][(r - TM) % NC] = rd_b(Bs, 4 * hf + (r - TM) / NC, (r - TM) % NC);
     };
-    // 256 MFMAs of one half stage on (fa, fb), k-step major, in 32 slots of 8 (one block row at
-    // one k-step); the 16 reads into (ga, gb) follow the even slots, and with a true with_dma the
-    // 16 DMAs of stage dma_st the odd ones.  The scheduling groups pin that order (left to
-    // itself the scheduler bunched the reads at the end of the half: 0.929-0.937 of peak at
-    // 8192^3 against 0.962-0.964).
-    auto run_half = [&](floatx4 (&fa)[8], floatx4 (&fb)[4][2], floatx4 (&ga)[8], floatx4 (&gb)[4][2],
+    // The MFMAs of one half stage on (fa, fb), k-step major, in SLOTS groups of TN (one block row
+    // at one k-step); the NR reads into (ga, gb) spread over the slots, and with a true with_dma
+    // the ND DMAs of stage dma_st too.  The scheduling groups pin that order (left to itself the
+    // scheduler bunched the reads at the end of the half: 0.929-0.937 of peak at 8192^3 on the
+    // 256x256 tile against 0.962-0.964).
+    auto run_half = [&](floatx4 (&fa)[TM], floatx4 (&fb)[4][NC], floatx4 (&ga)[TM], floatx4 (&gb)[4][NC],
                         const float* As, const float* Bs, int hf, auto with_dma, int dma_st, unsigned la,
                         unsigned lb) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
 #pragma unroll
-            for (int bi = 0; bi < 8; ++bi) {
+            for (int bi = 0; bi < TM; ++bi) {
 #pragma unroll
-                for (int bj = 0; bj < 8; ++bj)
+                for (int bj = 0; bj < TN; ++bj)
                     acc[bi][bj] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[bi][s], fb[s][bj >> 2][bj & 3], acc[bi][bj],
                                                                       0, 0, 0);
-                const int u = 8 * s + bi;
-                // Read r at slot 2 r: the 16 reads spread over all 32 slots of 8 MFMAs.
+                const int u = TM * s + bi;
+                bool read = false;
 #pragma unroll
-                for (int r = 0; r < 16; ++r)
-                    if (2 * r == u) read_one(ga, gb, As, Bs, hf, r);
-                // Keep each slot's 8 MFMAs, then its read, in that order.
-                __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-                if ((u & 1) == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                if constexpr (decltype(with_dma)::value) {
-                    if (u & 1) {
-                        const int v = u >> 1;
-                        if (v & 1)
-                            dma_b(dma_st, v >> 1, lb);
-                        else
-                            dma_a(dma_st, v >> 1, la);
+                for (int r = 0; r < NR; ++r)
+                    if ((r * SLOTS) / NR == u) {
+                        read_one(ga, gb, As, Bs, hf, r);
+                        read = true;
                     }
+                // Keep each slot's MFMAs, then its read, in that order.
+                __builtin_amdgcn_sched_group_barrier(0x008, TN, 0);
+                if (read) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                if constexpr (decltype(with_dma)::value) {
+#pragma unroll
+                    for (int d = 0; d < ND; ++d)
+                        if (((2 * d + 1) * SLOTS) / (2 * ND) == u) dma_one(dma_st, d, la, lb);
                 }
             }
         }
     };
-    auto read_half = [&](floatx4 (&ga)[8], floatx4 (&gb)[4][2], const float* As, const float* Bs, int hf) {
+    auto read_half = [&](floatx4 (&ga)[TM], floatx4 (&gb)[4][NC], const float* As, const float* Bs, int hf) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) read_one(ga, gb, As, Bs, hf, r);
+        for (int r = 0; r < NR; ++r) read_one(ga, gb, As, Bs, hf, r);
     };
 
+    // Every launch has at least one stage (k > 0; a split's chunk is a whole number of stages).
+    {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        dma_a(0, j, la0);
-        dma_b(0, j, lb0);
-    }
-    const int st1 = min(1, nst - 1);
+        for (int d = 0; d < ND; ++d) dma_one(0, d, la0, lb0);
+        const int st1 = min(1, nst - 1);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        dma_a(st1, j, la1);
-        dma_b(st1, j, lb1);
-    }
-    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-    read_half(fa0, fb0, As0, Bs0, 0);
+        for (int d = 0; d < ND; ++d) dma_one(st1, d, la1, lb1);
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(ND) : "memory");
+        read_half(fa0, fb0, As0, Bs0, 0);
 
-    // Stages past the last reload the last one (nothing reads them).  The operand sets rotate by
-    // copying (f1 -> f0 after each half); the allocator coalesces the copies, where alternating
-    // the two sets by reference kept both live in separate registers and spilled.
-    auto rotate = [&] {
+        // Stages past the last reload the last one (nothing reads them).  The operand sets rotate
+        // by copying (f1 -> f0 after each half); the allocator coalesces the copies, where
+        // alternating the two sets by reference kept both live in separate registers and spilled.
+        auto rotate = [&] {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) fa0[i] = fa1[i];
+            for (int i = 0; i < TM; ++i) fa0[i] = fa1[i];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            fb0[i][0] = fb1[i][0];
-            fb0[i][1] = fb1[i][1];
-        }
-    };
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int c = 0; c < NC; ++c) fb0[i][c] = fb1[i][c];
+        };
 #define FT_DMA32_PHASE(XA, XB, YA, YB, LXA, LXB, ST)                                              \
     run_half(fa0, fb0, fa1, fb1, XA, XB, 1, std::false_type{}, 0, 0u, 0u);                        \
     rotate();                                                                                     \
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");         \
     run_half(fa0, fb0, fa1, fb1, YA, YB, 0, std::true_type{}, min((ST) + 2, nst - 1), LXA, LXB);  \
     rotate();
-    int st = 0;
-    for (; st + 1 < nst; st += 2) {
-        FT_DMA32_PHASE(As0, Bs0, As1, Bs1, la0, lb0, st)
-        FT_DMA32_PHASE(As1, Bs1, As0, Bs0, la1, lb1, st + 1)
-    }
-    if (st < nst) {
-        FT_DMA32_PHASE(As0, Bs0, As1, Bs1, la0, lb0, st)
-    }
+        int st = 0;
+        for (; st + 1 < nst; st += 2) {
+            FT_DMA32_PHASE(As0, Bs0, As1, Bs1, la0, lb0, st)
+            FT_DMA32_PHASE(As1, Bs1, As0, Bs0, la1, lb1, st + 1)
+        }
+        if (st < nst) {
+            FT_DMA32_PHASE(As0, Bs0, As1, Bs1, la0, lb0, st)
+        }
 #undef FT_DMA32_PHASE
-    // The workgroup's LDS must not be released with a DMA still writing it.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // The workgroup's LDS must not be released with a DMA still writing it.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
 
     // Epilogue, one row block at a time: block (bi, bj) register r is D[row 16 bi + 4 g + r][col
     // (bj / 4) * 64 + 4 j16 + bj % 4], four adjacent columns per 128-bit access; c of row block
@@ -247,16 +280,18 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid)
     // lane part of the offset (4 g rows, 4 j16 columns) in the VGPR offset, the block part in the
     // scalar offset.  An element outside the matrix gets the lane offset 2^31, past the buffer's
     // size (at most 2^31 - 1 bytes), so its c load returns 0 and its store is dropped; ldc and
-    // ldd below 2^21 keep every sum below 2^32.
+    // ldd below 2^21 keep every sum below 2^32.  Split-k: the raw sums go to slice z (dense
+    // m x n, row stride n).
     const float alpha = p.alpha, beta = p.beta;
     const int rows_left = M - m0, cols_left = N - n0;
     auto span = [&](uint64_t ld) {
         const uint64_t b = ((uint64_t)(rows_left - 1) * ld + (uint64_t)cols_left) * 4;
         return static_cast<int>(b < 0x7FFFFFFFull ? b : 0x7FFFFFFFull);
     };
-    const __amdgpu_buffer_rsrc_t dres =
-        __builtin_amdgcn_make_buffer_rsrc(p.d + (size_t)m0 * p.ldd + n0, 0, span(p.ldd), kBufferConfig);
-    const unsigned ldd = static_cast<unsigned>(p.ldd), ldc = static_cast<unsigned>(p.ldc);
+    const uint64_t ldd64 = SPLIT ? (uint64_t)N : (uint64_t)p.ldd;
+    float* const dcorner = SPLIT ? p.d + (size_t)z * M * N + (size_t)m0 * N + n0 : p.d + (size_t)m0 * p.ldd + n0;
+    const __amdgpu_buffer_rsrc_t dres = __builtin_amdgcn_make_buffer_rsrc(dcorner, 0, span(ldd64), kBufferConfig);
+    const unsigned ldd = static_cast<unsigned>(ldd64), ldc = static_cast<unsigned>(p.ldc);
     constexpr unsigned kOut = 0x80000000u;
     const unsigned lane_d = (4 * g * ldd + 4 * j16) * 4, lane_c = (4 * g * ldc + 4 * j16) * 4;
     auto run = [&](auto c_tag) {
@@ -265,13 +300,13 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid)
         if constexpr (HAS_C)
             cres = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.c) + (size_t)m0 * p.ldc + n0, 0,
                                                      span(p.ldc), kBufferConfig);
-        floatx4 cv[HAS_C ? 2 : 1][4][2];
-        auto load_c = [&](int bi, floatx4 (&dst)[4][2]) {
+        floatx4 cv[HAS_C ? 2 : 1][4][NC];
+        auto load_c = [&](int bi, floatx4 (&dst)[4][NC]) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row0 = wrow + 16 * bi + r;  // row of lane group 0
 #pragma unroll
-                for (int q = 0; q < 2; ++q) {
+                for (int q = 0; q < NC; ++q) {
                     const int c0  = wcol + 64 * q;
                     const bool ok = 4 * g < rows_left - row0 && c0 + 4 * j16 < cols_left;
                     dst[r][q]     = __builtin_bit_cast(
@@ -282,21 +317,25 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid)
         };
         if constexpr (HAS_C) load_c(0, cv[0]);
 #pragma unroll
-        for (int bi = 0; bi < 8; ++bi) {
+        for (int bi = 0; bi < TM; ++bi) {
             if constexpr (HAS_C)
-                if (bi + 1 < 8) load_c(bi + 1, cv[(bi + 1) & 1]);
+                if (bi + 1 < TM) load_c(bi + 1, cv[(bi + 1) & 1]);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row0 = wrow + 16 * bi + r;
 #pragma unroll
-                for (int q = 0; q < 2; ++q) {
+                for (int q = 0; q < NC; ++q) {
                     const int c0  = wcol + 64 * q;
                     const bool ok = 4 * g < rows_left - row0 && c0 + 4 * j16 < cols_left;
                     floatx4 out;
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
-                        out[t] = alpha * acc[bi][4 * q + t][r];
-                        if constexpr (HAS_C) out[t] += beta * cv[HAS_C ? bi & 1 : 0][r][q][t];
+                        if constexpr (SPLIT) {
+                            out[t] = acc[bi][4 * q + t][r];
+                        } else {
+                            out[t] = alpha * acc[bi][4 * q + t][r];
+                            if constexpr (HAS_C) out[t] += beta * cv[HAS_C ? bi & 1 : 0][r][q][t];
+                        }
                     }
                     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, out), dres, ok ? lane_d : kOut,
                                                            static_cast<int>((row0 * ldd + c0) * 4), 0);
@@ -304,19 +343,35 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid)
             }
         }
     };
-    if (p.c != nullptr)
+    if (!SPLIT && p.c != nullptr)
         run(std::true_type{});
     else
         run(std::false_type{});
 }
 
-__global__ __launch_bounds__(256, 1) void fp32_gemm_dma(GemmParams p) { fp32_gemm_dma_tile(p, blockIdx.x); }
+template <int BM, int BN, int WM, int WN, int MINB, bool SPLIT>
+__global__ __launch_bounds__(256, MINB) void fp32_gemm_dma(GemmParams p) {
+    int bid = blockIdx.x, z = blockIdx.z;
+    if constexpr (SPLIT) {
+        // Workgroups are dealt to the 8 XCDs in grid order (x fastest); renumber so each XCD runs
+        // whole k splits and every tile of a split reuses the split's operand slices from one L2.
+        const int tiles = gridDim.x, total = tiles * gridDim.z;
+        if ((total & 7) == 0) {
+            const int lin = blockIdx.x + tiles * blockIdx.z;
+            const int w   = (lin & 7) * (total >> 3) + (lin >> 3);
+            z             = w / tiles;
+            const int t   = w - z * tiles, per = tiles >> 3;
+            bid           = t < (per << 3) ? ((t % per) << 3) + t / per : t;
+        }
+    }
+    fp32_gemm_dma_tile<BM, BN, WM, WN, SPLIT>(p, bid, z);
+}
 
-// Grouped GEMM over a device table of per-group parameters: the workgroup's
-// group is the last one whose first tile id is at most its own.  Group starts
-// are multiples of 8, so the group-local id keeps the hardware id's XCD; ids
-// past the group's tiles are padding and exit at once (the whole workgroup,
-// before any barrier).
+// Grouped GEMM over a device table of per-group parameters (256x256 whole-k
+// tiles): the workgroup's group is the last one whose first tile id is at
+// most its own.  Group starts are multiples of 8, so the group-local id keeps
+// the hardware id's XCD; ids past the group's tiles are padding and exit at
+// once (the whole workgroup, before any barrier).
 __global__ __launch_bounds__(256, 1) void grouped_fp32_gemm_dma(GroupedGemmArgs g) {
     const int bid = blockIdx.x;
     int lo = 0, hi = g.groups - 1;
@@ -330,7 +385,7 @@ __global__ __launch_bounds__(256, 1) void grouped_fp32_gemm_dma(GroupedGemmArgs 
     const GemmParams p = g.params[lo];
     const int local    = bid - g.tile_start[lo];
     if (local >= p.tiles_m * p.tiles_n) return;
-    fp32_gemm_dma_tile(p, local);
+    fp32_gemm_dma_tile<256, 256, 2, 2, false>(p, local, 0);
 }
 
 }  // namespace ftrain::gemm::d32

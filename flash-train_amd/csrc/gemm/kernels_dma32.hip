@@ -1,9 +1,19 @@
-// FP32 256x256 tiles with LDS staging by DMA, row-major a and b, plain and grouped (see gemm/dma32_tile.hpp).
+// FP32 tiles with LDS staging by DMA, row-major a and b, plain and grouped (see gemm/dma32_tile.hpp).
 #include "dma32_tile.hpp"
 
 namespace ftrain::gemm {
 
-const void* dma32Kernel() { return reinterpret_cast<const void*>(&d32::fp32_gemm_dma); }
+const void* dma32Kernel(Variant v) {
+    switch (v) {
+        case Variant::kMfma16Dma256x256: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<256, 256, 2, 2, 1, false>);
+        case Variant::kMfma16Dma256x256S: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<256, 256, 2, 2, 1, true>);
+        case Variant::kMfma16Dma128x128: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<128, 128, 2, 2, 2, false>);
+        case Variant::kMfma16Dma128x128S: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<128, 128, 2, 2, 2, true>);
+        case Variant::kMfma16Dma64x256S: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<64, 256, 1, 4, 2, true>);
+        case Variant::kMfma16Dma256x64S: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<256, 64, 4, 1, 2, true>);
+        default: return nullptr;
+    }
+}
 
 const void* groupedDma32Kernel() { return reinterpret_cast<const void*>(&d32::grouped_fp32_gemm_dma); }
 

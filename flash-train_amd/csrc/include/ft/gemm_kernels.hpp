@@ -123,10 +123,15 @@ constexpr int kGemvHalfRows = 4;
 enum class Variant : int {
     // v_mfma_f32_16x16x4_f32 256x256 tiles, 4 waves of 128x128 (one per
     // SIMD), 128-bit loads, every operand orientation; whole-k and split-k.
-    // fp32 256x256 tiles with operands staged into LDS by DMA
-    // (global_load_lds_dwordx4), v_mfma_f32_16x16x4_f32: row-major a and b,
-    // k a multiple of 32, any m and n.
+    // fp32 tiles with operands staged into LDS by DMA (global_load_lds_dwordx4),
+    // v_mfma_f32_16x16x4_f32: row-major a and b, k a multiple of 32, any m and
+    // n; 256x256 (one workgroup per CU) and 128x128 whole-k, and split-k forms.
     kMfma16Dma256x256,
+    kMfma16Dma256x256S,
+    kMfma16Dma128x128,
+    kMfma16Dma128x128S,
+    kMfma16Dma64x256S,
+    kMfma16Dma256x64S,
     kMfma16_256x256,
     kMfma16_256x256S,
     // Same instruction, 256x128 tiles of 4 waves of 128x64, two workgroups
@@ -267,7 +272,7 @@ const void* halfKernelFp16TN(int tile);
 const void* halfKernelFp16NT(int tile);
 const void* halfKernelFp16TT(int tile);
 // The DMA-staged 256x256 tiles per input type and operand orientation.
-const void* dma32Kernel();
+const void* dma32Kernel(Variant v);
 const void* groupedDma32Kernel();
 const void* dmaKernelBf16(bool ta, bool tb);
 const void* dmaKernelFp16(bool ta, bool tb);
