@@ -73,6 +73,8 @@ FTRAIN_TESTING_API uint32_t ftrainTestingChooseSplits(int v, uint64_t m, uint64_
     return gemm::chooseSplits(static_cast<gemm::Variant>(v), GemmShape{m, n, k}, cus);
 }
 
+FTRAIN_TESTING_API void ftrainTestingForceSplits(uint32_t s) { gemm::forceSplits(s); }
+
 // ---- selection cache ----
 
 FTRAIN_TESTING_API void* ftrainTestingCacheCreate(uint64_t max_entries, uint64_t shards) {

@@ -65,6 +65,17 @@ __device__ __forceinline__ void dma_1k(unsigned voff, const void* sbase, unsigne
                  : "memory", "m0");
 }
 
+// 128-bit buffer store whose data registers stay unwritten for two wait states after it.  A VALU
+// write of a store's data VGPRs right after a buffer_store_dwordx4 replaced the first dword of
+// some lanes' data on MI355X (measured: the dword took the value the next instruction wrote),
+// and the compiler inserts no wait for a buffer store with a register soffset.  The asm keeps
+// `v` live past the store (so no write to its registers can come earlier) and waits there.
+__device__ __forceinline__ void store_b128(floatx4 v, __amdgpu_buffer_rsrc_t res, unsigned voff, int soff) {
+    const u32x4 x = __builtin_bit_cast(u32x4, v);
+    __builtin_amdgcn_raw_buffer_store_b128(x, res, voff, soff, 0);
+    asm volatile("s_nop 1" ::"v"(x) : "memory");
+}
+
 // Output tile of workgroup `bid`: the 8 XCDs take contiguous runs of tile
 // ids (hardware ids are dealt to XCDs in turn), walked in bands of 4 tile
 // rows.
@@ -337,8 +348,7 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
                             if constexpr (HAS_C) out[t] += beta * cv[HAS_C ? bi & 1 : 0][r][q][t];
                         }
                     }
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, out), dres, ok ? lane_d : kOut,
-                                                           static_cast<int>((row0 * ldd + c0) * 4), 0);
+                    store_b128(out, dres, ok ? lane_d : kOut, static_cast<int>((row0 * ldd + c0) * 4));
                 }
             }
         }

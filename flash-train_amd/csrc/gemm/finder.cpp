@@ -34,10 +34,10 @@ namespace gemm {
 namespace {
 constexpr double kClockPerMicro = 2.4e3;  // peak engine clock (MHz)
 constexpr double kHbmBytesPerMicro = 8.0e6 * 0.8;  // sustained HBM bytes per microsecond
-constexpr double kLaunchMicros = 2.37;
-constexpr double kPoolMicros      = 1.40;  // dependency gap before the reduction kernel (fitted)
+constexpr double kLaunchMicros = 1.67;
+constexpr double kPoolMicros      = 1.10;  // dependency gap before the reduction kernel (fitted)
 // The reduction kernel's pass over the partial tiles, relative to HBM time (fitted).
-constexpr double kReduceFactor    = 0.893;
+constexpr double kReduceFactor    = 0.928;
 // The deep-k kernel (SplitKind::kFused): ramp of its single round, and the
 // tile's last workgroup storing, counting and gathering the partial tiles
 // (measured on MI355X: 3.7 us at 4 splits, 11-12 us at 16; the per-split
@@ -50,7 +50,7 @@ constexpr double kFusedPerSplitMicros = 0.9;
 constexpr double kFusedStoreMicros    = 2.0;  // per round: a split workgroup's partial store and count
 // Fixed cost per round of resident workgroups (operand prologue, epilogue
 // stores, the ramp of the first stages); fitted with the catalog efficiencies.
-constexpr double kRoundMicros     = 3.83;
+constexpr double kRoundMicros     = 6.02;
 constexpr uint64_t kMinSplitDepth = 256;  // reduction depth worth one split-k workgroup
 constexpr uint64_t kMinGemvDepth  = 64;
 
@@ -139,9 +139,26 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
 
 }  // namespace
 
+namespace {
+std::atomic<uint32_t> g_forced_splits{0};
+}
+
+void forceSplits(uint32_t s) { g_forced_splits.store(s, std::memory_order_relaxed); }
+
 uint32_t chooseSplits(Variant v, const GemmShape& s, int cus) {
     const VariantInfo& vi = info(v);
     if (vi.split == SplitKind::kNone) return 1;
+    if (const uint32_t forced = g_forced_splits.load(std::memory_order_relaxed); forced > 0 && !vi.gemv) {
+        // Clamped to whole reduction steps per split, the workspace cap, and
+        // (deep-k) one arrival counter per tile.
+        const uint64_t tiles = std::max<uint64_t>(ceilDiv(s.m, vi.bm) * ceilDiv(s.n, vi.bn), 1);
+        const uint64_t unit  = vi.split == SplitKind::kPartial ? s.m * s.n * sizeof(float)
+                                                               : tiles * vi.bm * vi.bn * sizeof(float);
+        const uint64_t most =
+            std::min<uint64_t>(s.k / vi.bk, (kMaxPartialBytes - kCounterBytes) / std::max<uint64_t>(unit, 1));
+        const uint64_t got = std::min<uint64_t>(forced, most);
+        return static_cast<uint32_t>(got >= 2 ? got : vi.split == SplitKind::kPartial ? 0 : 1);
+    }
     const uint64_t min_depth = vi.gemv ? kMinGemvDepth : kMinSplitDepth;
     uint64_t most            = std::min<uint64_t>(1024, s.k / min_depth);
     if (vi.split == SplitKind::kPartial && s.m * s.n > 0)

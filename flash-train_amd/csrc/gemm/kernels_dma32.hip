@@ -11,6 +11,9 @@ const void* dma32Kernel(Variant v) {
         case Variant::kMfma16Dma128x128S: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<128, 128, 2, 2, 2, true>);
         case Variant::kMfma16Dma64x256S: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<64, 256, 1, 4, 2, true>);
         case Variant::kMfma16Dma256x64S: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<256, 64, 4, 1, 2, true>);
+        case Variant::kMfma16Dma64x128S: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<64, 128, 2, 2, 2, true>);
+        case Variant::kMfma16Dma128x64S: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<128, 64, 4, 1, 2, true>);
+        case Variant::kMfma16Dma64x64S: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<64, 64, 4, 1, 2, true>);
         default: return nullptr;
     }
 }

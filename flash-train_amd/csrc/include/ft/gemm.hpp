@@ -120,6 +120,10 @@ namespace gemm {
 // Split count a split-k variant uses for a shape on a device with `cus`
 // compute units (>= 2), or 0 when the reduction is too shallow to split.
 uint32_t chooseSplits(Variant v, const GemmShape& s, int cus);
+// Test hook: with s > 0, every split-k variant takes s splits (clamped to what
+// its workspace, counters and k allow) instead of the modelled choice; 0
+// restores the model.  Process-wide.
+void forceSplits(uint32_t s);
 
 // Modelled execution time in microseconds (lower is better).
 double estimateMicros(Variant v, const GemmShape& s, bool has_c, int cus);

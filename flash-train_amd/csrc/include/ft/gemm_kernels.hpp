@@ -132,6 +132,9 @@ enum class Variant : int {
     kMfma16Dma128x128S,
     kMfma16Dma64x256S,
     kMfma16Dma256x64S,
+    kMfma16Dma64x128S,
+    kMfma16Dma128x64S,
+    kMfma16Dma64x64S,
     kMfma16_256x256,
     kMfma16_256x256S,
     // Same instruction, 256x128 tiles of 4 waves of 128x64, two workgroups

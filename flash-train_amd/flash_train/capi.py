@@ -122,6 +122,7 @@ def _declare_testing(lib: ctypes.CDLL) -> ctypes.CDLL:
         "ftrainTestingVariantName": (c_char_p, [c_int]),
         "ftrainTestingEstimateMicros": (c_double, [c_int, c_uint64, c_uint64, c_uint64, c_bool, c_int]),
         "ftrainTestingChooseSplits": (c_uint32, [c_int, c_uint64, c_uint64, c_uint64, c_int]),
+        "ftrainTestingForceSplits": (None, [c_uint32]),
         "ftrainTestingCacheCreate": (c_void_p, [c_uint64, c_uint64]),
         "ftrainTestingCacheDestroy": (None, [c_void_p]),
         "ftrainTestingCachePublish": (st, [c_void_p, POINTER(c_uint64), c_size_t, POINTER(c_uint64), c_size_t,

@@ -560,3 +560,87 @@ def test_fp32_dma_tile_skips_other_layouts_and_k_tails(capi, ops):
     assert "Fp32Mfma16Gemm_256x256_Dma" not in capi.plan_for(a, b.t().contiguous().t(), None, d, 1.0, 0.0, ops).names()
     a3 = torch.zeros(256, 48, device="cuda")
     assert "Fp32Mfma16Gemm_256x256_Dma" not in capi.plan_for(a3, b[:48], None, d, 1.0, 0.0, ops).names()
+
+
+@pytest.mark.parametrize("m,n,k,with_c,splits", [
+    (64, 4096, 4096, False, 16),   # BASELINE 5a shape at its split count
+    (4096, 64, 4096, True, 16),    # 5b, with c
+    (64, 1024, 4096, False, 64),
+    (100, 1000, 2080, True, 5),    # edge tiles in m and n, an odd split count
+    (300, 200, 1024, False, 3),
+    (64, 256, 512, True, 2),
+    (256, 512, 4128, False, 16),   # 15 used splits of 16 asked (chunk rounding)
+    (70, 2052, 3200, True, 7),
+    (1024, 4096, 512, False, 2),   # many tiles per CU: the epilogue's store-data hazard showed here
+    (4096, 1024, 512, True, 2),
+])
+def test_fp32_split_k_at_forced_split_counts(capi, oracle, m, n, k, with_c, splits):
+    """Every DMA split-k tile (partial tiles, then the reduction kernel) and the deep-k kernel
+    (reduction in the launch by the tile's last workgroup) at split counts forced through the
+    test hook rather than picked by the cost model: against fp64, d inside a 7.0-filled store,
+    bit-identical over repeats with the partials in the Plan's buffer or in a caller workspace
+    full of garbage, then again at 2 splits and back on the same buffers."""
+    t = capi.testing_lib()
+    ops = capi.GemmOps(l=t, order=("d", "beta", "alpha", "c", "b", "a"))
+    g = torch.Generator().manual_seed(m * 7 + n + k + splits)
+    a_h, b_h = torch.randn(m, k, generator=g), torch.randn(k, n, generator=g)
+    c_h = torch.randn(m, n, generator=g) if with_c else None
+    alpha, beta = 0.75, (1.5 if with_c else 0.0)
+    ref = oracle.gemm_f64(a_h, b_h, c_h, alpha, beta)
+    a_d, b_d = a_h.cuda(), b_h.cuda()
+    c_d = None if c_h is None else c_h.cuda()
+    d_s = torch.full((m + 1, n + 4), 7.0, device="cuda")
+    d = d_s[:m, :n]
+    keep = torch.ones_like(d_s, dtype=torch.bool)
+    keep[:m, :n] = False
+    tiles = ("256x256", "128x128", "64x256", "256x64", "64x128", "128x64", "64x64")
+    names = [f"Fp32Mfma16Gemm_{tl}_Dma_SplitK" for tl in tiles] + ["Fp32Mfma16Gemm_64x64_DeepK"]
+    s = torch.cuda.current_stream().cuda_stream
+    try:
+        for s_now in (splits, 2, splits):
+            t.ftrainTestingForceSplits(s_now)
+            plan = capi.plan_for(a_d, b_d, c_d, d, alpha, beta, ops)
+            for name in names:
+                assert name in plan.names(), (name, plan.names())
+                i = plan.names().index(name)
+                need = plan.workspace_bytes(i)
+                ws = torch.full((max(need, 16) // 4 + 64,), -1, dtype=torch.int32, device="cuda")
+                outs = []
+                for run in range(3):
+                    d.fill_(float("nan"))
+                    if need or run == 2:  # a caller workspace full of garbage (counters cleared first)
+                        plan.execute(i, s, ws.data_ptr(), ws.numel() * 4)
+                    else:
+                        plan.execute(i, s)
+                    torch.cuda.synchronize()
+                    outs.append(d.clone())
+                    assert torch.all(d_s[keep] == 7.0), (name, "wrote outside d")
+                rep = oracle.tolerance_check(outs[0].cpu().numpy(), ref, k)
+                assert rep["ok"], (name, s_now, rep)
+                assert rep["max_abs_err"] <= 1e-2 * rep["bound"], (name, s_now, rep)
+                assert all(torch.equal(outs[0], o) for o in outs[1:]), (name, s_now)
+            plan.close()
+    finally:
+        t.ftrainTestingForceSplits(0)
+
+
+@pytest.mark.parametrize("m,n,k", [(2048, 2048, 512), (4096, 1024, 256)])
+def test_fp32_dma_whole_k_tiles_every_output(capi, ops, oracle, m, n, k):
+    """The whole-k DMA tiles over many rounds of workgroups, every output checked, five runs:
+    a store whose data registers were overwritten right after it (a hardware hazard the
+    compiler does not cover for buffer stores) showed only under such load, as a few stray
+    dwords per launch."""
+    g = torch.Generator().manual_seed(m + n + k)
+    a_h, b_h, c_h = torch.randn(m, k, generator=g), torch.randn(k, n, generator=g), torch.randn(m, n, generator=g)
+    ref = oracle.gemm_f64(a_h, b_h, c_h, 1.0, 0.5)
+    d = torch.empty(m, n, device="cuda")
+    plan = capi.plan_for(a_h.cuda(), b_h.cuda(), c_h.cuda(), d, 1.0, 0.5, ops)
+    s = torch.cuda.current_stream().cuda_stream
+    for name in ("Fp32Mfma16Gemm_256x256_Dma", "Fp32Mfma16Gemm_128x128_Dma"):
+        i = plan.names().index(name)
+        for _ in range(5):
+            d.fill_(float("nan"))
+            plan.execute(i, s)
+            torch.cuda.synchronize()
+            rep = oracle.tolerance_check(d.cpu().numpy(), ref, k)
+            assert rep["ok"] and rep["max_abs_err"] <= 1e-2 * rep["bound"], (name, rep)
