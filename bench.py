@@ -229,23 +229,36 @@ CONFIG_STEPS = {
 }
 
 
-def time_steps(plan, index: int, stream, steps: int, warmup: int) -> dict:
-    """Per-step HIP events on the launch stream: mean and median step time (ms)."""
+def time_steps(plan, index: int, stream, steps: int, warmup: int, block: int = 10) -> dict:
+    """HIP events on the launch stream around blocks of `block` back-to-back calls: the mean over
+    all steps and the median of the block means (ms per call).  An event between every two calls
+    adds a marker to the queue that costs about 2-3 us next to a 25 us kernel; the per-call event
+    median is reported beside it."""
     import torch
 
     h = stream.cuda_stream
+    blocks = max(1, steps // block)
     with torch.cuda.stream(stream):
         for _ in range(warmup):
             plan.execute(index, h)
         torch.cuda.synchronize()
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(blocks + 1)]
         ev[0].record(stream)
-        for i in range(steps):
-            plan.execute(index, h)
+        for i in range(blocks):
+            for _ in range(block):
+                plan.execute(index, h)
             ev[i + 1].record(stream)
         torch.cuda.synchronize()
-    per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
-    return {"mean_ms": ev[0].elapsed_time(ev[-1]) / steps, "median_ms": per[steps // 2]}
+        per_block = sorted(ev[i].elapsed_time(ev[i + 1]) / block for i in range(blocks))
+        one = [torch.cuda.Event(enable_timing=True) for _ in range(block + 1)]
+        one[0].record(stream)
+        for i in range(block):
+            plan.execute(index, h)
+            one[i + 1].record(stream)
+        torch.cuda.synchronize()
+    per_call = sorted(one[i].elapsed_time(one[i + 1]) for i in range(block))
+    return {"mean_ms": ev[0].elapsed_time(ev[-1]) / (blocks * block), "median_ms": per_block[blocks // 2],
+            "event_per_call_median_ms": per_call[block // 2]}
 
 
 def parity_rows(oracle, a_h, b_h, c_h, cfg, d, rows_wanted: int = 64) -> dict:
@@ -285,6 +298,7 @@ def run_config(name: str, steps: int) -> dict:
     hbm_bound = flops / alg_bytes < FP32_MATRIX_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
     out = {"workload": name, "m": m, "n": n, "k": k, "c": c is not None, "primitive": plan.name(0),
            "steps": steps, "median_ms": round(ms, 5), "mean_ms": round(t["mean_ms"], 5),
+           "event_per_call_median_ms": round(t["event_per_call_median_ms"], 5),
            "tflops": round(tflops, 3), "gbs": round(gbs, 1),
            "roofline": {"bound": "hbm" if hbm_bound else "mfma",
                         "frac": round(gbs / HBM_PEAK_GBS if hbm_bound else tflops / FP32_MATRIX_PEAK_TFLOPS, 4),
