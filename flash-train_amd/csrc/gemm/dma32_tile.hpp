@@ -102,14 +102,15 @@ __device__ __forceinline__ int a_swz(int row) {
 }
 
 // Output tile `bid`, k split z of p; the whole workgroup calls it.
-template <int BM, int BN, int WM, int WN, bool SPLIT>
+// TB: b column-major (element (k, j) at b[j * ldb + k]); its stage is staged per column (below).
+template <int BM, int BN, int WM, int WN, bool SPLIT, bool TB = false>
 __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid, int z) {
     static_assert(WM * WN == 4, "4 waves");
     constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 16, TN = WTN / 16, NC = TN / 4;
     static_assert(TN % 4 == 0 && TM >= 1, "column runs of four blocks");
     constexpr int DA = BM / 32;        // A DMAs per wave per stage (8-row blocks)
-    constexpr int RB = 256 / BN;       // k rows per B DMA
-    constexpr int DB = 8 / RB;         // B DMAs per wave per stage
+    constexpr int RB = 256 / BN;       // k rows per B DMA (row-major b)
+    constexpr int DB = BN / 32;        // B DMAs per wave per stage (8 k rows or 8 columns of b each)
     constexpr int ND = DA + DB;        // DMAs per wave per stage
     constexpr int CPR = BN / 4;        // 16-byte chunks per B k row
     constexpr bool BSWZ = CPR >= 32;   // B k rows have a second half to swap
@@ -155,10 +156,27 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
         const unsigned row = min(ar + 32u * j, alast);
         dma_1k(row * lda4 + achunk, abase + (size_t)st * kStageK * 4, lds + (wave + 4 * j) * 1024);
     };
+    // Column-major b: block q = wave + 4 j holds columns 8q .. 8q + 7, each a whole 128-byte line of
+    // 32 k.  Slot L of the block holds column 8q + cb, chunk ch with
+    //   L = 16 (cb & 3) + 8 (cb >> 2) + (ch ^ (q & 7)),
+    // so the 16 columns 4j + c (j = 0..15) one 16-lane read takes at one chunk sit in 16
+    // distinct 16-byte slots modulo 256 bytes (no bank conflict).  Columns past n are clamped
+    // onto the last one; 255 columns of ldb < 2^22 keep the lane offset below 2^32.
+    const char* btbase = reinterpret_cast<const char*>(p.b + (size_t)n0 * ldb + kbeg);
+    const unsigned blast = static_cast<unsigned>(min(N - 1 - n0, BN - 1));
+    auto dma_bt = [&](int st, int j, unsigned lds) {
+        const int q = wave + 4 * j, cb = 4 * ((lane >> 3) & 1) + (lane >> 4), ch = (lane & 7) ^ (q & 7);
+        const unsigned col = min(static_cast<unsigned>(8 * q + cb), blast);
+        dma_1k(col * static_cast<unsigned>(4 * ldb) + 16 * ch, btbase + (size_t)st * kStageK * 4, lds + q * 1024);
+    };
     auto dma_b = [&](int st, int j, unsigned lds) {
-        const int q = wave + 4 * j, kr0 = RB * q;
-        dma_1k(BSWZ && ((kr0 >> 3) & 1) ? boff1 : boff0, bbase + ((size_t)st * kStageK + kr0) * ldb * 4,
-               lds + q * 1024);
+        if constexpr (TB) {
+            dma_bt(st, j, lds);
+        } else {
+            const int q = wave + 4 * j, kr0 = RB * q;
+            dma_1k(BSWZ && ((kr0 >> 3) & 1) ? boff1 : boff0, bbase + ((size_t)st * kStageK + kr0) * ldb * 4,
+                   lds + q * 1024);
+        }
     };
     // DMA d (0 .. ND - 1) of a stage: A and B alternate while both have some left.
     auto dma_one = [&](int st, int d, unsigned la, unsigned lb) {
@@ -185,6 +203,13 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
         return *reinterpret_cast<const floatx4*>(T + row * kStageK + 4 * (c ^ a_swz(row)));
     };
     // B operands of k-step s for column run cc (blocks 4 cc .. 4 cc + 3): B[8 g + s][4 cols].
+    // Column-major b: block bj's operands of half hf (k-steps 4 hf .. 4 hf + 3) for column
+    // wcol + (bj / 4) * 64 + 4 j16 + bj % 4 (the column interleave above).
+    auto rd_bt = [&](const float* T, int hf, int bj) {
+        const int col = wcol + (bj >> 2) * 64 + 4 * j16 + (bj & 3), q = col >> 3, cb = col & 7;
+        const int slot = 64 * q + 16 * (cb & 3) + 8 * (cb >> 2) + ((2 * g + hf) ^ (q & 7));
+        return *reinterpret_cast<const floatx4*>(T + 4 * slot);
+    };
     auto rd_b = [&](const float* T, int s, int cc) {
         const int kr = 8 * g + s, c = (wcol >> 2) + 16 * cc + j16;
         return *reinterpret_cast<const floatx4*>(T + kr * BN + 4 * (BSWZ ? c ^ (16 * ((kr >> 3) & 1)) : c));
@@ -196,12 +221,15 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // Operands of one half stage: fa[bi] (4 k-steps), fb[s][cc].
+    // Operands of one half stage: fa[bi] (4 k-steps), fb[s][cc] (4 columns); column-major b:
+    // fb[bj & 3][bj >> 2] holds block bj's 4 k-steps.
     floatx4 fa0[TM], fb0[4][NC], fa1[TM], fb1[4][NC];
     // Read r (0 .. NR - 1) of half hf: TM A reads, then the B reads (k-step major).
     auto read_one = [&](floatx4 (&ga)[TM], floatx4 (&gb)[4][NC], const float* As, const float* Bs, int hf, int r) {
         if (r < TM)
             ga[r] = rd_a(As, r, hf);
+        else if constexpr (TB)
+            gb[(r - TM) & 3][(r - TM) >> 2] = rd_bt(Bs, hf, r - TM);
         else
             gb[(r - TM) / NC][(r - TM) % NC] = rd_b(Bs, 4 * hf + (r - TM) / NC, (r - TM) % NC);
     };
@@ -219,7 +247,9 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
             for (int bi = 0; bi < TM; ++bi) {
 #pragma unroll
                 for (int bj = 0; bj < TN; ++bj)
-                    acc[bi][bj] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[bi][s], fb[s][bj >> 2][bj & 3], acc[bi][bj],
+                    acc[bi][bj] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[bi][s], TB ? fb[bj & 3][bj >> 2][s]
+                                                                                   : fb[s][bj >> 2][bj & 3],
+                                                                      acc[bi][bj],
                                                                       0, 0, 0);
                 const int u = TM * s + bi;
                 bool read = false;
@@ -359,7 +389,7 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
         run(std::false_type{});
 }
 
-template <int BM, int BN, int WM, int WN, int MINB, bool SPLIT>
+template <int BM, int BN, int WM, int WN, int MINB, bool SPLIT, bool TB = false>
 __global__ __launch_bounds__(256, MINB) void fp32_gemm_dma(GemmParams p) {
     int bid = blockIdx.x, z = blockIdx.z;
     if constexpr (SPLIT) {
@@ -374,9 +404,10 @@ __global__ __launch_bounds__(256, MINB) void fp32_gemm_dma(GemmParams p) {
             bid           = t < (per << 3) ? ((t % per) << 3) + t / per : t;
         }
     }
-    fp32_gemm_dma_tile<BM, BN, WM, WN, SPLIT>(p, bid, z);
+    fp32_gemm_dma_tile<BM, BN, WM, WN, SPLIT, TB>(p, bid, z);
 }
 
+#ifndef FT_DMA32_NO_GROUPED
 // Grouped GEMM over a device table of per-group parameters (256x256 whole-k
 // tiles): the workgroup's group is the last one whose first tile id is at
 // most its own.  Group starts are multiples of 8, so the group-local id keeps
@@ -397,5 +428,7 @@ __global__ __launch_bounds__(256, 1) void grouped_fp32_gemm_dma(GroupedGemmArgs 
     if (local >= p.tiles_m * p.tiles_n) return;
     fp32_gemm_dma_tile<256, 256, 2, 2, false>(p, local, 0);
 }
+
+#endif
 
 }  // namespace ftrain::gemm::d32

@@ -277,6 +277,7 @@ const void* halfKernelFp16TT(int tile);
 // The DMA-staged 256x256 tiles per input type and operand orientation.
 const void* dma32Kernel(Variant v);
 const void* groupedDma32Kernel();
+const void* dma32KernelTB(Variant v);  // column-major b
 const void* dmaKernelBf16(bool ta, bool tb);
 const void* dmaKernelFp16(bool ta, bool tb);
 const void* groupedDmaKernelBf16(bool ta, bool tb);

@@ -560,6 +560,11 @@ def test_fp32_dma_tile_skips_other_layouts_and_k_tails(capi, ops):
     assert "Fp32Mfma16Gemm_256x256_Dma" not in capi.plan_for(a, b.t().contiguous().t(), None, d, 1.0, 0.0, ops).names()
     a3 = torch.zeros(256, 48, device="cuda")
     assert "Fp32Mfma16Gemm_256x256_Dma" not in capi.plan_for(a3, b[:48], None, d, 1.0, 0.0, ops).names()
+    # the 128x128 tile and the split tiles take a column-major b; no DMA tile takes a column-major a
+    names = capi.plan_for(a, b.t().contiguous().t(), None, d, 1.0, 0.0, ops).names()
+    assert "Fp32Mfma16Gemm_128x128_Dma" in names, names
+    names = capi.plan_for(a.t().contiguous().t(), b, None, d, 1.0, 0.0, ops).names()
+    assert not any("_Dma" in x for x in names), names
 
 
 @pytest.mark.parametrize("m,n,k,with_c,splits", [
@@ -574,7 +579,8 @@ def test_fp32_dma_tile_skips_other_layouts_and_k_tails(capi, ops):
     (1024, 4096, 512, False, 2),   # many tiles per CU: the epilogue's store-data hazard showed here
     (4096, 1024, 512, True, 2),
 ])
-def test_fp32_split_k_at_forced_split_counts(capi, oracle, m, n, k, with_c, splits):
+@pytest.mark.parametrize("tb", [False, True], ids=["b_rows", "b_cols"])
+def test_fp32_split_k_at_forced_split_counts(capi, oracle, m, n, k, with_c, splits, tb):
     """Every DMA split-k tile (partial tiles, then the reduction kernel) and the deep-k kernel
     (reduction in the launch by the tile's last workgroup) at split counts forced through the
     test hook rather than picked by the cost model: against fp64, d inside a 7.0-filled store,
@@ -587,14 +593,15 @@ def test_fp32_split_k_at_forced_split_counts(capi, oracle, m, n, k, with_c, spli
     c_h = torch.randn(m, n, generator=g) if with_c else None
     alpha, beta = 0.75, (1.5 if with_c else 0.0)
     ref = oracle.gemm_f64(a_h, b_h, c_h, alpha, beta)
-    a_d, b_d = a_h.cuda(), b_h.cuda()
+    a_d = a_h.cuda()
+    b_d = b_h.t().contiguous().cuda().t() if tb else b_h.cuda()
     c_d = None if c_h is None else c_h.cuda()
     d_s = torch.full((m + 1, n + 4), 7.0, device="cuda")
     d = d_s[:m, :n]
     keep = torch.ones_like(d_s, dtype=torch.bool)
     keep[:m, :n] = False
-    tiles = ("256x256", "128x128", "64x256", "256x64", "64x128", "128x64", "64x64")
-    names = [f"Fp32Mfma16Gemm_{tl}_Dma_SplitK" for tl in tiles] + ["Fp32Mfma16Gemm_64x64_DeepK"]
+    tiles = ("128x128", "64x256", "256x64", "64x128", "128x64", "64x64") + (() if tb else ("256x256",))
+    names = [f"Fp32Mfma16Gemm_{tl}_Dma_SplitK" for tl in tiles] + ([] if tb else ["Fp32Mfma16Gemm_64x64_DeepK"])
     s = torch.cuda.current_stream().cuda_stream
     try:
         for s_now in (splits, 2, splits):
@@ -624,19 +631,22 @@ def test_fp32_split_k_at_forced_split_counts(capi, oracle, m, n, k, with_c, spli
         t.ftrainTestingForceSplits(0)
 
 
-@pytest.mark.parametrize("m,n,k", [(2048, 2048, 512), (4096, 1024, 256)])
-def test_fp32_dma_whole_k_tiles_every_output(capi, ops, oracle, m, n, k):
+@pytest.mark.parametrize("m,n,k,tb", [(2048, 2048, 512, False), (4096, 1024, 256, False), (2048, 2048, 512, True),
+                                       (1000, 1500, 544, True)])
+def test_fp32_dma_whole_k_tiles_every_output(capi, ops, oracle, m, n, k, tb):
     """The whole-k DMA tiles over many rounds of workgroups, every output checked, five runs:
     a store whose data registers were overwritten right after it (a hardware hazard the
     compiler does not cover for buffer stores) showed only under such load, as a few stray
-    dwords per launch."""
+    dwords per launch.  tb: b column-major (storage n x k), staged per column (the 128x128 tile;
+    1000 x 1500 has edge tiles in m and n)."""
     g = torch.Generator().manual_seed(m + n + k)
     a_h, b_h, c_h = torch.randn(m, k, generator=g), torch.randn(k, n, generator=g), torch.randn(m, n, generator=g)
     ref = oracle.gemm_f64(a_h, b_h, c_h, 1.0, 0.5)
     d = torch.empty(m, n, device="cuda")
-    plan = capi.plan_for(a_h.cuda(), b_h.cuda(), c_h.cuda(), d, 1.0, 0.5, ops)
+    b_d = b_h.t().contiguous().cuda().t() if tb else b_h.cuda()
+    plan = capi.plan_for(a_h.cuda(), b_d, c_h.cuda(), d, 1.0, 0.5, ops)
     s = torch.cuda.current_stream().cuda_stream
-    for name in ("Fp32Mfma16Gemm_256x256_Dma", "Fp32Mfma16Gemm_128x128_Dma"):
+    for name in ("Fp32Mfma16Gemm_128x128_Dma",) if tb else ("Fp32Mfma16Gemm_256x256_Dma", "Fp32Mfma16Gemm_128x128_Dma"):
         i = plan.names().index(name)
         for _ in range(5):
             d.fill_(float("nan"))
