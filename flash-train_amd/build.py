@@ -72,6 +72,7 @@ LIB_SOURCES = [
     "csrc/gemm/kernels_half_fp16_tt.hip",
     "csrc/gemm/kernels_dma32.hip",
     "csrc/gemm/kernels_dma32_tb.hip",
+    "csrc/gemm/kernels_dma32_ta.hip",
     "csrc/gemm/kernels_half_dma_bf16.hip",
     "csrc/gemm/kernels_half_dma_fp16.hip",
     "csrc/gemm/kernels_gemv_half.hip",

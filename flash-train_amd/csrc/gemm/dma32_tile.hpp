@@ -103,11 +103,17 @@ __device__ __forceinline__ int a_swz(int row) {
 
 // Output tile `bid`, k split z of p; the whole workgroup calls it.
 // TB: b column-major (element (k, j) at b[j * ldb + k]); its stage is staged per column (below).
-template <int BM, int BN, int WM, int WN, bool SPLIT, bool TB = false>
+// TA: a column-major (element (i, k) at a[k * lda + i]); its stage is [32 k][BM] like a row-major
+// b's, and its rows interleave like b's columns (below).
+template <int BM, int BN, int WM, int WN, bool SPLIT, bool TB = false, bool TA = false>
 __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid, int z) {
     static_assert(WM * WN == 4, "4 waves");
     constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 16, TN = WTN / 16, NC = TN / 4;
     static_assert(TN % 4 == 0 && TM >= 1, "column runs of four blocks");
+    static_assert(!TA || TM % 4 == 0, "row runs of four blocks");
+    constexpr int RA = 256 / BM;       // k rows per A DMA (column-major a)
+    constexpr int CPA = BM / 4;        // 16-byte chunks per A k row (column-major a)
+    constexpr bool ASWZ = CPA >= 32;
     constexpr int DA = BM / 32;        // A DMAs per wave per stage (8-row blocks)
     constexpr int RB = 256 / BN;       // k rows per B DMA (row-major b)
     constexpr int DB = BN / 32;        // B DMAs per wave per stage (8 k rows or 8 columns of b each)
@@ -152,9 +158,24 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
         return static_cast<unsigned>((kr * ldb + (min(n0 + 4 * chunk, N - 4) - n0)) * 4);
     };
     const unsigned boff0 = boff(0), boff1 = BSWZ ? boff(1) : boff0;
+    // Column-major a: block q = wave + 4 j holds k rows RA q .. RA q + RA - 1 of the stage (lane: k
+    // row RA q + lane / CPA, slot lane % CPA holds chunk (lane % CPA) ^ swizzle, four rows of a);
+    // a chunk past m is clamped onto the last whole one (m % 4 == 0).
+    const char* atbase = reinterpret_cast<const char*>(p.a + (size_t)kbeg * lda + m0);
+    auto aoff = [&](int x) {
+        const int kr = lane / CPA, chunk = (lane % CPA) ^ (x ? 16 : 0);
+        return static_cast<unsigned>((kr * lda + (min(m0 + 4 * chunk, M - 4) - m0)) * 4);
+    };
+    const unsigned aoff0 = TA ? aoff(0) : 0u, aoff1 = TA && ASWZ ? aoff(1) : aoff0;
     auto dma_a = [&](int st, int j, unsigned lds) {
-        const unsigned row = min(ar + 32u * j, alast);
-        dma_1k(row * lda4 + achunk, abase + (size_t)st * kStageK * 4, lds + (wave + 4 * j) * 1024);
+        if constexpr (TA) {
+            const int q = wave + 4 * j, kr0 = RA * q;
+            dma_1k(ASWZ && ((kr0 >> 3) & 1) ? aoff1 : aoff0, atbase + ((size_t)st * kStageK + kr0) * lda * 4,
+                   lds + q * 1024);
+        } else {
+            const unsigned row = min(ar + 32u * j, alast);
+            dma_1k(row * lda4 + achunk, abase + (size_t)st * kStageK * 4, lds + (wave + 4 * j) * 1024);
+        }
     };
     // Column-major b: block q = wave + 4 j holds columns 8q .. 8q + 7, each a whole 128-byte line of
     // 32 k.  Slot L of the block holds column 8q + cb, chunk ch with
@@ -198,6 +219,12 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
     const unsigned lb1 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) float*)Bs1;
 
     // A operands of half hf (k-steps 4 hf .. 4 hf + 3) for block row bi: A[row][8 g + 4 hf .. + 3].
+    // Column-major a: operands of k-step s for row run rr (blocks 4 rr .. 4 rr + 3): A[4 rows][8 g + s]
+    // (block bi, MFMA row j is wave-tile row (bi / 4) * 64 + 4 j + bi % 4).
+    auto rd_at = [&](const float* T, int s, int rr) {
+        const int kr = 8 * g + s, c = (wrow >> 2) + 16 * rr + j16;
+        return *reinterpret_cast<const floatx4*>(T + kr * BM + 4 * (ASWZ ? c ^ (16 * ((kr >> 3) & 1)) : c));
+    };
     auto rd_a = [&](const float* T, int bi, int hf) {
         const int row = wrow + 16 * bi + j16, c = 2 * g + hf;
         return *reinterpret_cast<const floatx4*>(T + row * kStageK + 4 * (c ^ a_swz(row)));
@@ -227,7 +254,7 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
     // Read r (0 .. NR - 1) of half hf: TM A reads, then the B reads (k-step major).
     auto read_one = [&](floatx4 (&ga)[TM], floatx4 (&gb)[4][NC], const float* As, const float* Bs, int hf, int r) {
         if (r < TM)
-            ga[r] = rd_a(As, r, hf);
+            ga[r] = TA ? rd_at(As, 4 * hf + r / (TM / 4), r % (TM / 4)) : rd_a(As, r, hf);
         else if constexpr (TB)
             gb[(r - TM) & 3][(r - TM) >> 2] = rd_bt(Bs, hf, r - TM);
         else
@@ -247,7 +274,9 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
             for (int bi = 0; bi < TM; ++bi) {
 #pragma unroll
                 for (int bj = 0; bj < TN; ++bj)
-                    acc[bi][bj] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[bi][s], TB ? fb[bj & 3][bj >> 2][s]
+                    acc[bi][bj] = __builtin_amdgcn_mfma_f32_16x16x4f32(TA ? fa[s * (TM / 4) + (bi >> 2)][bi & 3]
+                                                                                   : fa[bi][s],
+                                                                      TB ? fb[bj & 3][bj >> 2][s]
                                                                                    : fb[s][bj >> 2][bj & 3],
                                                                       acc[bi][bj],
                                                                       0, 0, 0);
@@ -334,7 +363,11 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
     const __amdgpu_buffer_rsrc_t dres = __builtin_amdgcn_make_buffer_rsrc(dcorner, 0, span(ldd64), kBufferConfig);
     const unsigned ldd = static_cast<unsigned>(ldd64), ldc = static_cast<unsigned>(p.ldc);
     constexpr unsigned kOut = 0x80000000u;
-    const unsigned lane_d = (4 * g * ldd + 4 * j16) * 4, lane_c = (4 * g * ldc + 4 * j16) * 4;
+    // Lane group g's first row: 4 g, or with column-major a (rows interleaved) 16 g.
+    constexpr int GROW = TA ? 16 : 4;
+    const unsigned lane_d = (GROW * g * ldd + 4 * j16) * 4, lane_c = (GROW * g * ldc + 4 * j16) * 4;
+    // Row of lane group 0 for block row bi, register r.
+    auto row_of = [&](int bi, int r) { return TA ? wrow + (bi >> 2) * 64 + 4 * r + (bi & 3) : wrow + 16 * bi + r; };
     auto run = [&](auto c_tag) {
         constexpr bool HAS_C = decltype(c_tag)::value;
         __amdgpu_buffer_rsrc_t cres = dres;
@@ -345,11 +378,11 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
         auto load_c = [&](int bi, floatx4 (&dst)[4][NC]) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int row0 = wrow + 16 * bi + r;  // row of lane group 0
+                const int row0 = row_of(bi, r);
 #pragma unroll
                 for (int q = 0; q < NC; ++q) {
                     const int c0  = wcol + 64 * q;
-                    const bool ok = 4 * g < rows_left - row0 && c0 + 4 * j16 < cols_left;
+                    const bool ok = GROW * g < rows_left - row0 && c0 + 4 * j16 < cols_left;
                     dst[r][q]     = __builtin_bit_cast(
                         floatx4, __builtin_amdgcn_raw_buffer_load_b128(cres, ok ? lane_c : kOut,
                                                                        static_cast<int>((row0 * ldc + c0) * 4), 0));
@@ -363,11 +396,11 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
                 if (bi + 1 < TM) load_c(bi + 1, cv[(bi + 1) & 1]);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int row0 = wrow + 16 * bi + r;
+                const int row0 = row_of(bi, r);
 #pragma unroll
                 for (int q = 0; q < NC; ++q) {
                     const int c0  = wcol + 64 * q;
-                    const bool ok = 4 * g < rows_left - row0 && c0 + 4 * j16 < cols_left;
+                    const bool ok = GROW * g < rows_left - row0 && c0 + 4 * j16 < cols_left;
                     floatx4 out;
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
@@ -389,7 +422,7 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
         run(std::false_type{});
 }
 
-template <int BM, int BN, int WM, int WN, int MINB, bool SPLIT, bool TB = false>
+template <int BM, int BN, int WM, int WN, int MINB, bool SPLIT, bool TB = false, bool TA = false>
 __global__ __launch_bounds__(256, MINB) void fp32_gemm_dma(GemmParams p) {
     int bid = blockIdx.x, z = blockIdx.z;
     if constexpr (SPLIT) {
@@ -404,7 +437,7 @@ __global__ __launch_bounds__(256, MINB) void fp32_gemm_dma(GemmParams p) {
             bid           = t < (per << 3) ? ((t % per) << 3) + t / per : t;
         }
     }
-    fp32_gemm_dma_tile<BM, BN, WM, WN, SPLIT, TB>(p, bid, z);
+    fp32_gemm_dma_tile<BM, BN, WM, WN, SPLIT, TB, TA>(p, bid, z);
 }
 
 #ifndef FT_DMA32_NO_GROUPED

@@ -278,6 +278,7 @@ const void* halfKernelFp16TT(int tile);
 const void* dma32Kernel(Variant v);
 const void* groupedDma32Kernel();
 const void* dma32KernelTB(Variant v);  // column-major b
+const void* dma32KernelTA(Variant v, bool tb);  // column-major a
 const void* dmaKernelBf16(bool ta, bool tb);
 const void* dmaKernelFp16(bool ta, bool tb);
 const void* groupedDmaKernelBf16(bool ta, bool tb);

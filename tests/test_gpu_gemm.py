@@ -560,11 +560,14 @@ def test_fp32_dma_tile_skips_other_layouts_and_k_tails(capi, ops):
     assert "Fp32Mfma16Gemm_256x256_Dma" not in capi.plan_for(a, b.t().contiguous().t(), None, d, 1.0, 0.0, ops).names()
     a3 = torch.zeros(256, 48, device="cuda")
     assert "Fp32Mfma16Gemm_256x256_Dma" not in capi.plan_for(a3, b[:48], None, d, 1.0, 0.0, ops).names()
-    # the 128x128 tile and the split tiles take a column-major b; no DMA tile takes a column-major a
-    names = capi.plan_for(a, b.t().contiguous().t(), None, d, 1.0, 0.0, ops).names()
-    assert "Fp32Mfma16Gemm_128x128_Dma" in names, names
-    names = capi.plan_for(a.t().contiguous().t(), b, None, d, 1.0, 0.0, ops).names()
-    assert not any("_Dma" in x for x in names), names
+    # the 128x128 tile takes a column-major b, a column-major a, or both; the 64x128 split tile
+    # (wave rows of 32) takes no column-major a
+    a, b = torch.zeros(256, 1024, device="cuda"), torch.zeros(1024, 256, device="cuda")  # deep enough to split
+    for at, bt in ((False, False), (False, True), (True, False), (True, True)):
+        names = capi.plan_for(a.t().contiguous().t() if at else a, b.t().contiguous().t() if bt else b, None, d,
+                              1.0, 0.0, ops).names()
+        assert "Fp32Mfma16Gemm_128x128_Dma" in names, (at, bt, names)
+        assert ("Fp32Mfma16Gemm_64x128_Dma_SplitK" in names) == (not at), (at, bt, names)
 
 
 @pytest.mark.parametrize("m,n,k,with_c,splits", [
@@ -579,13 +582,17 @@ def test_fp32_dma_tile_skips_other_layouts_and_k_tails(capi, ops):
     (1024, 4096, 512, False, 2),   # many tiles per CU: the epilogue's store-data hazard showed here
     (4096, 1024, 512, True, 2),
 ])
-@pytest.mark.parametrize("tb", [False, True], ids=["b_rows", "b_cols"])
-def test_fp32_split_k_at_forced_split_counts(capi, oracle, m, n, k, with_c, splits, tb):
-    """Every DMA split-k tile (partial tiles, then the reduction kernel) and the deep-k kernel
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)],
+                         ids=["nn", "nt", "tn", "tt"])
+def test_fp32_split_k_at_forced_split_counts(capi, oracle, m, n, k, with_c, splits, ta, tb):
+    """Every DMA split-k tile (partial tiles, then the reduction kernel) in every operand
+    orientation it has, and the deep-k kernel
     (reduction in the launch by the tile's last workgroup) at split counts forced through the
     test hook rather than picked by the cost model: against fp64, d inside a 7.0-filled store,
     bit-identical over repeats with the partials in the Plan's buffer or in a caller workspace
     full of garbage, then again at 2 splits and back on the same buffers."""
+    if ta and m % 4:
+        pytest.skip("a column-major a needs m % 4 == 0 for the 128-bit kernels")
     t = capi.testing_lib()
     ops = capi.GemmOps(l=t, order=("d", "beta", "alpha", "c", "b", "a"))
     g = torch.Generator().manual_seed(m * 7 + n + k + splits)
@@ -593,15 +600,18 @@ def test_fp32_split_k_at_forced_split_counts(capi, oracle, m, n, k, with_c, spli
     c_h = torch.randn(m, n, generator=g) if with_c else None
     alpha, beta = 0.75, (1.5 if with_c else 0.0)
     ref = oracle.gemm_f64(a_h, b_h, c_h, alpha, beta)
-    a_d = a_h.cuda()
+    a_d = a_h.t().contiguous().cuda().t() if ta else a_h.cuda()
     b_d = b_h.t().contiguous().cuda().t() if tb else b_h.cuda()
     c_d = None if c_h is None else c_h.cuda()
     d_s = torch.full((m + 1, n + 4), 7.0, device="cuda")
     d = d_s[:m, :n]
     keep = torch.ones_like(d_s, dtype=torch.bool)
     keep[:m, :n] = False
-    tiles = ("128x128", "64x256", "256x64", "64x128", "128x64", "64x64") + (() if tb else ("256x256",))
-    names = [f"Fp32Mfma16Gemm_{tl}_Dma_SplitK" for tl in tiles] + ([] if tb else ["Fp32Mfma16Gemm_64x64_DeepK"])
+    # Column-major a: the tiles with wave rows in runs of 64; column-major b: all but 256x256; the
+    # deep-k kernel takes row-major a and b only.
+    tiles = ("128x128", "64x256", "256x64") + (() if ta else ("64x128", "128x64", "64x64"))
+    tiles += () if ta or tb else ("256x256",)
+    names = [f"Fp32Mfma16Gemm_{tl}_Dma_SplitK" for tl in tiles] + ([] if ta or tb else ["Fp32Mfma16Gemm_64x64_DeepK"])
     s = torch.cuda.current_stream().cuda_stream
     try:
         for s_now in (splits, 2, splits):
@@ -631,22 +641,26 @@ def test_fp32_split_k_at_forced_split_counts(capi, oracle, m, n, k, with_c, spli
         t.ftrainTestingForceSplits(0)
 
 
-@pytest.mark.parametrize("m,n,k,tb", [(2048, 2048, 512, False), (4096, 1024, 256, False), (2048, 2048, 512, True),
-                                       (1000, 1500, 544, True)])
-def test_fp32_dma_whole_k_tiles_every_output(capi, ops, oracle, m, n, k, tb):
+@pytest.mark.parametrize("m,n,k,ta,tb", [(2048, 2048, 512, False, False), (4096, 1024, 256, False, False),
+                                          (2048, 2048, 512, False, True), (1000, 1500, 544, False, True),
+                                          (2048, 2048, 512, True, False), (1000, 1500, 544, True, False),
+                                          (1500, 1000, 544, True, True)])
+def test_fp32_dma_whole_k_tiles_every_output(capi, ops, oracle, m, n, k, ta, tb):
     """The whole-k DMA tiles over many rounds of workgroups, every output checked, five runs:
     a store whose data registers were overwritten right after it (a hardware hazard the
     compiler does not cover for buffer stores) showed only under such load, as a few stray
-    dwords per launch.  tb: b column-major (storage n x k), staged per column (the 128x128 tile;
-    1000 x 1500 has edge tiles in m and n)."""
+    dwords per launch.  ta / tb: a / b column-major (storage k x m / n x k), the 128x128 tile
+    (1000 x 1500 has edge tiles in m and n)."""
     g = torch.Generator().manual_seed(m + n + k)
     a_h, b_h, c_h = torch.randn(m, k, generator=g), torch.randn(k, n, generator=g), torch.randn(m, n, generator=g)
     ref = oracle.gemm_f64(a_h, b_h, c_h, 1.0, 0.5)
     d = torch.empty(m, n, device="cuda")
+    a_d = a_h.t().contiguous().cuda().t() if ta else a_h.cuda()
     b_d = b_h.t().contiguous().cuda().t() if tb else b_h.cuda()
-    plan = capi.plan_for(a_h.cuda(), b_d, c_h.cuda(), d, 1.0, 0.5, ops)
+    plan = capi.plan_for(a_d, b_d, c_h.cuda(), d, 1.0, 0.5, ops)
     s = torch.cuda.current_stream().cuda_stream
-    for name in ("Fp32Mfma16Gemm_128x128_Dma",) if tb else ("Fp32Mfma16Gemm_256x256_Dma", "Fp32Mfma16Gemm_128x128_Dma"):
+    for name in ("Fp32Mfma16Gemm_128x128_Dma",) if ta or tb else ("Fp32Mfma16Gemm_256x256_Dma",
+                                                                    "Fp32Mfma16Gemm_128x128_Dma"):
         i = plan.names().index(name)
         for _ in range(5):
             d.fill_(float("nan"))
