@@ -179,14 +179,16 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
     };
     // Column-major b: block q = wave + 4 j holds columns 8q .. 8q + 7, each a whole 128-byte line of
     // 32 k.  Slot L of the block holds column 8q + cb, chunk ch with
-    //   L = 16 (cb & 3) + 8 (cb >> 2) + (ch ^ (q & 7)),
-    // so the 16 columns 4j + c (j = 0..15) one 16-lane read takes at one chunk sit in 16
-    // distinct 16-byte slots modulo 256 bytes (no bank conflict).  Columns past n are clamped
-    // onto the last one; 255 columns of ldb < 2^22 keep the lane offset below 2^32.
+    //   L = 32 b1(cb) + 16 b1(ch) + 8 b2(cb) + ((q & 7) ^ (4 b2(ch) + 2 b0(ch) + b0(cb)))
+    // (bn(x) = bit n of x).  A half-wave read takes columns 4j + c (j = 0..15, c fixed) at chunks
+    // 2g + hf of two adjacent g: those 32 sit in 32 distinct 16-byte slots modulo 512 bytes, the
+    // width of the LDS banks (no bank conflict).  Columns past n are clamped onto the last one;
+    // 255 columns of ldb < 2^22 keep the lane offset below 2^32.
     const char* btbase = reinterpret_cast<const char*>(p.b + (size_t)n0 * ldb + kbeg);
     const unsigned blast = static_cast<unsigned>(min(N - 1 - n0, BN - 1));
     auto dma_bt = [&](int st, int j, unsigned lds) {
-        const int q = wave + 4 * j, cb = 4 * ((lane >> 3) & 1) + (lane >> 4), ch = (lane & 7) ^ (q & 7);
+        const int q = wave + 4 * j, t = (lane & 7) ^ (q & 7);
+        const int cb = 4 * ((lane >> 3) & 1) + 2 * (lane >> 5) + (t & 1), ch = 4 * (t >> 2) + 2 * ((lane >> 4) & 1) + ((t >> 1) & 1);
         const unsigned col = min(static_cast<unsigned>(8 * q + cb), blast);
         dma_1k(col * static_cast<unsigned>(4 * ldb) + 16 * ch, btbase + (size_t)st * kStageK * 4, lds + q * 1024);
     };
@@ -234,7 +236,9 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
     // wcol + (bj / 4) * 64 + 4 j16 + bj % 4 (the column interleave above).
     auto rd_bt = [&](const float* T, int hf, int bj) {
         const int col = wcol + (bj >> 2) * 64 + 4 * j16 + (bj & 3), q = col >> 3, cb = col & 7;
-        const int slot = 64 * q + 16 * (cb & 3) + 8 * (cb >> 2) + ((2 * g + hf) ^ (q & 7));
+        const int ch = 2 * g + hf;
+        const int slot = 64 * q + 32 * ((cb >> 1) & 1) + 16 * ((ch >> 1) & 1) + 8 * (cb >> 2) +
+                         ((q & 7) ^ (4 * (ch >> 2) + 2 * (ch & 1) + (cb & 1)));
         return *reinterpret_cast<const floatx4*>(T + 4 * slot);
     };
     auto rd_b = [&](const float* T, int s, int cc) {
