@@ -444,13 +444,12 @@ __global__ __launch_bounds__(256, MINB) void fp32_gemm_dma(GemmParams p) {
     fp32_gemm_dma_tile<BM, BN, WM, WN, SPLIT, TB, TA>(p, bid, z);
 }
 
-#ifndef FT_DMA32_NO_GROUPED
-// Grouped GEMM over a device table of per-group parameters (256x256 whole-k
-// tiles): the workgroup's group is the last one whose first tile id is at
-// most its own.  Group starts are multiples of 8, so the group-local id keeps
-// the hardware id's XCD; ids past the group's tiles are padding and exit at
-// once (the whole workgroup, before any barrier).
-__global__ __launch_bounds__(256, 1) void grouped_fp32_gemm_dma(GroupedGemmArgs g) {
+// Grouped GEMM over a device table of per-group parameters (whole-k tiles): the workgroup's
+// group is the last one whose first tile id is at most its own.  Group starts are multiples of
+// 8, so the group-local id keeps the hardware id's XCD; ids past the group's tiles are padding and
+// exit at once (the whole workgroup, before any barrier).
+template <int BM, int BN, int WM, int WN, int MINB, bool TB, bool TA>
+__global__ __launch_bounds__(256, MINB) void grouped_fp32_gemm_dma(GroupedGemmArgs g) {
     const int bid = blockIdx.x;
     int lo = 0, hi = g.groups - 1;
     while (lo < hi) {
@@ -463,9 +462,7 @@ __global__ __launch_bounds__(256, 1) void grouped_fp32_gemm_dma(GroupedGemmArgs 
     const GemmParams p = g.params[lo];
     const int local    = bid - g.tile_start[lo];
     if (local >= p.tiles_m * p.tiles_n) return;
-    fp32_gemm_dma_tile<256, 256, 2, 2, false>(p, local, 0);
+    fp32_gemm_dma_tile<BM, BN, WM, WN, false, TB, TA>(p, local, 0);
 }
-
-#endif
 
 }  // namespace ftrain::gemm::d32

@@ -1,6 +1,5 @@
 // FP32 tiles with LDS staging by DMA, column-major a and either b (see gemm/dma32_tile.hpp).  Only
 // the tiles whose wave rows come in runs of 64 (the row interleave of a column-major a) have one.
-#define FT_DMA32_NO_GROUPED
 #include "dma32_tile.hpp"
 
 namespace ftrain::gemm {

@@ -1,6 +1,5 @@
 // FP32 tiles with LDS staging by DMA, row-major a and column-major b (see gemm/dma32_tile.hpp).
 // The 256x256 tiles are not instantiated for column-major b: their register budget spills there.
-#define FT_DMA32_NO_GROUPED
 #include "dma32_tile.hpp"
 
 namespace ftrain::gemm {

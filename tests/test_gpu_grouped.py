@@ -258,3 +258,34 @@ def test_no_groups_and_all_empty_groups_launch_nothing(capi):
             plan.execute(i)
         torch.cuda.synchronize()
         assert torch.all(sentinel == 3.0), m_list
+
+
+def test_abcd_column_major_weights(capi, oracle):
+    """Per-expert weights stored as nn.Linear keeps them (n x k, so b_g is a column-major view):
+    every fp32 grouped Primitive, edge rows and columns, against fp64."""
+    m_list, k, n = [300, 0, 129, 512], 256, 200
+    G, M = len(m_list), sum(m_list)
+    a = rnd((M, k), 21).cuda()
+    w = rnd((G, n, k), 22).cuda()  # storage of b_g^T
+    c = rnd((M, n), 23).cuda()
+    d = torch.full((M, n), float("nan"), device="cuda")
+    ops = capi.GroupedOps("abcd")
+    al, be = capi.HostScalar(0.5), capi.HostScalar(2.0)
+    dims = [(m, n) for m in m_list]
+    args = ops.args(a=capi.GroupedSpec(capi.matrix(a), G, dims=[(m, k) for m in m_list]),
+                    b=capi.GroupedSpec(capi.matrix(w.view(G * n, k)), G, dims=[(k, n)] * G, strides=[(1, k)] * G,
+                                       offsets=[g * n * k for g in range(G)]),
+                    c=capi.GroupedSpec(capi.matrix(c), G, dims=dims), d=capi.GroupedSpec(capi.matrix(d), G, dims=dims),
+                    alpha=al.view, beta=be.view)
+    a_h, w_h, c_h = a.cpu().numpy(), w.cpu().numpy(), c.cpu().numpy()
+
+    def check(name):
+        d_h, row = d.cpu().numpy(), 0
+        for g, m in enumerate(m_list):
+            ref = oracle.gemm_f64(a_h[row:row + m], w_h[g].T.copy(), c_h[row:row + m], 0.5, 2.0)
+            close(oracle, d_h[row:row + m], ref, k, what=(name, g))
+            row += m
+        d.fill_(float("nan"))
+
+    names = run_all(capi, args, check)
+    assert "GroupedFp32Mfma16Gemm_128x128_Dma" in names, names

@@ -59,8 +59,8 @@ def test_every_grouped_kind_gets_an_ops(tlib):
         ops.close()
 
 
-FP32_GROUPED = ["GroupedFp32Mfma16Gemm_256x256_Dma", "GroupedFp32Mfma16Gemm_256x128", "GroupedFp32Mfma16Gemm_128x256",
-                "GroupedFp32MfmaGemm_128x128", "GroupedFp32MfmaGemm_64x64_Unaligned"]
+FP32_GROUPED = ["GroupedFp32Mfma16Gemm_256x256_Dma", "GroupedFp32Mfma16Gemm_128x128_Dma", "GroupedFp32Mfma16Gemm_256x128",
+                "GroupedFp32Mfma16Gemm_128x256", "GroupedFp32MfmaGemm_128x128", "GroupedFp32MfmaGemm_64x64_Unaligned"]
 
 
 def test_abcd_plan_and_primitive_order(tlib):
@@ -78,7 +78,8 @@ def test_large_groups_take_the_large_tiles(tlib):
     rows = [2100, 1900, 2300, 1700, 2048, 2200, 1800, 2336]
     st, msg, plan = moe_abcd(tlib, rows, k=4096, n=14336)
     assert st == c.SUCCESS, msg
-    assert plan.names()[0] in ("GroupedFp32Mfma16Gemm_256x256_Dma", "GroupedFp32Mfma16Gemm_128x256")
+    assert plan.names()[0] in ("GroupedFp32Mfma16Gemm_256x256_Dma", "GroupedFp32Mfma16Gemm_128x128_Dma",
+                               "GroupedFp32Mfma16Gemm_128x256")
     st, msg, plan = moe_abcd(tlib, rows, k=4096, n=14336, a_type=c.BF16)
     assert st == c.SUCCESS, msg
     assert plan.names()[0] == "GroupedBf16MfmaGemm_256x256_Dma"
@@ -134,7 +135,7 @@ def test_mixed_orientations_are_accepted(tlib):
     # Group 0 row-major, group 1 column-major a: one launch per orientation.
     st, msg, plan = moe_abcd(tlib, [64, 32], a_strides=[(64, 1), (1, 32)])
     assert st == c.SUCCESS, msg
-    # the fp32 DMA tile takes row-major a and b only
+    # the 256x256 fp32 DMA tile takes row-major a and b only
     assert sorted(plan.names()) == sorted(FP32_GROUPED[1:])
 
 
@@ -186,7 +187,7 @@ def test_ab_with_c_and_d_lists_and_a_column_major(tlib):
     cl = [D([M, N]) for _ in tokens]
     st, msg, plan = ops.args(a=a, b=b, c=cl, d=cl, alpha=al.view, beta=be.view).plan_status_on_device(0)
     assert st == c.SUCCESS, msg
-    assert sorted(plan.names()) == sorted(FP32_GROUPED[1:])  # column-major a: no fp32 DMA tile
+    assert sorted(plan.names()) == sorted(FP32_GROUPED[2:])  # k of 40 and 24: no fp32 DMA tile
 
 
 def test_descriptor_values_that_overflow_addresses_are_rejected(tlib):
