@@ -68,6 +68,10 @@ constexpr VariantInfo kInfo[] = {
     {"Fp16MfmaGemm_64x64_Unaligned", 64, 64, 32, 256, 2, false, N, false, false, true, 0.08, FP16, 4096.0, 0.08},
     {"Bf16MfmaGemm_256x256_Dma", 256, 256, 64, 256, 1, true, N, false, false, true, 0.66, BF16, 4096.0, 0.66},
     {"Fp16MfmaGemm_256x256_Dma", 256, 256, 64, 256, 1, true, N, false, false, true, 0.66, FP16, 4096.0, 0.66},
+    {"Bf16MfmaGemm_128x128_Dma", 128, 128, 64, 256, 2, true, N, false, false, true, 0.48, BF16, 4096.0, 0.45},
+    {"Bf16MfmaGemm_128x128_Dma_SplitK", 128, 128, 64, 256, 2, true, P, false, false, true, 0.55, BF16, 4096.0, 0.45},
+    {"Fp16MfmaGemm_128x128_Dma", 128, 128, 64, 256, 2, true, N, false, false, true, 0.48, FP16, 4096.0, 0.45},
+    {"Fp16MfmaGemm_128x128_Dma_SplitK", 128, 128, 64, 256, 2, true, P, false, false, true, 0.55, FP16, 4096.0, 0.45},
     {"Bf16Gemv", kGemvHalfRows, kGemvHalfCols, 1, 1024, 1, true, N, true, false, false, 0, BF16, 4096.0, 0},
     {"Fp16Gemv", kGemvHalfRows, kGemvHalfCols, 1, 1024, 1, true, N, true, false, false, 0, FP16, 4096.0, 0},
 };

@@ -1,5 +1,6 @@
-// BF16 / FP16 256x256 tile kernel whose operands reach LDS by DMA
-// (global_load_lds_dwordx4) instead of through registers, plain and grouped.
+// BF16 / FP16 tile kernels whose operands reach LDS by DMA
+// (global_load_lds_dwordx4) instead of through registers: 256x256 (plain and
+// grouped) and 128x128 (plain whole-k and split-k, grouped).
 // Device code only; the per-type translation units kernels_half_dma_*.hip
 // instantiate it.
 //
@@ -12,22 +13,23 @@
 // extents multiples of 8; m and n are free (edge tiles clamp their loads and
 // drop their out-of-matrix stores).
 //
-// Workgroup: 4 waves (one per SIMD), each a 128x128 block of the tile, as
-// 4x4 v_mfma_f32_32x32x16 blocks:
+// Workgroup: 4 waves (one per SIMD), each a T/2 x T/2 block of the tile, as
+// (T/64) x (T/64) v_mfma_f32_32x32x16 blocks (4x4 at T = 256, 2x2 at 128):
 //   A operand: lane l holds A[row l % 32][8 consecutive k]
 //   B operand: lane l holds B[the same 8 k][col l % 32]
 //   result   : lane l, register r holds D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]
 // In k-step s (16 k) lane half h = l / 32 takes k 16 s + 8 h .. 16 s + 8 h + 7.
 //
-// Stage = 64 k of both operands, 32 KiB each; two LDS stages (128 KiB).
-// One DMA instruction moves 64 lanes x 16 bytes into 1 KiB of LDS at
-// M0 + 16 * lane, each lane from its own global address, so a stage takes 32
-// instructions per operand, 8 per wave.  Each covers whole 128-byte lines:
+// Stage = 64 k of both operands, T x 64 x 2 bytes each; two LDS stages (128
+// KiB at T = 256, 64 KiB at 128).  One DMA instruction moves 64 lanes x 16
+// bytes into 1 KiB of LDS at M0 + 16 * lane, each lane from its own global
+// address, so a stage takes T/8 instructions per operand, T/32 per wave.
+// Each covers whole 128-byte lines:
 //   k-contiguous operand (row-major a, column-major b): 8 rows x 64 k, LDS
-//     [256 rows][64 k], 16-byte chunk c of row r at slot c ^ ((r >> 1) & 7);
+//     [T rows][64 k], 16-byte chunk c of row r at slot c ^ ((r >> 1) & 7);
 //     read with ds_read_b128 (one per operand);
-//   transposed operand (column-major a, row-major b): 2 k rows x 256, LDS
-//     [64 k][256], chunk c of k row kr at slot c ^ (4 (kr & 3)); read with
+//   transposed operand (column-major a, row-major b): 512 / T k rows x T,
+//     LDS [64 k][T], chunk c of k row kr at slot c ^ (4 (kr & 3)); read with
 //     ds_read_b64_tr_b16 (two per operand).
 // Both swizzles keep the reads free of bank conflicts (SQ_LDS_BANK_CONFLICT
 // reads 0 on MI355X).
@@ -68,11 +70,10 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 using u16 = unsigned short;
 
-constexpr int kTile = 256, kStageK = 64;
+constexpr int kStageK = 64;
 // Word 3 of a raw (untyped, stride 0) buffer resource on gfx9 parts: 32-bit data format, the range
 // check against num_records on every access.
 constexpr int kBufferConfig = 0x00020000;
-constexpr int kStageElems = kTile * kStageK;  // one operand, one stage: 32 KiB
 
 template <bool BF16>
 __device__ __forceinline__ floatx16 mfma(u32x4 a, u32x4 b, floatx16 acc) {
@@ -129,8 +130,10 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
 // columns) past the matrix edge are clamped onto its last row (column
 // group): they read valid memory and feed only outputs the epilogue does not
 // store.
-template <bool TR>
+template <bool TR, int T>
 struct Operand {
+    static constexpr int kCpr = T / 8;        // TR: 16-byte chunks per k row
+    static constexpr int kRpd = 64 / kCpr;    // TR: k rows per DMA block
     const char* base;  // tile origin (element 0 of its first row / k row)
     int64_t ld;        // leading dimension, elements
     unsigned voff;     // TR: this lane's byte offset inside every DMA block
@@ -143,10 +146,11 @@ struct Operand {
     __device__ __forceinline__ void init(const u16* m, int64_t ld_, int origin, int extent, int wave, int lane) {
         ld = ld_;
         if constexpr (TR) {
-            // Block q = wave + 4 j holds k rows 2q, 2q + 1 (lane: row 2q + lane / 32); slot lane % 32
-            // holds 8-element chunk (lane % 32) ^ (4 (kr & 3)).  kr & 3 does not depend on j.  The
-            // extent is a multiple of 8, so a clamped chunk is a whole one.
-            const int kr = 2 * wave + (lane >> 5), chunk = (lane & 31) ^ (4 * (kr & 3));
+            // Block q = wave + 4 j holds k rows R q .. R q + R - 1, R = 64 / (T / 8) (lane: row
+            // R q + lane / (T / 8)); slot lane % (T / 8) holds 8-element chunk (lane % (T / 8)) ^
+            // (4 (kr & 3)).  kr & 3 does not depend on j (4 R j is a multiple of 4).  The extent is a
+            // multiple of 8, so a clamped chunk is a whole one.
+            const int kr = kRpd * wave + lane / kCpr, chunk = (lane % kCpr) ^ (4 * (kr & 3));
             const int col = min(origin + 8 * chunk, extent - 8) - origin;
             base          = reinterpret_cast<const char*>(m + origin);
             voff          = static_cast<unsigned>((kr * ld + col) * 2);
@@ -155,15 +159,15 @@ struct Operand {
             // holds k chunk (lane % 8) ^ ((row >> 1) & 7), which does not depend on j.
             r8      = 8 * wave + (lane >> 3);
             chunk16 = 16 * ((lane & 7) ^ ((r8 >> 1) & 7));
-            last    = static_cast<unsigned>(min(extent - 1 - origin, kTile - 1));
+            last    = static_cast<unsigned>(min(extent - 1 - origin, T - 1));
             ld2     = static_cast<unsigned>(2 * ld);
             base    = reinterpret_cast<const char*>(m + (size_t)origin * ld);
         }
     }
-    // DMA j (0..7) of this wave for stage st into the stage buffer at LDS byte address lds.
+    // DMA j (0 .. T / 32 - 1) of this wave for stage st into the stage buffer at LDS byte address lds.
     __device__ __forceinline__ void dma(int st, int j, unsigned lds, int wave) const {
         if constexpr (TR) {
-            dma_1k(voff, base + ((size_t)st * kStageK + 8 * j) * ld * 2, lds + (wave + 4 * j) * 1024);
+            dma_1k(voff, base + ((size_t)st * kStageK + 4 * kRpd * j) * ld * 2, lds + (wave + 4 * j) * 1024);
         } else {
             // Row 32 j + r8 of the tile, clamped to the matrix (255 * ld2 < 2^32).
             const unsigned row = min(r8 + 32u * j, last);
@@ -172,27 +176,38 @@ struct Operand {
     }
 };
 
-// Output tile `bid` of p (tile_of order); the whole workgroup calls it.
-template <bool BF16, bool TA, bool TB>
-__device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int bid) {
+// Output tile `bid` of p (tile_of order), k split z when SPLIT; the whole workgroup calls it.
+// T: tile size (256: waves of 128x128, one workgroup per CU; 128: waves of 64x64, two per CU).
+// SPLIT: the workgroup reduces k range [z k_chunk, (z + 1) k_chunk) and stores its raw fp32 sums
+// to slice z of p.d (dense m x n); the reduction kernel forms d.
+template <bool BF16, bool TA, bool TB, int T = 256, bool SPLIT = false>
+__device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int bid, int z = 0) {
     constexpr bool A_TR = TA, B_TR = !TB;
+    constexpr int NB = T / 64;               // 32x32 blocks per wave row and column
+    constexpr int NDO = T / 32;              // DMAs per wave per operand per stage
+    constexpr int kStageElems = T * kStageK;  // one operand, one stage
     __shared__ __attribute__((aligned(1024))) u16 As0[kStageElems];
     __shared__ __attribute__((aligned(1024))) u16 Bs0[kStageElems];
     __shared__ __attribute__((aligned(1024))) u16 As1[kStageElems];
     __shared__ __attribute__((aligned(1024))) u16 Bs1[kStageElems];
     const int tid = threadIdx.x, lane = tid & 63, li = lane & 31, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wrow = (wave >> 1) * 128, wcol = (wave & 1) * 128;
+    const int wrow = (wave >> 1) * (T / 2), wcol = (wave & 1) * (T / 2);
     int tm, tn;
     tile_of(bid, p.tiles_m, p.tiles_n, tm, tn);
-    const int m0 = tm * kTile, n0 = tn * kTile;
+    const int m0 = tm * T, n0 = tn * T;
     const int M = p.m, N = p.n;
-    const int nst = p.k / kStageK;
+    const int kbeg = SPLIT ? z * p.k_chunk : 0;
+    const int nst  = ((SPLIT ? min(p.k, kbeg + p.k_chunk) : p.k) - kbeg) / kStageK;
 
-    Operand<A_TR> opa;
-    Operand<B_TR> opb;
-    opa.init(static_cast<const u16*>(p.a), p.lda, m0, M, wave, lane);
-    opb.init(static_cast<const u16*>(p.b), p.ldb, n0, N, wave, lane);
+    // A split's operands start at k = kbeg: a k-contiguous operand's rows advance by kbeg
+    // elements, a transposed one's by kbeg rows.
+    const u16* const pa = static_cast<const u16*>(p.a) + (A_TR ? (size_t)kbeg * p.lda : (size_t)kbeg);
+    const u16* const pb = static_cast<const u16*>(p.b) + (B_TR ? (size_t)kbeg * p.ldb : (size_t)kbeg);
+    Operand<A_TR, T> opa;
+    Operand<B_TR, T> opb;
+    opa.init(pa, p.lda, m0, M, wave, lane);
+    opb.init(pb, p.ldb, n0, N, wave, lane);
     const unsigned la0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)As0;
     const unsigned lb0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)Bs0;
     const unsigned la1 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)As1;
@@ -200,33 +215,35 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
 
     // Operand of k-step ks (0..3 in the stage) for rows (or columns) x .. x + 31.
     const int tr_k = (lane & 15) >> 2, tr_x = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    auto rd_k = [&](const u16* T, int x, int ks) {  // k-contiguous
+    auto rd_k = [&](const u16* S, int x, int ks) {  // k-contiguous
         const int row = x + li, pos = (2 * ks + h) ^ ((row >> 1) & 7);
-        return *reinterpret_cast<const u32x4*>(T + row * kStageK + 8 * pos);
+        return *reinterpret_cast<const u32x4*>(S + row * kStageK + 8 * pos);
     };
     // Transposed: within each 16 lanes, lane 4j + e reads elements x + tr_x .. + 3 of k row kk + j;
     // lane 4e + i receives element i of lanes e, 4 + e, 8 + e, 12 + e, i.e. 4 consecutive k of
     // column x + lane % 32.  Part `part` covers k 16 ks + 8 h + 4 part .. + 3.
-    auto rd_t = [&](const u16* T, int x, int ks, int part) {
+    auto rd_t = [&](const u16* S, int x, int ks, int part) {
         const int k = 16 * ks + 8 * h + 4 * part + tr_k, n = x + tr_x;
         const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_v4i16*)(T + k * kTile + 8 * ((n >> 3) ^ (4 * (k & 3))) + (n & 7)));
+            (lds_v4i16*)(S + k * T + 8 * ((n >> 3) ^ (4 * (k & 3))) + (n & 7)));
         return __builtin_bit_cast(u32x2, v);
     };
 
-    floatx16 acc[4][4];
+    floatx16 acc[NB][NB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NB; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NB; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     // Operands of one half stage (32 k): [k-step][block].
-    u32x4 fa0[2][4], fb0[2][4], fa1[2][4], fb1[2][4];
-    constexpr int NRA = A_TR ? 16 : 8, NRB = B_TR ? 16 : 8, NR = NRA + NRB;
+    u32x4 fa0[2][NB], fb0[2][NB], fa1[2][NB], fb1[2][NB];
+    constexpr int NRA = (A_TR ? 4 : 2) * NB, NRB = (B_TR ? 4 : 2) * NB, NR = NRA + NRB;
+    constexpr int NM = 2 * NB * NB;  // MFMAs per half stage
+    constexpr int ND = 2 * NDO;      // DMAs per wave per stage
     // LDS read r (0 .. NR-1) of half `hf`, ordered k-step major (A then B within a k-step), into (ga, gb).
-    auto read_one = [&](u32x4 (&ga)[2][4], u32x4 (&gb)[2][4], const u16* As, const u16* Bs, int hf, int r) {
+    auto read_one = [&](u32x4 (&ga)[2][NB], u32x4 (&gb)[2][NB], const u16* As, const u16* Bs, int hf, int r) {
         const int s = r / (NR / 2), q = r % (NR / 2), ks = 2 * hf + s;
         if (q < NRA / 2) {
             if constexpr (A_TR) {
@@ -247,46 +264,49 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
             }
         }
     };
-    // 32 MFMAs on (fa, fb); the NR reads of half hf of (As, Bs) into (ga, gb) and, with a true
-    // with_dma, the 16 DMAs of stage dma_st into (la, lb) are spread between them in a fixed order.
-    auto run_half = [&](u32x4 (&fa)[2][4], u32x4 (&fb)[2][4], u32x4 (&ga)[2][4], u32x4 (&gb)[2][4], const u16* As,
-                    const u16* Bs, int hf, auto with_dma, int dma_st, unsigned la, unsigned lb) {
+    // NM MFMAs on (fa, fb) (k-step major, then block row, block column); the NR reads of half hf
+    // of (As, Bs) into (ga, gb) and, with a true with_dma, the ND DMAs of stage dma_st into (la,
+    // lb) (A and B alternating) are spread between them in a fixed order.
+    auto run_half = [&](u32x4 (&fa)[2][NB], u32x4 (&fb)[2][NB], u32x4 (&ga)[2][NB], u32x4 (&gb)[2][NB],
+                        const u16* As, const u16* Bs, int hf, auto with_dma, int dma_st, unsigned la, unsigned lb) {
 #pragma unroll
-        for (int t = 0; t < 32; ++t) {
-            acc[(t >> 2) & 3][t & 3] = mfma<BF16>(fa[t >> 4][(t >> 2) & 3], fb[t >> 4][t & 3], acc[(t >> 2) & 3][t & 3]);
+        for (int t = 0; t < NM; ++t) {
+            const int s = t / (NB * NB), bi = (t / NB) % NB, bj = t % NB;
+            acc[bi][bj] = mfma<BF16>(fa[s][bi], fb[s][bj], acc[bi][bj]);
 #pragma unroll
             for (int r = 0; r < NR; ++r)
-                if ((r * 32) / NR == t) read_one(ga, gb, As, Bs, hf, r);
+                if ((r * NM) / NR == t) read_one(ga, gb, As, Bs, hf, r);
             if constexpr (decltype(with_dma)::value) {
-                if (t & 1) {
-                    const int u = t >> 1;
-                    if (u & 1)
-                        opb.dma(dma_st, u >> 1, lb, wave);
-                    else
-                        opa.dma(dma_st, u >> 1, la, wave);
-                }
+#pragma unroll
+                for (int d = 0; d < ND; ++d)
+                    if (((2 * d + 1) * NM) / (2 * ND) == t) {
+                        if (d & 1)
+                            opb.dma(dma_st, d >> 1, lb, wave);
+                        else
+                            opa.dma(dma_st, d >> 1, la, wave);
+                    }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    auto read_half = [&](u32x4 (&ga)[2][4], u32x4 (&gb)[2][4], const u16* As, const u16* Bs, int hf) {
+    auto read_half = [&](u32x4 (&ga)[2][NB], u32x4 (&gb)[2][NB], const u16* As, const u16* Bs, int hf) {
 #pragma unroll
         for (int r = 0; r < NR; ++r) read_one(ga, gb, As, Bs, hf, r);
     };
 
-    // Prologue: stages 0 and 1 in flight (8 + 8 DMAs per wave each); wait for stage 0.
+    // Prologue: stages 0 and 1 in flight (ND DMAs per wave each); wait for stage 0.
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < NDO; ++j) {
         opa.dma(0, j, la0, wave);
         opb.dma(0, j, lb0, wave);
     }
     const int st1 = min(1, nst - 1);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < NDO; ++j) {
         opa.dma(st1, j, la1, wave);
         opb.dma(st1, j, lb1, wave);
     }
-    asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(ND) : "memory");
     read_half(fa0, fb0, As0, Bs0, 0);
 
     // Stages past the last reload the last one (harmless: nothing reads them).
@@ -320,14 +340,18 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
         constexpr bool HAS_C = decltype(c_tag)::value;
         constexpr bool HALF  = decltype(half_tag)::value;
         constexpr unsigned ES = HALF ? 2 : 4;
-        const unsigned ldd = static_cast<unsigned>(p.ldd), ldc = static_cast<unsigned>(p.ldc);
+        // Split-k: raw fp32 sums to slice z of the workspace (dense m x n).
+        const uint64_t ldd64 = SPLIT ? (uint64_t)N : (uint64_t)p.ldd;
+        char* const dcorner = SPLIT ? reinterpret_cast<char*>(static_cast<float*>(p.d) + (size_t)z * M * N +
+                                                              (size_t)m0 * N + n0)
+                                    : static_cast<char*>(p.d) + ((size_t)m0 * p.ldd + n0) * ES;
+        const unsigned ldd = static_cast<unsigned>(ldd64), ldc = static_cast<unsigned>(p.ldc);
         const int rows_left = M - m0, cols_left = N - n0;
         auto span = [&](uint64_t ld) {  // bytes from the tile's corner to the matrix's last element
             const uint64_t b = ((uint64_t)(rows_left - 1) * ld + (uint64_t)cols_left) * ES;
             return static_cast<int>(b < 0x7FFFFFFFull ? b : 0x7FFFFFFFull);
         };
-        const __amdgpu_buffer_rsrc_t dres = __builtin_amdgcn_make_buffer_rsrc(
-            static_cast<char*>(p.d) + ((size_t)m0 * p.ldd + n0) * ES, 0, span(p.ldd), kBufferConfig);
+        const __amdgpu_buffer_rsrc_t dres = __builtin_amdgcn_make_buffer_rsrc(dcorner, 0, span(ldd64), kBufferConfig);
         __amdgpu_buffer_rsrc_t cres = dres;
         if constexpr (HAS_C)
             cres = __builtin_amdgcn_make_buffer_rsrc(
@@ -336,9 +360,9 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
         const unsigned lane_d = (4 * h * ldd + li) * ES, lane_c = (4 * h * ldc + li) * ES;
         constexpr unsigned kOut = 0x80000000u;
 #pragma unroll
-        for (int bi = 0; bi < 4; ++bi)
+        for (int bi = 0; bi < NB; ++bi)
 #pragma unroll
-            for (int bj = 0; bj < 4; ++bj) {
+            for (int bj = 0; bj < NB; ++bj) {
                 const int col    = wcol + 32 * bj;  // wave-uniform block column
                 const bool colok = col + li < cols_left;
                 float cv[16];
@@ -360,7 +384,7 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
                     const int row0 = wrow + 32 * bi + 8 * (r / 4) + (r % 4);
                     const bool ok  = colok && 4 * h < rows_left - row0;
                     const int so   = static_cast<int>((row0 * ldd + col) * ES);
-                    float out      = alpha * acc[bi][bj][r];
+                    float out      = SPLIT ? acc[bi][bj][r] : alpha * acc[bi][bj][r];
                     if constexpr (HAS_C) out += beta * cv[r];
                     // Non-temporal (aux 2): d is not read again here.
                     if constexpr (HALF)
@@ -371,7 +395,9 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
                 }
             }
     };
-    if (p.c != nullptr) {
+    if constexpr (SPLIT) {
+        epilogue(std::false_type{}, std::false_type{});
+    } else if (p.c != nullptr) {
         if (p.cd_half)
             epilogue(std::true_type{}, std::true_type{});
         else
@@ -389,13 +415,31 @@ __global__ __launch_bounds__(256, 1) void half_gemm_dma(HalfGemmParams p) {
     half_gemm_dma_tile<BF16, TA, TB>(p, blockIdx.x);
 }
 
+// 128x128 tiles, two workgroups per CU, whole-k or split-k.  Split-k workgroups are renumbered so
+// each XCD runs whole k splits (hardware ids go to the XCDs in turn, x fastest).
+template <bool BF16, bool TA, bool TB, bool SPLIT>
+__global__ __launch_bounds__(256, 2) void half_gemm_dma128(HalfGemmParams p) {
+    int bid = blockIdx.x, z = blockIdx.z;
+    if constexpr (SPLIT) {
+        const int tiles = gridDim.x, total = tiles * gridDim.z;
+        if ((total & 7) == 0) {
+            const int lin = blockIdx.x + tiles * blockIdx.z;
+            const int w   = (lin & 7) * (total >> 3) + (lin >> 3);
+            z             = w / tiles;
+            const int t   = w - z * tiles, per = tiles >> 3;
+            bid           = t < (per << 3) ? ((t % per) << 3) + t / per : t;
+        }
+    }
+    half_gemm_dma_tile<BF16, TA, TB, 128, SPLIT>(p, bid, z);
+}
+
 // Grouped GEMM over a device table of per-group parameters: the workgroup's
 // group is the last one whose first tile id is at most its own.  Group starts
 // are multiples of 8, so the group-local id keeps the hardware id's XCD;
 // ids past the group's tiles are padding and exit at once (before any
 // barrier, the whole workgroup).
-template <bool BF16, bool TA, bool TB>
-__global__ __launch_bounds__(256, 1) void grouped_half_gemm_dma(GroupedHalfArgs g) {
+template <bool BF16, bool TA, bool TB, int T = 256>
+__global__ __launch_bounds__(256, 256 / T) void grouped_half_gemm_dma(GroupedHalfArgs g) {
     const int bid = blockIdx.x;
     int lo = 0, hi = g.groups - 1;
     while (lo < hi) {
@@ -408,16 +452,24 @@ __global__ __launch_bounds__(256, 1) void grouped_half_gemm_dma(GroupedHalfArgs 
     const HalfGemmParams p = g.params[lo];
     const int local        = bid - g.tile_start[lo];
     if (local >= p.tiles_m * p.tiles_n) return;
-    half_gemm_dma_tile<BF16, TA, TB>(p, local);
+    half_gemm_dma_tile<BF16, TA, TB, T>(p, local);
 }
 
-// Kernel for one input type and operand orientation (ta: column-major a, tb: column-major b).
-template <bool BF16>
+// Kernel for one input type, tile size and operand orientation (ta: column-major a, tb:
+// column-major b).
+template <bool BF16, int T = 256>
 const void* groupedDmaKernel(bool ta, bool tb) {
-    if (ta) return tb ? reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, true, true>)
-                      : reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, true, false>);
-    return tb ? reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, false, true>)
-              : reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, false, false>);
+    if (ta) return tb ? reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, true, true, T>)
+                      : reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, true, false, T>);
+    return tb ? reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, false, true, T>)
+              : reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, false, false, T>);
+}
+template <bool BF16, bool SPLIT>
+const void* dma128Kernel(bool ta, bool tb) {
+    if (ta) return tb ? reinterpret_cast<const void*>(&half_gemm_dma128<BF16, true, true, SPLIT>)
+                      : reinterpret_cast<const void*>(&half_gemm_dma128<BF16, true, false, SPLIT>);
+    return tb ? reinterpret_cast<const void*>(&half_gemm_dma128<BF16, false, true, SPLIT>)
+              : reinterpret_cast<const void*>(&half_gemm_dma128<BF16, false, false, SPLIT>);
 }
 template <bool BF16>
 const void* dmaKernel(bool ta, bool tb) {

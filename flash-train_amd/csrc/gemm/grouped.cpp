@@ -287,10 +287,12 @@ constexpr GroupedVariant kGroupedVariants[] = {
     {"GroupedFp32MfmaGemm_128x128", FTRAIN_NUMERIC_TYPE_FP32, 0, gemm::Variant::kMfma128x128},
     {"GroupedFp32MfmaGemm_64x64_Unaligned", FTRAIN_NUMERIC_TYPE_FP32, 1, gemm::Variant::kMfma64x64U},
     {"GroupedBf16MfmaGemm_256x256_Dma", FTRAIN_NUMERIC_TYPE_BF16, 3, gemm::Variant::kBf16MfmaDma256x256},
+    {"GroupedBf16MfmaGemm_128x128_Dma", FTRAIN_NUMERIC_TYPE_BF16, 4, gemm::Variant::kBf16MfmaDma128x128},
     {"GroupedBf16MfmaGemm_256x256", FTRAIN_NUMERIC_TYPE_BF16, 2, gemm::Variant::kBf16Mfma256x256},
     {"GroupedBf16MfmaGemm_128x128", FTRAIN_NUMERIC_TYPE_BF16, 0, gemm::Variant::kBf16Mfma128x128},
     {"GroupedBf16MfmaGemm_64x64_Unaligned", FTRAIN_NUMERIC_TYPE_BF16, 1, gemm::Variant::kBf16Mfma64x64U},
     {"GroupedFp16MfmaGemm_256x256_Dma", FTRAIN_NUMERIC_TYPE_FP16, 3, gemm::Variant::kFp16MfmaDma256x256},
+    {"GroupedFp16MfmaGemm_128x128_Dma", FTRAIN_NUMERIC_TYPE_FP16, 4, gemm::Variant::kFp16MfmaDma128x128},
     {"GroupedFp16MfmaGemm_256x256", FTRAIN_NUMERIC_TYPE_FP16, 2, gemm::Variant::kFp16Mfma256x256},
     {"GroupedFp16MfmaGemm_128x128", FTRAIN_NUMERIC_TYPE_FP16, 0, gemm::Variant::kFp16Mfma128x128},
     {"GroupedFp16MfmaGemm_64x64_Unaligned", FTRAIN_NUMERIC_TYPE_FP16, 1, gemm::Variant::kFp16Mfma64x64U},
@@ -376,7 +378,8 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
                 return Result(FTRAIN_STATUS_UNSUPPORTED,
                               "a group's k is not a positive multiple of 32 or a leading dimension is too large for "
                               "32-bit offsets (fp32 DMA tiles)");
-            if ((v_->tile == gemm::Variant::kBf16MfmaDma256x256 || v_->tile == gemm::Variant::kFp16MfmaDma256x256) &&
+            if ((v_->tile == gemm::Variant::kBf16MfmaDma256x256 || v_->tile == gemm::Variant::kFp16MfmaDma256x256 ||
+                 v_->tile == gemm::Variant::kBf16MfmaDma128x128 || v_->tile == gemm::Variant::kFp16MfmaDma128x128) &&
                 (l.shape.k == 0 || l.shape.k % 64 != 0 || l.lda >= (int64_t(1) << 23) || l.ldb >= (int64_t(1) << 23) ||
                  l.ldc >= (int64_t(1) << 21) || l.ldd >= (int64_t(1) << 21)))
                 return Result(FTRAIN_STATUS_UNSUPPORTED,

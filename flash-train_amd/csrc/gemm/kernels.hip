@@ -425,6 +425,10 @@ const void* kernelFor(Variant v, bool ta, bool tb) {
     if (v >= Variant::kMfma16Dma256x256 && v <= Variant::kMfma16Dma64x64S) return ta ? dma32KernelTA(v, tb) : tb ? dma32KernelTB(v) : dma32Kernel(v);
     if (v == Variant::kBf16MfmaDma256x256) return dmaKernelBf16(ta, tb);
     if (v == Variant::kFp16MfmaDma256x256) return dmaKernelFp16(ta, tb);
+    if (v == Variant::kBf16MfmaDma128x128 || v == Variant::kBf16MfmaDma128x128S)
+        return dma128KernelBf16(ta, tb, v == Variant::kBf16MfmaDma128x128S);
+    if (v == Variant::kFp16MfmaDma128x128 || v == Variant::kFp16MfmaDma128x128S)
+        return dma128KernelFp16(ta, tb, v == Variant::kFp16MfmaDma128x128S);
     if (ta || tb) {
         if (v == Variant::kSimt) return reinterpret_cast<const void*>(&simt_gemm);  // strides are runtime values
         if (v == Variant::kGemvS && !tb && ta) return reinterpret_cast<const void*>(&gemv_splitk<true, true>);
@@ -459,6 +463,7 @@ const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool t
     const int t = input == FTRAIN_NUMERIC_TYPE_FP32 ? 0 : input == FTRAIN_NUMERIC_TYPE_BF16 ? 1 : 2;
     const int o = (ta ? 1 : 0) + (tb ? 2 : 0);
     if (t != 0 && which == 3) return t == 1 ? groupedDmaKernelBf16(ta, tb) : groupedDmaKernelFp16(ta, tb);
+    if (t != 0 && which == 4) return t == 1 ? groupedDma128KernelBf16(ta, tb) : groupedDma128KernelFp16(ta, tb);
     if (t == 0 && which == 4) return ta || tb ? nullptr : groupedDma32Kernel();
     if (t == 0 && which == 5) return groupedDma32Kernel128(ta, tb);
     if (t == 0 && (which == 2 || which == 3)) {

@@ -7,4 +7,10 @@ const void* dmaKernelBf16(bool ta, bool tb) { return ddev::dmaKernel<true>(ta, t
 
 const void* groupedDmaKernelBf16(bool ta, bool tb) { return ddev::groupedDmaKernel<true>(ta, tb); }
 
+const void* groupedDma128KernelBf16(bool ta, bool tb) { return ddev::groupedDmaKernel<true, 128>(ta, tb); }
+
+const void* dma128KernelBf16(bool ta, bool tb, bool split) {
+    return split ? ddev::dma128Kernel<true, true>(ta, tb) : ddev::dma128Kernel<true, false>(ta, tb);
+}
+
 }  // namespace ftrain::gemm

@@ -7,4 +7,10 @@ const void* dmaKernelFp16(bool ta, bool tb) { return ddev::dmaKernel<false>(ta, 
 
 const void* groupedDmaKernelFp16(bool ta, bool tb) { return ddev::groupedDmaKernel<false>(ta, tb); }
 
+const void* groupedDma128KernelFp16(bool ta, bool tb) { return ddev::groupedDmaKernel<false, 128>(ta, tb); }
+
+const void* dma128KernelFp16(bool ta, bool tb, bool split) {
+    return split ? ddev::dma128Kernel<false, true>(ta, tb) : ddev::dma128Kernel<false, false>(ta, tb);
+}
+
 }  // namespace ftrain::gemm

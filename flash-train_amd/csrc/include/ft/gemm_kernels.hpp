@@ -196,6 +196,11 @@ enum class Variant : int {
     // (global_load_lds_dwordx4): k a multiple of 64, any m and n.
     kBf16MfmaDma256x256,
     kFp16MfmaDma256x256,
+    // bf16 / fp16 128x128 DMA-staged tiles (two workgroups per CU), whole-k and split-k.
+    kBf16MfmaDma128x128,
+    kBf16MfmaDma128x128S,
+    kFp16MfmaDma128x128,
+    kFp16MfmaDma128x128S,
     // One-pass skinny-m kernels (m <= 8, row-major b) for bf16 / fp16 inputs.
     kBf16Gemv,
     kFp16Gemv,
@@ -282,8 +287,12 @@ const void* dma32KernelTB(Variant v);  // column-major b
 const void* dma32KernelTA(Variant v, bool tb);  // column-major a
 const void* dmaKernelBf16(bool ta, bool tb);
 const void* dmaKernelFp16(bool ta, bool tb);
+const void* dma128KernelBf16(bool ta, bool tb, bool split);
+const void* dma128KernelFp16(bool ta, bool tb, bool split);
 const void* groupedDmaKernelBf16(bool ta, bool tb);
 const void* groupedDmaKernelFp16(bool ta, bool tb);
+const void* groupedDma128KernelBf16(bool ta, bool tb);
+const void* groupedDma128KernelFp16(bool ta, bool tb);
 // Grouped kernels: element type (FTRAIN_NUMERIC_TYPE_FP32 / BF16 / FP16),
 // tile (0 = 128x128 with 16-byte loads, 1 = 64x64 per-element, 2 = the
 // family's large tile: fp32 16x16x4 256x128, bf16/fp16 256x256; 3 = fp32

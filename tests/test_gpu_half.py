@@ -110,13 +110,17 @@ def test_half_every_primitive(capi, ops, oracle, kind, cd, la, lb, m, n, k, pad)
                                               (256, 512, 1024, 0, True), (296, 520, 128, 8, True),
                                               (40, 24, 64, 0, False)])
 def test_half_dma_tile(capi, ops, oracle, kind, cd, la, lb, m, n, k, pad, with_c):
-    # The 256x256 tile with LDS staging by DMA: one stage (k = 64), an odd stage count (the tail
+    # The 256x256 and 128x128 tiles with LDS staging by DMA (the 128x128 one also split-k): one
+    # stage (k = 64), an odd stage count (the tail
     # copy of the pipeline), a long even one, edge tiles in m and n (loads clamped, stores
     # checked) and a matrix smaller than one tile; every operand orientation, NaN past each
     # leading dimension's used extent, 7.0 around d (nothing written outside it).
     names = run_case(capi, ops, oracle, kind, kind if cd == "same" else "fp32", m, n, k, la, lb, pad=pad,
                      with_c=with_c, seed=k + pad)
     assert f"{kind.capitalize()}MfmaGemm_256x256_Dma" in names, names
+    assert f"{kind.capitalize()}MfmaGemm_128x128_Dma" in names, names
+    if k >= 512:
+        assert f"{kind.capitalize()}MfmaGemm_128x128_Dma_SplitK" in names, names
 
 
 @pytest.mark.parametrize("cd", ["fp32", "same"])
@@ -141,12 +145,13 @@ def test_half_dma_tile_exact_and_repeatable(capi, ops, kind):
     bt = torch.from_numpy(b).to(DT[kind]).cuda()
     d = torch.empty(m, n, device="cuda")
     plan = capi.plan_for(at, bt, None, d, 1.0, 0.0, ops)
-    i = plan.names().index(f"{kind.capitalize()}MfmaGemm_256x256_Dma")
-    for _ in range(2):
-        d.fill_(float("nan"))
-        plan.execute(i, torch.cuda.current_stream().cuda_stream)
-        torch.cuda.synchronize()
-        np.testing.assert_array_equal(d.cpu().numpy(), exact)
+    for tile in ("256x256", "128x128"):
+        i = plan.names().index(f"{kind.capitalize()}MfmaGemm_{tile}_Dma")
+        for _ in range(2):
+            d.fill_(float("nan"))
+            plan.execute(i, torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(d.cpu().numpy(), exact)
 
 
 @pytest.mark.parametrize("kind", ["bf16", "fp16"])

@@ -110,15 +110,16 @@ def test_unaligned_groups_take_the_per_element_tile(tlib):
 def test_half_types_select_their_variants(tlib):
     st, msg, plan = moe_abcd(tlib, [64, 32], a_type=c.BF16)
     assert st == c.SUCCESS, msg
-    assert sorted(plan.names()) == sorted(["GroupedBf16MfmaGemm_256x256_Dma", "GroupedBf16MfmaGemm_256x256",
-                                           "GroupedBf16MfmaGemm_128x128", "GroupedBf16MfmaGemm_64x64_Unaligned"])
+    assert sorted(plan.names()) == sorted(["GroupedBf16MfmaGemm_256x256_Dma", "GroupedBf16MfmaGemm_128x128_Dma",
+                                           "GroupedBf16MfmaGemm_256x256", "GroupedBf16MfmaGemm_128x128",
+                                           "GroupedBf16MfmaGemm_64x64_Unaligned"])
     st, msg, plan = moe_abcd(tlib, [64, 32], a_type=c.FP16, d_type=c.FP16)
     assert st == c.SUCCESS, msg
-    assert all(n.startswith("GroupedFp16") for n in plan.names()) and len(plan) == 4
-    # k not a multiple of 64: the DMA tile (whole 64-k stages) steps aside.
+    assert all(n.startswith("GroupedFp16") for n in plan.names()) and len(plan) == 5
+    # k not a multiple of 64: the DMA tiles (whole 64-k stages) step aside.
     st, msg, plan = moe_abcd(tlib, [64, 32], k=72, a_type=c.BF16)
     assert st == c.SUCCESS, msg
-    assert "GroupedBf16MfmaGemm_256x256_Dma" not in plan.names() and len(plan) == 3
+    assert not any(n.endswith("_Dma") for n in plan.names()) and len(plan) == 3
 
 
 def test_group_shape_mismatch_is_invalid(tlib):
