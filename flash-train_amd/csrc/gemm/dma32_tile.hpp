@@ -1,8 +1,11 @@
 // FP32 tile kernels (v_mfma_f32_16x16x4_f32) whose operands reach LDS by DMA
-// (global_load_lds_dwordx4), for row-major a and b: 256x256 (4 waves of
-// 128x128, one workgroup per CU) and 64x256 / 256x64 / 128x128 (4 waves of
-// 64x64, two workgroups per CU), whole-k or split-k.  Device code only;
-// kernels_dma32.hip instantiates them (plain and grouped).
+// (global_load_lds_dwordx4): 256x256 (4 waves of 128x128, one workgroup per
+// CU), 64x256 / 256x64 / 128x128 (4 waves of 64x64, two workgroups per CU),
+// 64x128 / 128x64 (waves of 32x64) and 64x64 (waves of 16x64), whole-k or
+// split-k.  Row-major a and b on every tile; a column-major b (TB) and a
+// column-major a (TA) on the tiles their kernels instantiate.  Device code
+// only; kernels_dma32.hip (row-major, plain and grouped),
+// kernels_dma32_tb.hip and kernels_dma32_ta.hip instantiate them.
 //
 // d = alpha * (a @ b) + beta * c (the reference's formula,
 // src/primitive/hygon/gemm/fp32_gemm.hip:18-31: the beta term dropped for a
