@@ -40,7 +40,7 @@
 //     with X, and stage st + 1 has landed in Y;
 //   half 2: MFMAs on k 32..63 while reading k 0..31 of Y and issuing the
 //     DMA of stage st + 2 into X.
-// A DMA has one stage of MFMAs (2048 MFMA cycles per wave) to land.  The
+// A DMA has one stage of MFMAs (2048 MFMA cycles per wave at T = 256) to land.  The
 // DMA is issued from inline assembly with M0 set in the same statement, so
 // the compiler's wait-count bookkeeping never sees it: every wait on it is
 // the explicit vmcnt in this file.  The compiler does not otherwise use M0
