@@ -23,42 +23,44 @@ constexpr SplitKind N = SplitKind::kNone, P = SplitKind::kPartial, F = SplitKind
 constexpr FTrainNumericType FP32 = FTRAIN_NUMERIC_TYPE_FP32, BF16 = FTRAIN_NUMERIC_TYPE_BF16,
                             FP16 = FTRAIN_NUMERIC_TYPE_FP16;
 constexpr VariantInfo kInfo[] = {
-    {"Fp32Mfma16Gemm_256x256_Dma", 256, 256, 32, 256, 1, true, N, false, false, false, 0.931, FP32, 256.0, 0.931},
-    {"Fp32Mfma16Gemm_256x256_Dma_SplitK", 256, 256, 32, 256, 1, true, P, false, false, false, 0.954, FP32, 256.0, 0.954},
-    {"Fp32Mfma16Gemm_128x128_Dma", 128, 128, 32, 256, 2, true, N, false, false, false, 0.952, FP32, 256.0, 0.971},
-    {"Fp32Mfma16Gemm_128x128_Dma_SplitK", 128, 128, 32, 256, 2, true, P, false, false, false, 0.971, FP32, 256.0, 0.958},
-    {"Fp32Mfma16Gemm_64x256_Dma_SplitK", 64, 256, 32, 256, 2, true, P, false, false, false, 0.956, FP32, 256.0, 0.910},
-    {"Fp32Mfma16Gemm_256x64_Dma_SplitK", 256, 64, 32, 256, 2, true, P, false, false, false, 0.985, FP32, 256.0, 0.886},
-    {"Fp32Mfma16Gemm_64x128_Dma_SplitK", 64, 128, 32, 256, 3, true, P, false, false, false, 0.962, FP32, 256.0, 0.964},
-    {"Fp32Mfma16Gemm_128x64_Dma_SplitK", 128, 64, 32, 256, 3, true, P, false, false, false, 0.985, FP32, 256.0, 0.920},
-    {"Fp32Mfma16Gemm_64x64_Dma_SplitK", 64, 64, 32, 256, 5, true, P, false, false, false, 0.956, FP32, 256.0, 0.859},
-    {"Fp32Mfma16Gemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, true, 0.897, FP32, 256.0, 0.897},
-    {"Fp32Mfma16Gemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, true, 0.836, FP32, 256.0, 0.836},
-    {"Fp32Mfma16Gemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, true, 0.887, FP32, 256.0, 0.816},
-    {"Fp32Mfma16Gemm_256x128_SplitK", 256, 128, 16, 256, 2, true, P, false, false, true, 0.902, FP32, 256.0, 0.845},
-    {"Fp32Mfma16Gemm_128x256", 128, 256, 16, 256, 2, true, N, false, false, true, 0.886, FP32, 256.0, 0.815},
-    {"Fp32Mfma16Gemm_64x256", 64, 256, 16, 256, 2, true, N, false, false, true, 0.859, FP32, 256.0, 0.791},
-    {"Fp32Mfma16Gemm_64x256_SplitK", 64, 256, 16, 256, 2, true, P, false, false, true, 0.824, FP32, 256.0, 0.812},
-    {"Fp32Mfma16Gemm_256x64", 256, 64, 16, 256, 2, true, N, false, false, true, 0.867, FP32, 256.0, 0.777},
-    {"Fp32Mfma16Gemm_256x64_SplitK", 256, 64, 16, 256, 2, true, P, false, false, true, 0.854, FP32, 256.0, 0.726},
-    {"Fp32MfmaGemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, false, 0.849, FP32, 256.0, 0.849},
-    {"Fp32MfmaGemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, false, 0.843, FP32, 256.0, 0.843},
-    {"Fp32MfmaGemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, false, 0.850, FP32, 256.0, 0.788},
-    {"Fp32MfmaGemm_128x128", 128, 128, 16, 256, 3, true, N, false, false, true, 0.871, FP32, 256.0, 0.747},
-    {"Fp32MfmaGemm_128x128_SplitK", 128, 128, 16, 256, 3, true, P, false, false, true, 0.884, FP32, 256.0, 0.791},
-    {"Fp32MfmaGemm_64x256", 64, 256, 16, 256, 2, true, N, false, false, false, 0.787, FP32, 256.0, 0.640},
-    {"Fp32MfmaGemm_64x256_SplitK", 64, 256, 16, 256, 2, true, P, false, false, false, 0.790, FP32, 256.0, 0.722},
-    {"Fp32MfmaGemm_256x64", 256, 64, 16, 256, 2, true, N, false, false, false, 0.817, FP32, 256.0, 0.733},
-    {"Fp32MfmaGemm_256x64_SplitK", 256, 64, 16, 256, 2, true, P, false, false, false, 0.789, FP32, 256.0, 0.727},
-    {"Fp32MfmaGemm_64x64", 64, 64, 16, 256, 4, true, N, false, false, true, 0.732, FP32, 256.0, 0.612},
-    {"Fp32MfmaGemm_64x64_SplitK", 64, 64, 16, 256, 4, true, P, false, false, true, 0.711, FP32, 256.0, 0.605},
+    {"Fp32Mfma16Gemm_256x256_Dma", 256, 256, 32, 256, 1, true, N, false, false, false, 0.965, FP32, 256.0, 0.965},
+    {"Fp32Mfma16Gemm_256x256_Dma_SplitK", 256, 256, 32, 256, 1, true, P, false, false, false, 0.957, FP32, 256.0, 0.957},
+    {"Fp32Mfma16Gemm_128x128_Dma", 128, 128, 32, 256, 2, true, N, false, false, false, 0.982, FP32, 256.0, 0.928},
+    {"Fp32Mfma16Gemm_128x128_Dma_SplitK", 128, 128, 32, 256, 2, true, P, false, false, false, 0.990, FP32, 256.0, 0.957},
+    {"Fp32Mfma16Gemm_64x256_Dma_SplitK", 64, 256, 32, 256, 2, true, P, false, false, false, 0.958, FP32, 256.0, 0.915},
+    {"Fp32Mfma16Gemm_256x64_Dma_SplitK", 256, 64, 32, 256, 2, true, P, false, false, false, 0.984, FP32, 256.0, 0.966},
+    {"Fp32Mfma16Gemm_64x128_Dma_SplitK", 64, 128, 32, 256, 3, true, P, false, false, false, 0.977, FP32, 256.0, 0.893},
+    {"Fp32Mfma16Gemm_128x64_Dma_SplitK", 128, 64, 32, 256, 3, true, P, false, false, false, 0.939, FP32, 256.0, 0.957},
+    {"Fp32Mfma16Gemm_64x64_Dma_SplitK", 64, 64, 32, 256, 5, true, P, false, false, false, 0.964, FP32, 256.0, 0.907},
+    {"Fp32Mfma16Gemm_64x128_Dma", 64, 128, 32, 256, 3, true, N, false, false, false, 0.966, FP32, 256.0, 0.933},
+    {"Fp32Mfma16Gemm_128x64_Dma", 128, 64, 32, 256, 3, true, N, false, false, false, 0.965, FP32, 256.0, 0.958},
+    {"Fp32Mfma16Gemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, true, 0.903, FP32, 256.0, 0.903},
+    {"Fp32Mfma16Gemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, true, 0.842, FP32, 256.0, 0.842},
+    {"Fp32Mfma16Gemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, true, 0.891, FP32, 256.0, 0.821},
+    {"Fp32Mfma16Gemm_256x128_SplitK", 256, 128, 16, 256, 2, true, P, false, false, true, 0.905, FP32, 256.0, 0.836},
+    {"Fp32Mfma16Gemm_128x256", 128, 256, 16, 256, 2, true, N, false, false, true, 0.892, FP32, 256.0, 0.819},
+    {"Fp32Mfma16Gemm_64x256", 64, 256, 16, 256, 2, true, N, false, false, true, 0.861, FP32, 256.0, 0.789},
+    {"Fp32Mfma16Gemm_64x256_SplitK", 64, 256, 16, 256, 2, true, P, false, false, true, 0.829, FP32, 256.0, 0.810},
+    {"Fp32Mfma16Gemm_256x64", 256, 64, 16, 256, 2, true, N, false, false, true, 0.869, FP32, 256.0, 0.776},
+    {"Fp32Mfma16Gemm_256x64_SplitK", 256, 64, 16, 256, 2, true, P, false, false, true, 0.854, FP32, 256.0, 0.747},
+    {"Fp32MfmaGemm_256x256", 256, 256, 16, 256, 1, true, N, false, false, false, 0.853, FP32, 256.0, 0.853},
+    {"Fp32MfmaGemm_256x256_SplitK", 256, 256, 16, 256, 1, true, P, false, false, false, 0.848, FP32, 256.0, 0.848},
+    {"Fp32MfmaGemm_256x128", 256, 128, 16, 256, 2, true, N, false, false, false, 0.854, FP32, 256.0, 0.791},
+    {"Fp32MfmaGemm_128x128", 128, 128, 16, 256, 3, true, N, false, false, true, 0.867, FP32, 256.0, 0.749},
+    {"Fp32MfmaGemm_128x128_SplitK", 128, 128, 16, 256, 3, true, P, false, false, true, 0.888, FP32, 256.0, 0.792},
+    {"Fp32MfmaGemm_64x256", 64, 256, 16, 256, 2, true, N, false, false, false, 0.791, FP32, 256.0, 0.640},
+    {"Fp32MfmaGemm_64x256_SplitK", 64, 256, 16, 256, 2, true, P, false, false, false, 0.782, FP32, 256.0, 0.687},
+    {"Fp32MfmaGemm_256x64", 256, 64, 16, 256, 2, true, N, false, false, false, 0.812, FP32, 256.0, 0.735},
+    {"Fp32MfmaGemm_256x64_SplitK", 256, 64, 16, 256, 2, true, P, false, false, false, 0.787, FP32, 256.0, 0.720},
+    {"Fp32MfmaGemm_64x64", 64, 64, 16, 256, 4, true, N, false, false, true, 0.720, FP32, 256.0, 0.571},
+    {"Fp32MfmaGemm_64x64_SplitK", 64, 64, 16, 256, 4, true, P, false, false, true, 0.704, FP32, 256.0, 0.632},
     {"Fp32MfmaGemm_128x128_Unaligned", 128, 128, 16, 256, 2, false, N, false, false, true, 0.654, FP32, 256.0, 0.658},
-    {"Fp32MfmaGemm_128x128_Unaligned_SplitK", 128, 128, 16, 256, 2, false, P, false, false, true, 0.696, FP32, 256.0, 0.651},
+    {"Fp32MfmaGemm_128x128_Unaligned_SplitK", 128, 128, 16, 256, 2, false, P, false, false, true, 0.683, FP32, 256.0, 0.590},
     {"Fp32MfmaGemm_64x64_Unaligned", 64, 64, 16, 256, 4, false, N, false, false, true, 0.678, FP32, 256.0, 0.469},
     {"Fp32Gemv", kGemvRows, kGemvPassCols, 1, 1024, 1, true, N, true, false, false, 0, FP32, 256.0, 0},
     {"Fp32Gemv_SplitK", kGemvRows, kGemvCols, 1, 256, 8, true, P, true, false, false, 0, FP32, 256.0, 0},
     {"Fp32Gemv_Unaligned_SplitK", kGemvRows, kGemvCols, 1, 256, 8, false, P, true, false, false, 0, FP32, 256.0, 0},
-    {"Fp32Mfma16Gemm_64x64_DeepK", 64, 64, 32, 256, 1, true, F, false, false, false, 0.592, FP32, 256.0, 0.592},
+    {"Fp32Mfma16Gemm_64x64_DeepK", 64, 64, 32, 256, 1, true, F, false, false, false, 0.698, FP32, 256.0, 0.698},
     {"Fp32Gemm", 64, 64, 16, 256, 2, false, N, false, true, true, 0.2, FP32, 256.0, 0.2},
     {"Bf16MfmaGemm_256x256", 256, 256, 64, 512, 1, true, N, false, false, true, 0.6, BF16, 4096.0, 0.6},
     {"Bf16MfmaGemm_128x128", 128, 128, 64, 256, 2, true, N, false, false, true, 0.4, BF16, 4096.0, 0.4},

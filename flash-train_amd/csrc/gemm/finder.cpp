@@ -34,10 +34,10 @@ namespace gemm {
 namespace {
 constexpr double kClockPerMicro = 2.4e3;  // peak engine clock (MHz)
 constexpr double kHbmBytesPerMicro = 8.0e6 * 0.8;  // sustained HBM bytes per microsecond
-constexpr double kLaunchMicros = 1.16;
-constexpr double kPoolMicros      = 1.40;  // dependency gap before the reduction kernel (fitted)
+constexpr double kLaunchMicros = 1.23;
+constexpr double kPoolMicros      = 3.48;  // dependency gap before the reduction kernel (fitted)
 // The reduction kernel's pass over the partial tiles, relative to HBM time (fitted).
-constexpr double kReduceFactor    = 1.321;
+constexpr double kReduceFactor    = 1.206;
 // The deep-k kernel (SplitKind::kFused): ramp of its single round, and the
 // tile's last workgroup storing, counting and gathering the partial tiles
 // (measured on MI355X: 3.7 us at 4 splits, 11-12 us at 16; the per-split
@@ -50,7 +50,7 @@ constexpr double kFusedPerSplitMicros = 0.9;
 constexpr double kFusedStoreMicros    = 2.0;  // per round: a split workgroup's partial store and count
 // Fixed cost per round of resident workgroups (operand prologue, epilogue
 // stores, the ramp of the first stages); fitted with the catalog efficiencies.
-constexpr double kRoundMicros     = 5.24;
+constexpr double kRoundMicros     = 3.35;
 constexpr uint64_t kMinSplitDepth = 256;  // reduction depth worth one split-k workgroup
 constexpr uint64_t kMinGemvDepth  = 64;
 

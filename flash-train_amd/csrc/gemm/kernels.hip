@@ -422,7 +422,7 @@ const void* kernelFor(Variant v, bool ta, bool tb) {
             {halfKernelFp16NN, halfKernelFp16TN, halfKernelFp16NT, halfKernelFp16TT}};
         return table[i / kHalfTiles][(ta ? 1 : 0) + (tb ? 2 : 0)](tile);
     }
-    if (v >= Variant::kMfma16Dma256x256 && v <= Variant::kMfma16Dma64x64S) return ta ? dma32KernelTA(v, tb) : tb ? dma32KernelTB(v) : dma32Kernel(v);
+    if (v >= Variant::kMfma16Dma256x256 && v <= Variant::kMfma16Dma128x64) return ta ? dma32KernelTA(v, tb) : tb ? dma32KernelTB(v) : dma32Kernel(v);
     if (v == Variant::kBf16MfmaDma256x256) return dmaKernelBf16(ta, tb);
     if (v == Variant::kFp16MfmaDma256x256) return dmaKernelFp16(ta, tb);
     if (v == Variant::kBf16MfmaDma128x128 || v == Variant::kBf16MfmaDma128x128S)

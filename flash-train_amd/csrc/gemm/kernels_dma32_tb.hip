@@ -13,6 +13,8 @@ const void* dma32KernelTB(Variant v) {
         case Variant::kMfma16Dma64x128S: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<64, 128, 2, 2, 2, true, true>);
         case Variant::kMfma16Dma128x64S: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<128, 64, 4, 1, 2, true, true>);
         case Variant::kMfma16Dma64x64S: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<64, 64, 4, 1, 2, true, true>);
+        case Variant::kMfma16Dma64x128: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<64, 128, 2, 2, 2, false, true>);
+        case Variant::kMfma16Dma128x64: return reinterpret_cast<const void*>(&d32::fp32_gemm_dma<128, 64, 4, 1, 2, false, true>);
         default: return nullptr;
     }
 }

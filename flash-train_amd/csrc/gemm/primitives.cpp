@@ -165,7 +165,7 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
                 if (!vecAligned(p.port(i).memory()))
                     return Result(FTRAIN_STATUS_UNSUPPORTED, "a matrix address is not 16-byte aligned");
         }
-        if (v_ >= Variant::kMfma16Dma256x256 && v_ <= Variant::kMfma16Dma64x64S &&
+        if (v_ >= Variant::kMfma16Dma256x256 && v_ <= Variant::kMfma16Dma128x64 &&
             (s.k == 0 || s.k % 32 != 0 || g.lda >= (int64_t(1) << 22) || g.ldb >= (int64_t(1) << 22) ||
              g.ldc >= (int64_t(1) << 21) || g.ldd >= (int64_t(1) << 21)))
             return Result(FTRAIN_STATUS_UNSUPPORTED,

@@ -135,6 +135,8 @@ enum class Variant : int {
     kMfma16Dma64x128S,
     kMfma16Dma128x64S,
     kMfma16Dma64x64S,
+    kMfma16Dma64x128,
+    kMfma16Dma128x64,
     kMfma16_256x256,
     kMfma16_256x256S,
     // Same instruction, 256x128 tiles of 4 waves of 128x64, two workgroups

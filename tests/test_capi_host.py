@@ -601,8 +601,10 @@ def test_finder_choices_for_the_baseline_configs(tlib):
     # leave a ragged last round), the 32x32 128x128 tile 3375.
     assert rank(tlib, 6144, 6144, 6144)[0] == "Fp32Mfma16Gemm_128x128_Dma"
     assert rank(tlib, 4096, 4096, 4096, with_c=True)[0].startswith("Fp32Mfma16Gemm_")
-    # 2048^3: DMA 128x128 126.1, its split-k form 127.1, the register-staged 256x64 139.1.
-    assert rank(tlib, 2048, 2048, 2048)[0] in ("Fp32Mfma16Gemm_128x128_Dma", "Fp32Mfma16Gemm_128x128_Dma_SplitK")
+    # 2048^3: DMA 128x64 117.4, 64x128 117.6, 128x128 122.0, its split-k form 127.1, the
+    # register-staged 256x64 139.1.
+    assert rank(tlib, 2048, 2048, 2048)[0] in ("Fp32Mfma16Gemm_128x64_Dma", "Fp32Mfma16Gemm_64x128_Dma",
+                                               "Fp32Mfma16Gemm_128x128_Dma")
     # 1024^3: DMA 64x128 split-k 25.7, the deep-k tile unsplit 26.7, DMA 128x64 split-k 27.9.
     assert rank(tlib, 1024, 1024, 1024)[0] in ("Fp32Mfma16Gemm_64x64_DeepK", "Fp32Mfma16Gemm_64x128_Dma_SplitK",
                                                "Fp32Mfma16Gemm_64x64_Dma_SplitK")

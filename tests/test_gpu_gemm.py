@@ -649,8 +649,8 @@ def test_fp32_dma_whole_k_tiles_every_output(capi, ops, oracle, m, n, k, ta, tb)
     """The whole-k DMA tiles over many rounds of workgroups, every output checked, five runs:
     a store whose data registers were overwritten right after it (a hardware hazard the
     compiler does not cover for buffer stores) showed only under such load, as a few stray
-    dwords per launch.  ta / tb: a / b column-major (storage k x m / n x k), the 128x128 tile
-    (1000 x 1500 has edge tiles in m and n)."""
+    dwords per launch.  ta / tb: a / b column-major (storage k x m / n x k), on the tiles that
+    take them (1000 x 1500 has edge tiles in m and n)."""
     g = torch.Generator().manual_seed(m + n + k)
     a_h, b_h, c_h = torch.randn(m, k, generator=g), torch.randn(k, n, generator=g), torch.randn(m, n, generator=g)
     ref = oracle.gemm_f64(a_h, b_h, c_h, 1.0, 0.5)
@@ -659,8 +659,8 @@ def test_fp32_dma_whole_k_tiles_every_output(capi, ops, oracle, m, n, k, ta, tb)
     b_d = b_h.t().contiguous().cuda().t() if tb else b_h.cuda()
     plan = capi.plan_for(a_d, b_d, c_h.cuda(), d, 1.0, 0.5, ops)
     s = torch.cuda.current_stream().cuda_stream
-    for name in ("Fp32Mfma16Gemm_128x128_Dma",) if ta or tb else ("Fp32Mfma16Gemm_256x256_Dma",
-                                                                    "Fp32Mfma16Gemm_128x128_Dma"):
+    tiles = ("128x128",) if ta else ("128x128", "64x128", "128x64") if tb else ("256x256", "128x128", "64x128", "128x64")
+    for name in (f"Fp32Mfma16Gemm_{t}_Dma" for t in tiles):
         i = plan.names().index(name)
         for _ in range(5):
             d.fill_(float("nan"))
