@@ -17,7 +17,7 @@ namespace {
 // 1024^3 to 8192^3 in every layout (the 64x64 tile loses to 128x128 from 1024^3 on, 128x128
 // to the 256x256 tiles from 3072^3 on), in grouped MoE shapes with 8 and 64 experts, and in
 // deep-k shapes where split-k wins (384x4096x4096, 512x512x8192, 1536x1536x8192); the 128x128
-// DMA tiles' figures pick the fastest Primitive on 13 of 14 bf16 shapes from 64x4096x4096 to
+// DMA tiles' figures pick the fastest Primitive on each of 14 bf16 shapes from 64x4096x4096 to
 // 16384x14336x4096 (one box).
 constexpr SplitKind N = SplitKind::kNone, P = SplitKind::kPartial, F = SplitKind::kFused;
 constexpr FTrainNumericType FP32 = FTRAIN_NUMERIC_TYPE_FP32, BF16 = FTRAIN_NUMERIC_TYPE_BF16,
