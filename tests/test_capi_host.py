@@ -640,6 +640,19 @@ def test_finder_choices_for_16_bit_skinny_m(tlib):
         assert name not in rank(tlib, 5, 8192, 8192, ab_type=t)
 
 
+def test_finder_choices_for_16_bit_tiles(tlib):
+    # bf16, MI355X, every applicable Primitive timed (us): the Finder's pick was the fastest on each
+    # of these.  Small and mid-size squares: the 128x128 DMA tile (2048^3 25.3 against 256x256 DMA
+    # 39.1); large ones: the 256x256 DMA tile (8192^3 871 against 128x128 DMA 906); deep k: the
+    # 128x128 DMA split-k tile (64x4096x4096 15.1 against the register-staged split-k 20.1,
+    # 256x256x65536 21.2 against 29.3).
+    assert rank(tlib, 2048, 2048, 2048, ab_type=c.BF16)[0] == "Bf16MfmaGemm_128x128_Dma"
+    assert rank(tlib, 8192, 8192, 8192, ab_type=c.BF16)[0] == "Bf16MfmaGemm_256x256_Dma"
+    assert rank(tlib, 16384, 14336, 4096, ab_type=c.BF16)[0] == "Bf16MfmaGemm_256x256_Dma"
+    for shape in ((64, 4096, 4096), (256, 256, 65536), (384, 4096, 4096), (1536, 1536, 8192)):
+        assert rank(tlib, *shape, ab_type=c.BF16)[0] == "Bf16MfmaGemm_128x128_Dma_SplitK", shape
+
+
 def test_finder_respects_alignment_and_row_limits(tlib):
     names = rank(tlib, 512, 512, 512, addr=FAKE + 4)
     assert names and all(("Unaligned" in n) or n == "Fp32Gemm" for n in names)
