@@ -314,7 +314,8 @@ const void* groupedHalfKernelFp16TN(int which);
 const void* groupedHalfKernelFp16NT(int which);
 const void* groupedHalfKernelFp16TT(int which);
 // Split-k reduction (ReduceParams); wide: one thread per output unit (outputs
-// with at least kWideReduceUnits units), else 16 threads per unit.
+// with at least kWideReduceUnits units, or at most 8 splits), else 16 threads
+// per unit.
 const void* reduceKernel(bool vec, bool wide);
 constexpr uint64_t kWideReduceUnits = 256 * 1024;
 const void* deepkKernel();              // kDeepK64x64 (DeepKParams)
