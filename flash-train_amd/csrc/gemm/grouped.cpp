@@ -282,6 +282,7 @@ struct GroupedVariant {
 constexpr GroupedVariant kGroupedVariants[] = {
     {"GroupedFp32Mfma16Gemm_256x256_Dma", FTRAIN_NUMERIC_TYPE_FP32, 4, gemm::Variant::kMfma16Dma256x256},
     {"GroupedFp32Mfma16Gemm_128x128_Dma", FTRAIN_NUMERIC_TYPE_FP32, 5, gemm::Variant::kMfma16Dma128x128},
+    {"GroupedFp32Mfma16Gemm_64x128_Dma", FTRAIN_NUMERIC_TYPE_FP32, 6, gemm::Variant::kMfma16Dma64x128},
     {"GroupedFp32Mfma16Gemm_256x128", FTRAIN_NUMERIC_TYPE_FP32, 2, gemm::Variant::kMfma16_256x128},
     {"GroupedFp32Mfma16Gemm_128x256", FTRAIN_NUMERIC_TYPE_FP32, 3, gemm::Variant::kMfma16_128x256},
     {"GroupedFp32MfmaGemm_128x128", FTRAIN_NUMERIC_TYPE_FP32, 0, gemm::Variant::kMfma128x128},
@@ -372,7 +373,9 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
                 return Result(FTRAIN_STATUS_UNSUPPORTED,
                               "a group is not row-major a and b with k a positive multiple of 32 and leading dimensions "
                               "that fit 32-bit offsets (fp32 DMA tiles)");
-            if (v_->tile == gemm::Variant::kMfma16Dma128x128 &&
+            if (v_->tile == gemm::Variant::kMfma16Dma64x128 && l.ta)
+                return Result(FTRAIN_STATUS_UNSUPPORTED, "a group's a is column-major (the 64x128 DMA tile takes row-major a)");
+            if ((v_->tile == gemm::Variant::kMfma16Dma128x128 || v_->tile == gemm::Variant::kMfma16Dma64x128) &&
                 (l.shape.k == 0 || l.shape.k % 32 != 0 || l.lda >= (int64_t(1) << 22) || l.ldb >= (int64_t(1) << 22) ||
                  l.ldc >= (int64_t(1) << 21) || l.ldd >= (int64_t(1) << 21)))
                 return Result(FTRAIN_STATUS_UNSUPPORTED,

@@ -466,6 +466,7 @@ const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool t
     if (t != 0 && which == 4) return t == 1 ? groupedDma128KernelBf16(ta, tb) : groupedDma128KernelFp16(ta, tb);
     if (t == 0 && which == 4) return ta || tb ? nullptr : groupedDma32Kernel();
     if (t == 0 && which == 5) return groupedDma32Kernel128(ta, tb);
+    if (t == 0 && which == 6) return ta ? nullptr : groupedDma32Kernel64x128(tb);
     if (t == 0 && (which == 2 || which == 3)) {
         // The fp32 256x128 / 128x256 tiles of the 16x16x4 family (grouped entries 16 and 17).
         static constexpr Fn m16[4] = {mfma16KernelNN, mfma16KernelTN, mfma16KernelNT, mfma16KernelTT};

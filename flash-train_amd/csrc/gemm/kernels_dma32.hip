@@ -24,6 +24,12 @@ const void* groupedDma32Kernel() {
     return reinterpret_cast<const void*>(&d32::grouped_fp32_gemm_dma<256, 256, 2, 2, 1, false, false>);
 }
 
+const void* groupedDma32Kernel64x128(bool tb) {
+    using namespace d32;
+    return tb ? reinterpret_cast<const void*>(&grouped_fp32_gemm_dma<64, 128, 2, 2, 2, true, false>)
+              : reinterpret_cast<const void*>(&grouped_fp32_gemm_dma<64, 128, 2, 2, 2, false, false>);
+}
+
 const void* groupedDma32Kernel128(bool ta, bool tb) {
     using namespace d32;
     if (ta) return tb ? reinterpret_cast<const void*>(&grouped_fp32_gemm_dma<128, 128, 2, 2, 2, true, true>)

@@ -285,6 +285,7 @@ const void* halfKernelFp16TT(int tile);
 const void* dma32Kernel(Variant v);
 const void* groupedDma32Kernel();
 const void* groupedDma32Kernel128(bool ta, bool tb);  // grouped 128x128 DMA tile, any orientation
+const void* groupedDma32Kernel64x128(bool tb);        // grouped 64x128 DMA tile, row-major a
 const void* dma32KernelTB(Variant v);  // column-major b
 const void* dma32KernelTA(Variant v, bool tb);  // column-major a
 const void* dmaKernelBf16(bool ta, bool tb);

@@ -59,7 +59,8 @@ def test_every_grouped_kind_gets_an_ops(tlib):
         ops.close()
 
 
-FP32_GROUPED = ["GroupedFp32Mfma16Gemm_256x256_Dma", "GroupedFp32Mfma16Gemm_128x128_Dma", "GroupedFp32Mfma16Gemm_256x128",
+FP32_GROUPED = ["GroupedFp32Mfma16Gemm_256x256_Dma", "GroupedFp32Mfma16Gemm_128x128_Dma", "GroupedFp32Mfma16Gemm_64x128_Dma",
+                "GroupedFp32Mfma16Gemm_256x128",
                 "GroupedFp32Mfma16Gemm_128x256", "GroupedFp32MfmaGemm_128x128", "GroupedFp32MfmaGemm_64x64_Unaligned"]
 
 
@@ -136,8 +137,8 @@ def test_mixed_orientations_are_accepted(tlib):
     # Group 0 row-major, group 1 column-major a: one launch per orientation.
     st, msg, plan = moe_abcd(tlib, [64, 32], a_strides=[(64, 1), (1, 32)])
     assert st == c.SUCCESS, msg
-    # the 256x256 fp32 DMA tile takes row-major a and b only
-    assert sorted(plan.names()) == sorted(FP32_GROUPED[1:])
+    # the 256x256 fp32 DMA tile takes row-major a and b only, the 64x128 one row-major a
+    assert sorted(plan.names()) == sorted(n for n in FP32_GROUPED if n not in FP32_GROUPED[0:3:2])
 
 
 def test_group_count_mismatch_is_invalid(tlib):
@@ -188,7 +189,7 @@ def test_ab_with_c_and_d_lists_and_a_column_major(tlib):
     cl = [D([M, N]) for _ in tokens]
     st, msg, plan = ops.args(a=a, b=b, c=cl, d=cl, alpha=al.view, beta=be.view).plan_status_on_device(0)
     assert st == c.SUCCESS, msg
-    assert sorted(plan.names()) == sorted(FP32_GROUPED[2:])  # k of 40 and 24: no fp32 DMA tile
+    assert sorted(plan.names()) == sorted(FP32_GROUPED[3:])  # k of 40 and 24: no fp32 DMA tile
 
 
 def test_descriptor_values_that_overflow_addresses_are_rejected(tlib):
