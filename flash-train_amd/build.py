@@ -7,7 +7,7 @@ Outputs (all git-ignored, all shipped to the GPU box with the tree):
   flash_train/torch/_flash_train_torch*.so the flash_train.torch.gemm binding
   bench/plan_overhead                     C++ host-overhead probe used by bench.py
 
-Usage: python build.py [--jobs N] [--no-torch]
+Usage: python build.py [--jobs N] [--no-torch] [--incremental]
 """
 
 from __future__ import annotations
@@ -94,9 +94,26 @@ def obj_path(src: str) -> str:
     return os.path.join(BUILD, src.replace("/", "_") + ".o")
 
 
+def up_to_date(out: str) -> bool:
+    """True when `out` and its dependency file exist and no listed dependency is newer."""
+    dep = out + ".d"
+    if not (os.path.exists(out) and os.path.exists(dep)):
+        return False
+    with open(dep) as f:
+        text = f.read().replace("\\\n", " ")
+    deps = text.split(":", 1)[1].split() if ":" in text else []
+    t = os.path.getmtime(out)
+    return all(os.path.exists(x) and os.path.getmtime(x) <= t for x in deps)
+
+
+INCREMENTAL = False
+
+
 def compile_one(src: str) -> str:
     out = obj_path(src)
-    cmd = [HIPCC, *COMMON]
+    if INCREMENTAL and up_to_date(out):
+        return out
+    cmd = [HIPCC, *COMMON, "-MD", "-MF", out + ".d"]
     if src.endswith(".hip"):
         cmd += ["-x", "hip", *DEVICE]
     cmd += ["-c", os.path.join(HERE, src), "-o", out]
@@ -151,7 +168,11 @@ def main(argv: list[str] | None = None) -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
     ap.add_argument("--no-torch", action="store_true")
+    ap.add_argument("--incremental", action="store_true",
+                    help="skip sources whose object is newer than every file it includes")
     args = ap.parse_args(argv)
+    global INCREMENTAL
+    INCREMENTAL = args.incremental
     os.makedirs(BUILD, exist_ok=True)
     with concurrent.futures.ThreadPoolExecutor(args.jobs) as pool:
         lib_objs = list(pool.map(compile_one, LIB_SOURCES))

@@ -7,6 +7,7 @@
 // other exception -> INTERNAL_ERROR) and records the status and message as
 // the thread's last result (reference src/include/flash_train/api.hpp:37-62).
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <exception>
 #include <mutex>
@@ -70,13 +71,78 @@ FTrainStatus setOperation(FTrainArgs args, uint64_t op, OperationKind kind, FTra
     });
 }
 
-// Keeps `plan` alive until the process ends (for Plans a captured graph may
-// replay: its kernels point at the Plan's split-k buffer).
-void retire(FTrainPlan plan) {
-    static std::mutex mutex;
-    static auto* retired = new std::vector<FTrainPlan>();
-    std::lock_guard<std::mutex> lock(mutex);
-    retired->push_back(plan);
+// A convenience Plan shared by its cache entry and by every graph that
+// captured one of its executions (the graph's kernels point at the Plan's
+// split-k buffer).  The last owner to let go destroys the Plan.  A graph lets
+// go through a HIP user object whose destructor HIP runs when the graph and
+// every executable graph made from it are destroyed; that destructor must not
+// call HIP, so it only queues the Plan, and the next convenience call destroys
+// it on an ordinary thread.
+struct SharedPlan {
+    FTrainPlan plan;
+    std::atomic<int> owners{1};
+};
+
+std::mutex& releasedMutex() {
+    static std::mutex m;
+    return m;
+}
+std::vector<FTrainPlan>& releasedPlans() {
+    static auto* v = new std::vector<FTrainPlan>();
+    return *v;
+}
+std::atomic<long>& livePlans() {
+    static std::atomic<long> n{0};
+    return n;
+}
+
+void destroyPlan(FTrainPlan plan) {
+    delete plan;
+    livePlans().fetch_sub(1);
+}
+
+// Destroys the Plans whose last graph has been destroyed.
+void destroyReleasedPlans() {
+    std::vector<FTrainPlan> batch;
+    {
+        std::lock_guard<std::mutex> lock(releasedMutex());
+        if (releasedPlans().empty()) return;
+        batch.swap(releasedPlans());
+    }
+    for (FTrainPlan p : batch) destroyPlan(p);
+}
+
+void dropOwner(SharedPlan* s, bool may_call_hip) {
+    if (s->owners.fetch_sub(1) != 1) return;
+    FTrainPlan plan = s->plan;
+    delete s;
+    if (may_call_hip) {
+        destroyPlan(plan);
+    } else {
+        std::lock_guard<std::mutex> lock(releasedMutex());
+        releasedPlans().push_back(plan);
+    }
+}
+
+void graphReleased(void* shared) { dropOwner(static_cast<SharedPlan*>(shared), false); }
+
+// Makes the graph `stream` is capturing into an owner of `s`.  When HIP
+// cannot attach the user object, the Plan is kept until the process ends
+// instead (the graph may still replay it).
+void ownByCapturingGraph(SharedPlan* s, FTrainStream stream) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    hipGraph_t graph              = nullptr;
+    s->owners.fetch_add(1);
+    if (hipStreamGetCaptureInfo_v2(stream, &status, nullptr, &graph, nullptr, nullptr) == hipSuccess &&
+        status == hipStreamCaptureStatusActive && graph != nullptr) {
+        hipUserObject_t object = nullptr;
+        if (hipUserObjectCreate(&object, s, graphReleased, 1, hipUserObjectNoDestructorSync) == hipSuccess) {
+            if (hipGraphRetainUserObject(graph, object, 1, hipGraphUserObjectMove) == hipSuccess) return;
+            s->owners.fetch_add(1);                 // the graph may replay the Plan: never let go
+            (void)hipUserObjectRelease(object, 1);  // runs graphReleased for the reference just taken
+        }
+    }
+    (void)hipGetLastError();
 }
 
 // Plans created by ftrainGemm, kept per thread and reused when a later call
@@ -84,7 +150,8 @@ void retire(FTrainPlan plan) {
 // strides, types, placement), the same host alpha/beta values, compute type
 // and device.  A Plan binds exactly those values, so reuse is
 // indistinguishable from creating it again.  Least recently used entries are
-// destroyed beyond kCapacity.  Skipped when FTRAIN_DISABLE_CACHE is set.
+// released beyond kCapacity (destroyed, unless a graph still owns them).
+// Skipped when FTRAIN_DISABLE_CACHE is set.
 class ConveniencePlans {
   public:
     static constexpr std::size_t kCapacity = 32;
@@ -137,48 +204,35 @@ class ConveniencePlans {
         return k;
     }
 
-    FTrainPlan find(const std::vector<uint64_t>& key) {
+    SharedPlan* find(const std::vector<uint64_t>& key) {
         for (std::size_t i = 0; i < entries_.size(); ++i) {
             if (entries_[i].key == key) {
                 if (i != 0) std::rotate(entries_.begin(), entries_.begin() + i, entries_.begin() + i + 1);
-                return entries_.front().plan;
+                return entries_.front().shared;
             }
         }
         return nullptr;
     }
 
-    void insert(std::vector<uint64_t> key, FTrainPlan plan) {
-        entries_.insert(entries_.begin(), Entry{std::move(key), plan, false});
+    SharedPlan* insert(std::vector<uint64_t> key, FTrainPlan plan) {
+        auto* shared = new SharedPlan{plan};
+        entries_.insert(entries_.begin(), Entry{std::move(key), shared});
         while (entries_.size() > kCapacity) {
-            drop(entries_.back());
+            dropOwner(entries_.back().shared, true);
             entries_.pop_back();
         }
-    }
-
-    // The most recent entry (the one just found or inserted) was executed
-    // under stream capture: a graph may replay its kernels, which point at
-    // the Plan's split-k buffer, at any later time.
-    void markFrontCaptured() {
-        if (!entries_.empty()) entries_.front().captured = true;
+        return shared;
     }
 
     ~ConveniencePlans() {
-        for (auto& e : entries_) drop(e);
+        for (auto& e : entries_) dropOwner(e.shared, true);
     }
 
   private:
     struct Entry {
         std::vector<uint64_t> key;
-        FTrainPlan plan;
-        bool captured;
+        SharedPlan* shared;
     };
-
-    static void drop(Entry& e) {
-        if (e.captured)
-            retire(e.plan);
-        else
-            delete e.plan;
-    }
 
     std::vector<Entry> entries_;  // most recent first
 };
@@ -202,21 +256,39 @@ FTrainStatus createUnpreparedPlan(FTrainPlan* plan, FTrainArgs args) {
     });
 }
 
-FTrainStatus executeConvenience(FTrainPlan plan, void* workspace, uint64_t workspace_bytes, FTrainStream stream,
-                                const DeviceScratch* scratch) {
-    if (scratch == nullptr) return ftrainPlanExecutePrimitive(plan, 0, workspace, workspace_bytes, stream);
+// Runs a convenience Plan.  With `scratch` set (ftrainGemmNoAlloc) the first
+// Primitive whose split-k partials fit the scratch array runs with the array
+// as its workspace.  Otherwise, with `fit_bytes` nonzero (a Plan made under
+// capture, without a buffer of its own), the first Primitive whose workspace
+// requirement is below `fit_bytes` runs; else Primitive 0.
+FTrainStatus executeConvenience(FTrainPlan plan, uint64_t fit_bytes, void* workspace, uint64_t workspace_bytes,
+                                FTrainStream stream, const DeviceScratch* scratch) {
+    if (scratch == nullptr && fit_bytes == 0)
+        return ftrainPlanExecutePrimitive(plan, 0, workspace, workspace_bytes, stream);
     uint64_t index = 0;
     const FTrainStatus s = guarded([&] {
         const uint64_t n = plan->plan.size();
-        while (index < n && plan->plan.scratchBytes(index) > scratch->bytes) ++index;
-        if (index == n)
-            raise(FTRAIN_STATUS_UNSUPPORTED,
-                  "ftrainGemmNoAlloc: every Primitive of the Plan needs more than the %llu-byte device scratch "
-                  "array (Primitive 0, %s, needs %llu bytes)",
-                  static_cast<unsigned long long>(scratch->bytes), plan->plan.primitiveName(0),
-                  static_cast<unsigned long long>(plan->plan.scratchBytes(0)));
+        if (scratch != nullptr) {
+            while (index < n && plan->plan.scratchBytes(index) > scratch->bytes) ++index;
+            if (index == n)
+                raise(FTRAIN_STATUS_UNSUPPORTED,
+                      "ftrainGemmNoAlloc: every Primitive of the Plan needs more than the %llu-byte device scratch "
+                      "array (Primitive 0, %s, needs %llu bytes)",
+                      static_cast<unsigned long long>(scratch->bytes), plan->plan.primitiveName(0),
+                      static_cast<unsigned long long>(plan->plan.scratchBytes(0)));
+        } else {
+            while (index < n && plan->plan.requiredWorkspaceBytes(index) >= fit_bytes) ++index;
+            if (index == n)
+                raise(FTRAIN_STATUS_UNSUPPORTED,
+                      "ftrainGemm under stream capture: the problem is not in the calling thread's Plan cache and "
+                      "every Primitive needs more than the %llu-byte workspace given (Primitive 0, %s, needs %llu "
+                      "bytes); call ftrainGemm once before the capture, pass a workspace, or use ftrainGemmNoAlloc",
+                      static_cast<unsigned long long>(fit_bytes - 1), plan->plan.primitiveName(0),
+                      static_cast<unsigned long long>(plan->plan.requiredWorkspaceBytes(0)));
+        }
     });
     if (s != FTRAIN_STATUS_SUCCESS) return s;
+    if (scratch == nullptr) return ftrainPlanExecutePrimitive(plan, index, workspace, workspace_bytes, stream);
     // The scratch array's split-k arrival counters are 0 (zero at load, left
     // zero by every launch), so no clearing launch is needed.
     return guarded([&] { plan->plan.execute(index, scratch->memory, scratch->bytes, stream, true); });
@@ -254,40 +326,57 @@ FTrainStatus convenienceGemm(const FTrainStorageView* const views[6], FTrainNume
     }();
     if (entry.status != FTRAIN_STATUS_SUCCESS) return entry.status;
 
-    const bool no_alloc               = scratch != nullptr;
-    const bool cacheable              = !selectionCacheDisabled() && ConveniencePlans::describable(views);
-    int device                        = -1;
+    destroyReleasedPlans();
+    const bool no_alloc  = scratch != nullptr;
+    const bool capturing = streamCapturing(stream);
+    const bool cacheable = !selectionCacheDisabled() && ConveniencePlans::describable(views);
+    int device           = -1;
     std::vector<uint64_t> key;
     if (cacheable && hipGetDevice(&device) == hipSuccess) {
         key = ConveniencePlans::describe(views, compute_type, device, stream);
-        if (FTrainPlan cached = ConveniencePlans::local(no_alloc).find(key)) {
-            if (streamCapturing(stream)) ConveniencePlans::local(no_alloc).markFrontCaptured();
-            return executeConvenience(cached, workspace, workspace_bytes, stream, scratch);
+        if (SharedPlan* cached = ConveniencePlans::local(no_alloc).find(key)) {
+            const FTrainStatus s = executeConvenience(cached->plan, 0, workspace, workspace_bytes, stream, scratch);
+            if (s == FTRAIN_STATUS_SUCCESS && capturing) ownByCapturingGraph(cached, stream);
+            return s;
         }
     } else {
         (void)hipGetLastError();
     }
 
-    FTrainArgs args = nullptr;
-    FTrainPlan plan = nullptr;
-    FTrainStatus s  = ftrainArgsCreate(&args, entry.ops);
+    // Under capture ftrainGemm makes its new Plan without preparation
+    // (Plan::prepare allocates and clears device memory, which a capture
+    // forbids) and runs the first Primitive that needs no more than the
+    // caller's workspace.  That Plan is owned by the graph alone and not
+    // cached: uncaptured calls expect Primitive 0 to run without a workspace.
+    const bool fit_workspace = capturing && !no_alloc;
+    FTrainArgs args          = nullptr;
+    FTrainPlan plan          = nullptr;
+    FTrainStatus s           = ftrainArgsCreate(&args, entry.ops);
     const std::pair<FTrainTensorId, const FTrainStorageView*> ports[] = {
         {entry.a, &a}, {entry.b, &b}, {entry.c, &c}, {entry.d, &d}, {entry.alpha, &alpha}, {entry.beta, &beta}};
     for (const auto& port : ports)
         if (s == FTRAIN_STATUS_SUCCESS) s = ftrainArgsSetTensor(args, port.first, *port.second);
     if (s == FTRAIN_STATUS_SUCCESS) s = ftrainArgsSetGemm(args, entry.gemm, compute_type);
-    if (s == FTRAIN_STATUS_SUCCESS) s = no_alloc ? createUnpreparedPlan(&plan, args) : ftrainPlanCreate(&plan, args);
-    if (s == FTRAIN_STATUS_SUCCESS) s = executeConvenience(plan, workspace, workspace_bytes, stream, scratch);
+    if (s == FTRAIN_STATUS_SUCCESS)
+        s = no_alloc || fit_workspace ? createUnpreparedPlan(&plan, args) : ftrainPlanCreate(&plan, args);
+    if (s == FTRAIN_STATUS_SUCCESS) livePlans().fetch_add(1);
+    if (s == FTRAIN_STATUS_SUCCESS)
+        s = executeConvenience(plan, fit_workspace ? workspace_bytes + 1 : 0, workspace, workspace_bytes, stream,
+                               scratch);
     // Keep the failing step's diagnostic across the clean-up calls.
     const Result failure = s != FTRAIN_STATUS_SUCCESS ? lastResult() : Result{};
     if (plan != nullptr) {
-        if (s == FTRAIN_STATUS_SUCCESS && !key.empty()) {
-            ConveniencePlans::local(no_alloc).insert(std::move(key), plan);  // the cache now owns it
-            if (streamCapturing(stream)) ConveniencePlans::local(no_alloc).markFrontCaptured();
-        } else if (s == FTRAIN_STATUS_SUCCESS && streamCapturing(stream)) {
-            retire(plan);
+        if (s != FTRAIN_STATUS_SUCCESS) {
+            destroyPlan(plan);
+        } else if (!key.empty() && !fit_workspace) {
+            SharedPlan* shared = ConveniencePlans::local(no_alloc).insert(std::move(key), plan);  // the cache owns it
+            if (capturing) ownByCapturingGraph(shared, stream);
+        } else if (capturing) {
+            auto* shared = new SharedPlan{plan};
+            ownByCapturingGraph(shared, stream);
+            dropOwner(shared, true);  // the graph is now its only owner
         } else {
-            ftrainPlanDestroy(plan);
+            destroyPlan(plan);
         }
     }
     if (args != nullptr) ftrainArgsDestroy(args);
@@ -296,6 +385,12 @@ FTrainStatus convenienceGemm(const FTrainStorageView* const views[6], FTrainNume
 }
 
 }  // namespace
+
+long conveniencePlansAlive() {
+    destroyReleasedPlans();
+    return livePlans().load();
+}
+
 }  // namespace ftrain
 
 using namespace ftrain;

@@ -75,6 +75,9 @@ FTRAIN_TESTING_API uint32_t ftrainTestingChooseSplits(int v, uint64_t m, uint64_
 
 FTRAIN_TESTING_API void ftrainTestingForceSplits(uint32_t s) { gemm::forceSplits(s); }
 
+// Convenience Plans still alive (cached per thread or owned by captured graphs).
+FTRAIN_TESTING_API long ftrainTestingConveniencePlansAlive(void) { return conveniencePlansAlive(); }
+
 // ---- selection cache ----
 
 FTRAIN_TESTING_API void* ftrainTestingCacheCreate(uint64_t max_entries, uint64_t shards) {

@@ -26,6 +26,11 @@ namespace ftrain {
 // The calling thread's last result (shared by the C API and test hooks).
 Result& lastResult() noexcept;
 
+// Plans made by ftrainGemm / ftrainGemmNoAlloc that are still alive (held by
+// a thread's convenience cache or by a graph that captured them), after
+// destroying those whose last graph is gone.
+long conveniencePlansAlive();
+
 // Runs `body` at the C boundary: success clears the thread's last result;
 // Failure -> its own status and message, std::bad_alloc -> OUT_OF_MEMORY,
 // any other exception -> INTERNAL_ERROR.  Never throws.

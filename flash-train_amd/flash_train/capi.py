@@ -123,6 +123,7 @@ def _declare_testing(lib: ctypes.CDLL) -> ctypes.CDLL:
         "ftrainTestingEstimateMicros": (c_double, [c_int, c_uint64, c_uint64, c_uint64, c_bool, c_int]),
         "ftrainTestingChooseSplits": (c_uint32, [c_int, c_uint64, c_uint64, c_uint64, c_int]),
         "ftrainTestingForceSplits": (None, [c_uint32]),
+        "ftrainTestingConveniencePlansAlive": (ctypes.c_long, []),
         "ftrainTestingCacheCreate": (c_void_p, [c_uint64, c_uint64]),
         "ftrainTestingCacheDestroy": (None, [c_void_p]),
         "ftrainTestingCachePublish": (st, [c_void_p, POINTER(c_uint64), c_size_t, POINTER(c_uint64), c_size_t,

@@ -160,3 +160,89 @@ def test_convenience_graph_survives_plan_cache_eviction(capi, oracle):
         rep_ = oracle.tolerance_check(d.cpu().numpy(), ref, k)
         assert rep_["ok"], (rep, rep_)
     del junk
+
+
+def test_captured_convenience_plan_lives_exactly_as_long_as_its_graph(capi, oracle):
+    """A Plan that ftrainGemm ran under capture is owned by the capturing
+    graph (a HIP user object) as well as by the thread's Plan cache.  Evicted
+    from the cache, it stays alive while the graph exists -- the replays after
+    the eviction are checked against the oracle -- and is destroyed once the
+    graph is.  Counted through the testing library's hook, so every call here
+    goes through that library."""
+    import gc
+
+    t = capi.testing_lib()
+    m, n, k = 64, 4096, 4096
+    a, b = rnd((m, k), 51).cuda(), rnd((k, n), 52).cuda()
+    d = torch.empty(m, n, device="cuda")
+    al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+    views = (capi.matrix(a), capi.matrix(b), capi.matrix(None, [m, n]), capi.matrix(d), al.view, be.view)
+    side = torch.cuda.Stream()
+    assert capi.gemm_status(*views, stream=side.cuda_stream, l=t) == capi.SUCCESS, capi.last_message(t)
+    side.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        assert capi.gemm_status(*views, stream=side.cuda_stream, l=t) == capi.SUCCESS
+    others = []
+    for i in range(40):
+        mm = 8 + i
+        x, y, z = torch.ones(mm, 32, device="cuda"), torch.ones(32, 16, device="cuda"), torch.empty(mm, 16, device="cuda")
+        others.append((x, y, z))
+        v = (capi.matrix(x), capi.matrix(y), capi.matrix(None, [mm, 16]), capi.matrix(z), al.view, be.view)
+        assert capi.gemm_status(*v, stream=side.cuda_stream, l=t) == capi.SUCCESS
+    side.synchronize()
+    alive_with_graph = t.ftrainTestingConveniencePlansAlive()
+    assert alive_with_graph >= 33, alive_with_graph  # 32 cached + the evicted, captured one
+    junk = [torch.full((1 << 20,), 7.0, device="cuda") for _ in range(8)]
+    for rep in range(3):
+        a.copy_(rnd((m, k), 60 + rep).cuda())
+        d.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = oracle.gemm_f64(a.cpu().numpy(), b.cpu().numpy(), None, 1.0, 0.0)
+        rep_ = oracle.tolerance_check(d.cpu().numpy(), ref, k)
+        assert rep_["ok"], (rep, rep_)
+    assert t.ftrainTestingConveniencePlansAlive() == alive_with_graph
+    del graph, junk
+    gc.collect()
+    torch.cuda.synchronize()
+    assert t.ftrainTestingConveniencePlansAlive() == alive_with_graph - 1
+
+
+def test_first_convenience_call_of_a_shape_can_be_captured(capi, oracle):
+    """ftrainGemm on a problem it has never seen, inside a global-mode
+    capture: Plan preparation would allocate, so the Plan is made without it
+    and runs its first Primitive that needs no workspace.  The graph replays
+    correctly after the inputs change, and owning it alone, the Plan goes
+    when the graph goes."""
+    import gc
+
+    t = capi.testing_lib()
+    m, n, k = 64, 2048, 8192  # split-k / deep-k is Primitive 0 of this shape
+    a, b, c = rnd((m, k), 71).cuda(), rnd((k, n), 72).cuda(), rnd((m, n), 73).cuda()
+    d = torch.empty(m, n, device="cuda")
+    plan = capi.plan_for(a, b, c, d, 0.75, 0.5)
+    assert plan.name(0).endswith(("_SplitK", "_DeepK")), plan.names()
+    al, be = capi.HostScalar(0.75), capi.HostScalar(0.5)
+    views = (capi.matrix(a), capi.matrix(b), capi.matrix(c), capi.matrix(d), al.view, be.view)
+    side = torch.cuda.Stream()
+    before = t.ftrainTestingConveniencePlansAlive()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        st = capi.gemm_status(*views, stream=side.cuda_stream, l=t)
+    assert st == capi.SUCCESS, capi.last_message(t)
+    assert t.ftrainTestingConveniencePlansAlive() == before + 1
+    for rep in range(3):
+        a.copy_(rnd((m, k), 80 + rep).cuda())
+        d.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = oracle.gemm_f64(a.cpu().numpy(), b.cpu().numpy(), c.cpu().numpy(), 0.75, 0.5)
+        rep_ = oracle.tolerance_check(d.cpu().numpy(), ref, k)
+        assert rep_["ok"], (rep, rep_)
+    del graph
+    gc.collect()
+    torch.cuda.synchronize()
+    assert t.ftrainTestingConveniencePlansAlive() == before

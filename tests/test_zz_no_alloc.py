@@ -74,8 +74,114 @@ def test_no_alloc_whole_k_and_odd_shapes(capi, oracle):
         assert torch.equal(d_ref, d_new), (names[0], m, n, k)
 
 
-def test_no_alloc_when_partials_exceed_the_scratch(capi, oracle):
-    # 4608 x 4608 fp32 is 81 MiB per partial slice: no split-k Primitive fits
-    # the 64 MiB array, so ftrainGemmNoAlloc runs the best whole-k Primitive
-    # (both results are checked against the oracle in run_both).
-    run_both(capi, oracle, 4608, 4608, 2048, 41, False)
+def test_no_alloc_first_call_allocates_nothing_and_can_be_captured(capi, oracle):
+    """The first ftrainGemmNoAlloc call of a shape creates its Plan: free
+    device memory is the same before and after it (warm-up calls on other
+    shapes have loaded the kernels' code and looked up the scratch array), and
+    the first call of yet another shape can run inside a global-mode capture,
+    whose replays are checked against the oracle after the inputs change."""
+    s = torch.cuda.current_stream().cuda_stream
+    al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+
+    def call(m, n, k, seed, stream=s):
+        a, b = rnd((m, k), seed).cuda(), rnd((k, n), seed + 1).cuda()
+        d = torch.full((m, n), float("nan"), device="cuda")
+        views = (capi.matrix(a), capi.matrix(b), capi.matrix(None, [m, n]), capi.matrix(d), al.view, be.view)
+        return a, b, d, views
+
+    for seed, shape in ((91, (64, 4096, 4096)), (93, (4096, 64, 4096)), (95, (256, 256, 65536))):
+        *_, views = call(*shape, seed)
+        assert capi.gemm_no_alloc_status(*views, stream=s) == capi.SUCCESS, capi.last_message()
+    torch.cuda.synchronize()
+    a, b, d, views = call(64, 3072, 4096, 97)
+    torch.cuda.synchronize()
+    free_before = torch.cuda.mem_get_info()[0]
+    assert capi.gemm_no_alloc_status(*views, stream=s) == capi.SUCCESS, capi.last_message()
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free_before
+    rep = oracle.tolerance_check(d.cpu().numpy(), oracle.gemm_f64(a.cpu().numpy(), b.cpu().numpy(), None, 1.0, 0.0),
+                                 4096)
+    assert rep["ok"], rep
+
+    m, n, k = 64, 2560, 8192
+    side = torch.cuda.Stream()
+    a, b, d, views = call(m, n, k, 99, side.cuda_stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        st = capi.gemm_no_alloc_status(*views, stream=side.cuda_stream)
+    assert st == capi.SUCCESS, capi.last_message()
+    for rep_i in range(3):
+        a.copy_(rnd((m, k), 100 + rep_i).cuda())
+        d.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = oracle.gemm_f64(a.cpu().numpy(), b.cpu().numpy(), None, 1.0, 0.0)
+        rep = oracle.tolerance_check(d.cpu().numpy(), ref, k)
+        assert rep["ok"], (rep_i, rep)
+    del graph
+
+
+# Run in a child process: the Primitive allow-list is read once per process.
+FALLBACK_CHILD = r"""
+import json, sys, torch
+sys.path[:0] = sys.argv[1:3]
+from flash_train import capi
+from oracle import oracle
+m, n, k = 4608, 4608, 2048
+g = torch.Generator().manual_seed(41)
+a, b = torch.randn(m, k, generator=g).cuda(), torch.randn(k, n, generator=g).cuda()
+d_plan = torch.full((m, n), float("nan"), device="cuda")
+d_new = torch.full((m, n), float("nan"), device="cuda")
+plan = capi.plan_for(a, b, None, d_plan, 1.0, 0.0)
+names = plan.names()
+s = torch.cuda.current_stream().cuda_stream
+if len(names) > 1:
+    plan.execute(1, s)
+al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+st = capi.gemm_no_alloc_status(capi.matrix(a), capi.matrix(b), capi.matrix(None, [m, n]), capi.matrix(d_new),
+                               al.view, be.view, stream=s)
+msg = capi.last_message()
+torch.cuda.synchronize()
+out = {"names": names, "status": st, "message": msg}
+if st == capi.SUCCESS:
+    out["equal_to_primitive_1"] = bool(torch.equal(d_plan, d_new))
+    rows = list(range(0, m, 97))
+    ref = oracle.gemm_f64(a.cpu().numpy()[rows], b.cpu().numpy(), None, 1.0, 0.0)
+    out["ok"] = bool(oracle.tolerance_check(d_new.cpu().numpy()[rows], ref, k)["ok"])
+print("RESULT " + json.dumps(out))
+"""
+
+
+def run_fallback_child(enabled):
+    import json
+    import os
+    import subprocess
+    import sys
+
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, FTRAIN_ENABLED_PRIMITIVES=enabled)
+    proc = subprocess.run([sys.executable, "-c", FALLBACK_CHILD, os.path.join(repo, "flash-train_amd"), repo],
+                          env=env, capture_output=True, text=True, timeout=110)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    line = next(x for x in proc.stdout.splitlines() if x.startswith("RESULT "))
+    return json.loads(line[len("RESULT "):])
+
+
+def test_no_alloc_when_partials_exceed_the_scratch():
+    # 4608 x 4608 fp32 is 81 MiB per partial slice, more than the 64 MiB
+    # array.  With a split-k Primitive ranked first (the allow-list keeps it
+    # and the SIMT kernel only), ftrainGemmNoAlloc runs Primitive 1, bit for
+    # bit as the Plan's own Primitive 1 does.
+    out = run_fallback_child("Fp32Mfma16Gemm_128x128_Dma_SplitK,Fp32Gemm")
+    assert out["names"] == ["Fp32Mfma16Gemm_128x128_Dma_SplitK", "Fp32Gemm"], out
+    assert out["status"] == 0, out
+    assert out["equal_to_primitive_1"] and out["ok"], out
+
+
+def test_no_alloc_rejects_a_plan_without_a_fitting_primitive():
+    out = run_fallback_child("Fp32Mfma16Gemm_128x128_Dma_SplitK")
+    assert out["names"] == ["Fp32Mfma16Gemm_128x128_Dma_SplitK"], out
+    assert out["status"] == 4, out  # UNSUPPORTED
+    assert "device scratch array" in out["message"] and "Fp32Mfma16Gemm_128x128_Dma_SplitK" in out["message"], out
