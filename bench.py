@@ -138,17 +138,20 @@ def expert_rows(m: int, experts: int) -> list:
     return rows
 
 
-def run_grouped(args, a_h, b_h, c_h, cfg) -> None:
-    """One step = one GroupedABCDGemm launch sequence over all experts (Primitive 0 of its Plan)."""
+def grouped_core(workload: str, E: int, dtype: str, steps: int, warmup: int) -> dict:
+    """One GroupedABCDGemm Plan (Primitive 0) over E experts: the workload's m rows split unevenly, each
+    expert with its own k x n weight.  Timed with HIP events on the launch stream; 8 sampled rows of every
+    expert checked against fp64."""
     import numpy as np
     import torch
 
     import flash_train.capi as capi
     from oracle import oracle
 
-    m, n, k, E = cfg["m"], cfg["n"], cfg["k"], args.grouped
+    a_h, b_h, c_h, cfg = oracle.seeded_inputs(workload)
+    m, n, k = cfg["m"], cfg["n"], cfg["k"]
     rows = expert_rows(m, E)
-    dt = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[args.dtype]
+    dt = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[dtype]
     # Expert e's weight: the workload's b with its columns rotated by 97·e (distinct memory, same distribution).
     b_all = torch.stack([torch.roll(b_h, 97 * e, dims=1) for e in range(E)]).to(dt)
     a_h = a_h.to(dt)
@@ -165,22 +168,21 @@ def run_grouped(args, a_h, b_h, c_h, cfg) -> None:
     plan = gargs.plan()
     gargs.close()
     name = plan.name(0)
-    log(f"grouped {args.workload} ({m}x{n}x{k}) over {E} experts, rows {rows}; primitive 0 = {name}")
+    log(f"grouped {workload} ({m}x{n}x{k}) over {E} experts, rows {rows}; primitive 0 = {name}")
     stream = torch.cuda.Stream()
     h = stream.cuda_stream
     with torch.cuda.stream(stream):
-        for _ in range(args.warmup):
+        for _ in range(warmup):
             plan.execute(0, h)
         torch.cuda.synchronize()
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
-        for _ in range(args.steps):
+        for _ in range(steps):
             plan.execute(0, h)
         stop.record(stream)
         torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / args.steps
+    ms = start.elapsed_time(stop) / steps
 
-    # Parity spot check: 8 sampled rows of every expert against fp64.
     rng = np.random.default_rng(1)
     ok, worst, row0 = True, 0.0, 0
     for e, r in enumerate(rows):
@@ -189,28 +191,40 @@ def run_grouped(args, a_h, b_h, c_h, cfg) -> None:
         rep = oracle.tolerance_check(d[torch.as_tensor(pick).cuda()].cpu().numpy(), ref, k)
         ok, worst = ok and rep["ok"], max(worst, rep["max_abs_err"] / max(rep["bound"], 1e-30))
         row0 += r
+    del a, b, c, d, plan
+    torch.cuda.empty_cache()
 
-    half = args.dtype != "fp32"
+    half = dtype != "fp32"
     flops = 2.0 * m * n * k
     tflops = flops / (ms * 1e-3) / 1e12
     peak = HALF_MATRIX_PEAK_TFLOPS if half else FP32_MATRIX_PEAK_TFLOPS
     eb = 2.0 if half else 4.0
-    alg_bytes = eb * (m * k + E * k * n) + 4.0 * m * n * (2 if c is not None else 1)
-    workload = f"grouped_{args.workload}_e{E}"
+    alg_bytes = eb * (m * k + E * k * n) + 4.0 * m * n * (2 if c_h is not None else 1)
+    key = f"grouped_{workload}_e{E}"
+    return {"workload": key + ("" if not half else f"_{dtype}"), "m": m, "n": n, "k": k, "experts": E,
+            "rows": rows, "dtype": dtype, "c": c_h is not None, "primitive": name, "steps": steps,
+            "ms": round(ms, 5), "tflops": round(tflops, 3),
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak, "unit": "TFLOP/s",
+                         "frac": round(tflops / peak, 4),
+                         "traffic": traffic_from_profiles(key + ("" if not half else f"_{dtype}_nn")),
+                         "algorithmic_bytes": alg_bytes, "algorithmic_flops": flops},
+            "parity": {"rows_checked": int(sum(min(8, r) for r in rows)), "worst_err_over_bound": worst,
+                       "ok": bool(ok)}}
+
+
+def run_grouped(args) -> None:
+    """--grouped E: one step = one GroupedABCDGemm launch sequence over all experts; prints one JSON line."""
+    g = grouped_core(args.workload, args.grouped, args.dtype, args.steps, args.warmup)
     print(json.dumps({
-        "metric": METRIC, "value": round(tflops, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "metric": METRIC, "value": g["tflops"], "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(g["ms"], 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": args.dtype,
         "data": "synthetic (seeded CPU torch.Generator 2026; expert weights are column rotations of b)",
-        "config": {"workload": workload, "m": m, "n": n, "k": k, "experts": E, "rows": rows,
-                   "c": c is not None, "primitive": name, "parallelism": "single GPU"},
-        "pct_of_matrix_peak": round(100.0 * tflops / peak, 2),
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(tflops / peak, 4),
-                     "traffic": traffic_from_profiles(workload + ("" if args.dtype == "fp32" else f"_{args.dtype}_nn")),
-                     "algorithmic_bytes": alg_bytes, "algorithmic_flops": flops, "kernel_ms": round(ms, 4),
-                     "kernel": name},
-        "parity": {"rows_checked": 8 * E, "worst_err_over_bound": worst, "ok": ok},
+        "config": {"workload": g["workload"], "m": g["m"], "n": g["n"], "k": g["k"], "experts": g["experts"],
+                   "rows": g["rows"], "c": g["c"], "primitive": g["primitive"], "parallelism": "single GPU"},
+        "pct_of_matrix_peak": round(100.0 * g["roofline"]["frac"], 2),
+        "roofline": dict(g["roofline"], kernel_ms=round(g["ms"], 4), kernel=g["primitive"]),
+        "parity": g["parity"],
     }), flush=True)
 
 
@@ -229,7 +243,7 @@ CONFIG_STEPS = {
 }
 
 
-def time_steps(plan, index: int, stream, steps: int, warmup: int, block: int = 10) -> dict:
+def time_steps(plan, index: int, stream, steps: int, warmup: int, block: int = 10, workspace=(0, 0)) -> dict:
     """HIP events on the launch stream around blocks of `block` back-to-back calls: the mean over
     all steps and the median of the block means (ms per call).  An event between every two calls
     adds a marker to the queue that costs about 2-3 us next to a 25 us kernel; the per-call event
@@ -240,20 +254,20 @@ def time_steps(plan, index: int, stream, steps: int, warmup: int, block: int = 1
     blocks = max(1, steps // block)
     with torch.cuda.stream(stream):
         for _ in range(warmup):
-            plan.execute(index, h)
+            plan.execute(index, h, *workspace)
         torch.cuda.synchronize()
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(blocks + 1)]
         ev[0].record(stream)
         for i in range(blocks):
             for _ in range(block):
-                plan.execute(index, h)
+                plan.execute(index, h, *workspace)
             ev[i + 1].record(stream)
         torch.cuda.synchronize()
         per_block = sorted(ev[i].elapsed_time(ev[i + 1]) / block for i in range(blocks))
         one = [torch.cuda.Event(enable_timing=True) for _ in range(block + 1)]
         one[0].record(stream)
         for i in range(block):
-            plan.execute(index, h)
+            plan.execute(index, h, *workspace)
             one[i + 1].record(stream)
         torch.cuda.synchronize()
     per_call = sorted(one[i].elapsed_time(one[i + 1]) for i in range(block))
@@ -261,50 +275,159 @@ def time_steps(plan, index: int, stream, steps: int, warmup: int, block: int = 1
             "event_per_call_median_ms": per_call[block // 2]}
 
 
-def parity_rows(oracle, a_h, b_h, c_h, cfg, d, rows_wanted: int = 64) -> dict:
+def parity_rows(oracle, a_h, b_h, c_h, cfg, d, rows_wanted: int = 64, ref=None) -> tuple:
     """fp64 check of sampled rows (all rows when m is small) against the north-star bar, and how far
-    inside it the result is (a subtle pipeline slip would show as a ratio far above the usual 1e-3)."""
+    inside it the result is (a subtle pipeline slip would show as a ratio far above the usual 1e-3).
+    Returns the report and the (rows, fp64 reference) pair, which later checks of the same inputs reuse."""
     import numpy as np
     import torch
 
     m = cfg["m"]
-    rows = np.arange(m) if m <= rows_wanted else np.sort(np.random.default_rng(1).choice(m, size=rows_wanted, replace=False))
-    ref = oracle.sampled_rows_f64(a_h.float(), b_h.float(), c_h, cfg["alpha"], cfg["beta"], rows)
-    rep = oracle.tolerance_check(d[torch.as_tensor(rows).cuda()].cpu().numpy(), ref, cfg["k"])
+    if ref is None:
+        rows = np.arange(m) if m <= rows_wanted else np.sort(
+            np.random.default_rng(1).choice(m, size=rows_wanted, replace=False))
+        ref = (rows, oracle.sampled_rows_f64(a_h.float(), b_h.float(), c_h, cfg["alpha"], cfg["beta"], rows))
+    rows, want = ref
+    rep = oracle.tolerance_check(d[torch.as_tensor(rows).cuda()].cpu().numpy(), want, cfg["k"])
     ratio = rep["max_abs_err"] / rep["bound"] if rep["bound"] > 0 else 0.0
-    return {"rows_checked": int(len(rows)), "max_abs_err": rep["max_abs_err"], "bound": rep["bound"],
-            "err_over_bound": ratio, "ok": bool(rep["ok"] and ratio <= 1e-2)}
+    return ({"rows_checked": int(len(rows)), "max_abs_err": rep["max_abs_err"], "bound": rep["bound"],
+             "err_over_bound": ratio, "ok": bool(rep["ok"] and ratio <= 1e-2)}, ref)
 
 
-def run_config(name: str, steps: int) -> dict:
-    """One BASELINE config on one cached Plan (Primitive 0): median step time, rate, roofline, parity."""
+# BASELINE configs whose every Primitive is timed as well (the reference harness's L4 tier,
+# benchmarks/csrc/ftrain_bench.cpp:158-166): config 5 ("verifies Finder choice") and 4096³ + c.
+PRIMITIVE_MATRIX = ("square_4096_beta", "skinny_64x4096x4096", "skinny_4096x64x4096", "splitk_256x256x65536",
+                    "gemv_1x8192x8192", "odd_127x97x33")
+
+
+def primitive_matrix(plan, stream, d, check, steps: int, passes: int = 2) -> dict:
+    """Every Primitive of the Plan, timed like Primitive 0 (blocks of 10 back-to-back calls) with one
+    caller workspace as large as the largest requirement, each result checked.  The matrix is walked
+    `passes` times and each Primitive keeps its best median, so a clock still ramping after a pause
+    (the parity check runs on the host) does not count against whichever Primitive comes first.
+    `pick_loss` is how much slower the Finder's pick (Primitive 0) runs than the fastest Primitive."""
+    import torch
+
+    names = plan.names()
+    need = max(plan.workspace_bytes(i) for i in range(len(names)))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+    best_ms = [math.inf] * len(names)
+    ok = [True] * len(names)
+    for _ in range(passes):
+        for i in range(len(names)):
+            d.fill_(float("nan"))
+            t = time_steps(plan, i, stream, steps, warmup=3, workspace=(ws.data_ptr(), ws.numel()))
+            best_ms[i] = min(best_ms[i], t["median_ms"])
+            ok[i] = ok[i] and bool(check()["ok"])
+    rows = [{"index": i, "primitive": nm, "workspace_bytes": plan.workspace_bytes(i),
+             "median_ms": round(best_ms[i], 5), "ok": ok[i]} for i, nm in enumerate(names)]
+    best = min(rows, key=lambda r: r["median_ms"])
+    del ws
+    return {"primitives": rows, "fastest": best["primitive"],
+            "pick_loss": round(rows[0]["median_ms"] / best["median_ms"] - 1.0, 4)}
+
+
+def run_config(name: str, steps: int, dtype: str = "fp32", all_primitives: bool = False) -> dict:
+    """One BASELINE config on one cached Plan (Primitive 0): median step time, rate, roofline, parity;
+    with `all_primitives`, the per-Primitive matrix too."""
     import torch
 
     import flash_train.capi as capi
     from oracle import oracle
 
     a_h, b_h, c_h, cfg = oracle.seeded_inputs(name)
+    half = dtype != "fp32"
+    if half:
+        dt = torch.bfloat16 if dtype == "bf16" else torch.float16
+        a_h, b_h = a_h.to(dt), b_h.to(dt)
     m, n, k = cfg["m"], cfg["n"], cfg["k"]
     a, b = a_h.cuda(), b_h.cuda()
     c = c_h.cuda() if c_h is not None else None
     d = torch.empty(m, n, device="cuda")
     plan = capi.plan_for(a, b, c, d, cfg["alpha"], cfg["beta"])
-    t = time_steps(plan, 0, torch.cuda.Stream(), steps, warmup=max(3, steps // 20))
+    stream = torch.cuda.Stream()
+    t = time_steps(plan, 0, stream, steps, warmup=max(3, steps // 20))
     ms = t["median_ms"]
+    parity, ref = parity_rows(oracle, a_h, b_h, c_h, cfg, d)
     flops = 2.0 * m * n * k
-    alg_bytes = 4.0 * (m * k + k * n + m * n * (2 if c is not None else 1))
+    eb = 2.0 if half else 4.0
+    alg_bytes = eb * (m * k + k * n) + 4.0 * m * n * (2 if c is not None else 1)
+    peak = HALF_MATRIX_PEAK_TFLOPS if half else FP32_MATRIX_PEAK_TFLOPS
     tflops = flops / (ms * 1e-3) / 1e12
     gbs = alg_bytes / (ms * 1e-3) / 1e9
-    hbm_bound = flops / alg_bytes < FP32_MATRIX_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
-    out = {"workload": name, "m": m, "n": n, "k": k, "c": c is not None, "primitive": plan.name(0),
-           "steps": steps, "median_ms": round(ms, 5), "mean_ms": round(t["mean_ms"], 5),
+    hbm_bound = flops / alg_bytes < peak * 1e12 / (HBM_PEAK_GBS * 1e9)
+    key = name if not half else f"{name}_{dtype}"
+    out = {"workload": key, "m": m, "n": n, "k": k, "dtype": dtype, "c": c is not None,
+           "primitive": plan.name(0), "steps": steps, "median_ms": round(ms, 5), "mean_ms": round(t["mean_ms"], 5),
            "event_per_call_median_ms": round(t["event_per_call_median_ms"], 5),
            "tflops": round(tflops, 3), "gbs": round(gbs, 1),
            "roofline": {"bound": "hbm" if hbm_bound else "mfma",
-                        "frac": round(gbs / HBM_PEAK_GBS if hbm_bound else tflops / FP32_MATRIX_PEAK_TFLOPS, 4),
-                        "traffic": traffic_from_profiles(name)},
-           "parity": parity_rows(oracle, a_h, b_h, c_h, cfg, d)}
+                        "frac": round(gbs / HBM_PEAK_GBS if hbm_bound else tflops / peak, 4),
+                        "peak": HBM_PEAK_GBS if hbm_bound else peak, "unit": "GB/s" if hbm_bound else "TFLOP/s",
+                        "traffic": traffic_from_profiles(name if not half else f"{name}_{dtype}_nn")},
+           "parity": parity}
+    if all_primitives:
+        out.update(primitive_matrix(plan, stream, d, lambda: parity_rows(oracle, a_h, b_h, c_h, cfg, d, ref=ref)[0],
+                                    steps=20))
     del a, b, c, d, plan
+    torch.cuda.empty_cache()
+    return out
+
+
+# The reference's own benchmark shapes, (m, k, n): its published table (docs/benchmarks/gemm-fp32.md:10-42)
+# and its "standard" suite (benchmarks/ftrain_bench/ops/gemm.py:41-52).
+REFERENCE_SHAPES = ((64, 64, 64), (128, 128, 128), (256, 256, 256), (512, 512, 512), (1024, 1024, 1024),
+                    (2048, 2048, 2048), (4096, 4096, 4096), (8192, 8192, 8192), (1024, 4096, 4096),
+                    (4096, 1024, 11008))
+
+
+def reference_measure(fn, warmup: int = 10, target_ms: float = 200.0, lo: int = 10, hi: int = 200) -> float:
+    """The reference harness's timing policy (benchmarks/ftrain_bench/timing.py:21-43): warm-up, then
+    each call bracketed by events on the current stream and synchronised, the iteration count adapted to
+    about 200 ms within [10, 200]; the median in ms."""
+    import statistics
+
+    import torch
+
+    def once():
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e)
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    iters = max(lo, min(hi, int(target_ms / max(once(), 1e-3)) + 1))
+    return statistics.median(once() for _ in range(iters))
+
+
+def reference_suite() -> list:
+    """L1 (flash_train.torch.gemm), L3 (cached Plan, Primitive 0) and the torch.matmul baseline per
+    reference shape, with a, b ~ N(0, 1) drawn as the reference harness draws them (seed 2026)."""
+    import torch
+
+    import flash_train.capi as capi
+    import flash_train.torch as ftt
+
+    out = []
+    for m, k, n in REFERENCE_SHAPES:
+        torch.manual_seed(2026)
+        a = torch.randn((m, k), device="cuda")
+        b = torch.randn((k, n), device="cuda")
+        d = torch.empty(m, n, device="cuda")
+        plan = capi.plan_for(a, b, None, d, 1.0, 0.0)
+        h = torch.cuda.current_stream().cuda_stream
+        l3 = reference_measure(lambda: plan.execute(0, h))
+        l1 = reference_measure(lambda: ftt.gemm(a, b))
+        base = reference_measure(lambda: torch.matmul(a, b))
+        flops = 2.0 * m * n * k
+        out.append({"shape_mkn": [m, k, n], "primitive": plan.name(0), "l3_plan_ms": round(l3, 5),
+                    "l1_torch_gemm_ms": round(l1, 5), "torch_matmul_ms": round(base, 5),
+                    "l3_tflops": round(flops / (l3 * 1e-3) / 1e12, 3)})
+        del a, b, d, plan
     torch.cuda.empty_cache()
     return out
 
@@ -357,7 +480,7 @@ def main() -> None:
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     a_h, b_h, c_h, cfg = oracle.seeded_inputs(args.workload)
     if args.grouped:
-        run_grouped(args, a_h, b_h, c_h, cfg)
+        run_grouped(args)
         return
     m, n, k = cfg["m"], cfg["n"], cfg["k"]
     half = args.dtype != "fp32"
@@ -448,8 +571,17 @@ def main() -> None:
         configs = []
         for name, steps in CONFIG_STEPS.items():
             log(f"config {name}")
-            configs.append(run_config(name, steps))
+            configs.append(run_config(name, steps, all_primitives=name in PRIMITIVE_MATRIX))
+        # Grouped GEMM (mixture-of-experts forward) and bf16 inputs on the BASELINE shapes.
+        for name, steps in (("square_8192", 20), ("mlp_fwd", 20)):
+            log(f"config {name} bf16")
+            configs.append(run_config(name, steps, dtype="bf16"))
+        for experts in (8, 64):
+            log(f"config grouped mlp_fwd over {experts} experts")
+            configs.append(grouped_core("mlp_fwd", experts, "fp32", steps=10, warmup=2))
         result["configs"] = configs
+        log("reference benchmark shapes")
+        result["reference_suite"] = reference_suite()
     if not args.no_cpu and not half:
         result["cpu_baseline"] = cpu_baseline(a_h, b_h, cfg["alpha"], cfg["beta"], args.cpu_budget)
         result["cpu_torch_matmul"] = torch_cpu_matmul(a_h, b_h, min(args.cpu_budget, 5.0))

@@ -296,9 +296,18 @@ __global__ __launch_bounds__(256) void splitk_reduce_wide(ReduceParams p) {
     const uint64_t units  = VEC ? p.count / 4 : p.count;
     const V* __restrict__ W = reinterpret_cast<const V*>(p.partials);
     for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < units; i += (uint64_t)gridDim.x * 256) {
+        // Up to 8 slices' loads in flight before their adds (in increasing z): the pass is
+        // latency-bound, a load per add kept one or two in flight.
         V s = W[i];
-#pragma unroll 4
-        for (int z = 1; z < p.splits; ++z) s += W[(uint64_t)z * units + i];
+        for (int z = 1; z < p.splits; z += 8) {
+            V v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (z + j < p.splits) v[j] = W[(uint64_t)(z + j) * units + i];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (z + j < p.splits) s += v[j];
+        }
         if constexpr (VEC) {
             const uint64_t row_vecs = p.n / 4;
             const uint64_t r = i / row_vecs, c = 4 * (i - r * row_vecs);
