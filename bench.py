@@ -172,9 +172,7 @@ def grouped_core(workload: str, E: int, dtype: str, steps: int, warmup: int) -> 
     stream = torch.cuda.Stream()
     h = stream.cuda_stream
     with torch.cuda.stream(stream):
-        for _ in range(warmup):
-            plan.execute(0, h)
-        torch.cuda.synchronize()
+        warm_up(lambda: plan.execute(0, h), stream, warmup)
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
         for _ in range(steps):
@@ -243,6 +241,26 @@ CONFIG_STEPS = {
 }
 
 
+def warm_up(call, stream, calls: int, min_ms: float = 25.0) -> None:
+    """`calls` untimed calls, then more until about `min_ms` of GPU work has run: a few calls of a
+    short kernel leave the clock below its steady-state value (measured on MI355X: 256x256x65536
+    73 us right after 10 warm-up calls, 66 us once warm)."""
+    import torch
+
+    for _ in range(calls):
+        call()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record(stream)
+    for _ in range(10):
+        call()
+    e.record(stream)
+    torch.cuda.synchronize()
+    per = max(s.elapsed_time(e) / 10, 1e-3)
+    for _ in range(min(int(min_ms / per), 20000)):
+        call()
+    torch.cuda.synchronize()
+
+
 def time_steps(plan, index: int, stream, steps: int, warmup: int, block: int = 10, workspace=(0, 0)) -> dict:
     """HIP events on the launch stream around blocks of `block` back-to-back calls: the mean over
     all steps and the median of the block means (ms per call).  An event between every two calls
@@ -253,9 +271,7 @@ def time_steps(plan, index: int, stream, steps: int, warmup: int, block: int = 1
     h = stream.cuda_stream
     blocks = max(1, steps // block)
     with torch.cuda.stream(stream):
-        for _ in range(warmup):
-            plan.execute(index, h, *workspace)
-        torch.cuda.synchronize()
+        warm_up(lambda: plan.execute(index, h, *workspace), stream, warmup)
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(blocks + 1)]
         ev[0].record(stream)
         for i in range(blocks):

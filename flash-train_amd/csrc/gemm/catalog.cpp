@@ -26,7 +26,7 @@ constexpr SplitKind N = SplitKind::kNone, P = SplitKind::kPartial, F = SplitKind
 constexpr FTrainNumericType FP32 = FTRAIN_NUMERIC_TYPE_FP32, BF16 = FTRAIN_NUMERIC_TYPE_BF16,
                             FP16 = FTRAIN_NUMERIC_TYPE_FP16;
 constexpr VariantInfo kInfo[] = {
-    {"Fp32Mfma16Gemm_256x256_Dma", 256, 256, 32, 256, 1, true, N, false, false, false, 0.980, FP32, 256.0, 0.980},
+    {"Fp32Mfma16Gemm_256x256_Dma", 256, 256, 32, 256, 1, true, N, false, false, false, 0.965, FP32, 256.0, 0.965},
     {"Fp32Mfma16Gemm_256x256_Dma_SplitK", 256, 256, 32, 256, 1, true, P, false, false, false, 0.957, FP32, 256.0, 0.957},
     {"Fp32Mfma16Gemm_128x128_Dma", 128, 128, 32, 256, 2, true, N, false, false, false, 0.982, FP32, 256.0, 0.956},
     {"Fp32Mfma16Gemm_128x128_Dma_SplitK", 128, 128, 32, 256, 2, true, P, false, false, false, 0.990, FP32, 256.0, 0.974},
