@@ -97,10 +97,10 @@ def main() -> None:
         "Commands, run from the repository root on the MI355X box after "
         "`cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT`, then the summary:", "", "```",
         f"rocprofv3 --kernel-trace --stats --output-format csv -d {d}/kt -o run -- {b} > {d}/kt.log",
-        f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d {d}/F -o run -- {b} --steps 3 --warmup 1",
-        f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d {d}/W -o run -- {b} --steps 3 --warmup 1",
+        f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d {d}/F -o run -- {b} --steps 3 --warmup 1 --warm-ms 0",
+        f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d {d}/W -o run -- {b} --steps 3 --warmup 1 --warm-ms 0",
         f"rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE GRBM_GUI_ACTIVE "
-        f"--output-format csv -d {d}/M -o run -- {b} --steps 3 --warmup 1",
+        f"--output-format csv -d {d}/M -o run -- {b} --steps 3 --warmup 1 --warm-ms 0",
         f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d {a.copy}/F -o run -- python3 bench.py --copy-calibration",
         f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d {a.copy}/W -o run -- python3 bench.py --copy-calibration",
         f"python3 flash-train_amd/bench/rocprof_summary.py --dir {d} --copy {a.copy} --kernel {a.kernel} "
