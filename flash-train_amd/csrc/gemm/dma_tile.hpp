@@ -71,6 +71,8 @@ typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 using u16 = unsigned short;
 
 constexpr int kStageK = 64;
+// Most tile rows a grouped launch walks as one band (tile_of).
+constexpr int kGroupBand = 16;
 // Word 3 of a raw (untyped, stride 0) buffer resource on gfx9 parts: 32-bit data format, the range
 // check against num_records on every access.
 constexpr int kBufferConfig = 0x00020000;
@@ -108,14 +110,15 @@ __device__ __forceinline__ void dma_1k(unsigned voff, const void* sbase, unsigne
 }
 
 // Output tile of workgroup `bid`: consecutive ids go to the 8 XCDs in turn,
-// so each XCD gets a contiguous run of tile ids, walked in bands of 8 tile
-// rows (a band's a panels stay in that XCD's L2 while its b panels stream).
-__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+// so each XCD gets a contiguous run of tile ids, walked in bands of
+// `rows_per_band` tile rows (a band's a panels stay in that XCD's L2 while its b panels
+// stream; every band fetches the whole of b once).
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn, int rows_per_band = 8) {
     const int tiles = tiles_m * tiles_n;
     const int per   = tiles >> 3;
     int t           = bid;
     if (bid < (per << 3)) t = (bid & 7) * per + (bid >> 3);
-    constexpr int kBand = 8;
+    const int kBand = rows_per_band;
     const int band_span = kBand * tiles_n;
     const int band      = t / band_span;
     const int first_m   = band * kBand;
@@ -181,7 +184,8 @@ struct Operand {
 // SPLIT: the workgroup reduces k range [z k_chunk, (z + 1) k_chunk) and stores its raw fp32 sums
 // to slice z of p.d (dense m x n); the reduction kernel forms d.
 template <bool BF16, bool TA, bool TB, int T = 256, bool SPLIT = false>
-__device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int bid, int z = 0) {
+// band: tile rows per band of the tile order (tile_of).
+__device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int bid, int z = 0, int band = 8) {
     constexpr bool A_TR = TA, B_TR = !TB;
     constexpr int NB = T / 64;               // 32x32 blocks per wave row and column
     constexpr int NDO = T / 32;              // DMAs per wave per operand per stage
@@ -194,7 +198,7 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wrow = (wave >> 1) * (T / 2), wcol = (wave & 1) * (T / 2);
     int tm, tn;
-    tile_of(bid, p.tiles_m, p.tiles_n, tm, tn);
+    tile_of(bid, p.tiles_m, p.tiles_n, tm, tn, band);
     const int m0 = tm * T, n0 = tn * T;
     const int M = p.m, N = p.n;
     const int kbeg = SPLIT ? z * p.k_chunk : 0;
@@ -452,7 +456,10 @@ __global__ __launch_bounds__(256, 256 / T) void grouped_half_gemm_dma(GroupedHal
     const HalfGemmParams p = g.params[lo];
     const int local        = bid - g.tile_start[lo];
     if (local >= p.tiles_m * p.tiles_n) return;
-    half_gemm_dma_tile<BF16, TA, TB, T>(p, local);
+    // One band per group when the group has at most kGroupBand tile rows: each group has a b of its
+    // own, which bands of 8 rows fetched once per band (8 MoE experts of 4 to 13 tile rows: 1.5x
+    // the b bytes of one band per expert).
+    half_gemm_dma_tile<BF16, TA, TB, T>(p, local, 0, p.tiles_m <= kGroupBand ? p.tiles_m : 8);
 }
 
 // Kernel for one input type, tile size and operand orientation (ta: column-major a, tb:
