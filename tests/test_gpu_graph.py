@@ -246,3 +246,46 @@ def test_first_convenience_call_of_a_shape_can_be_captured(capi, oracle):
     gc.collect()
     torch.cuda.synchronize()
     assert t.ftrainTestingConveniencePlansAlive() == before
+
+
+# A child process: the Primitive allow-list is read once per process.
+CAPTURE_CHILD = r"""
+import json, sys, torch
+sys.path[:0] = sys.argv[1:3]
+from flash_train import capi
+m, n, k = 64, 4096, 4096
+g = torch.Generator().manual_seed(5)
+a, b = torch.randn(m, k, generator=g).cuda(), torch.randn(k, n, generator=g).cuda()
+d = torch.empty(m, n, device="cuda")
+al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+views = (capi.matrix(a), capi.matrix(b), capi.matrix(None, [m, n]), capi.matrix(d), al.view, be.view)
+side = torch.cuda.Stream()
+out = {}
+graph = torch.cuda.CUDAGraph()
+try:
+    with torch.cuda.graph(graph, stream=side):
+        out["status"] = capi.gemm_status(*views, stream=side.cuda_stream)
+        out["message"] = capi.last_message()
+except Exception as e:  # an empty capture may be refused by torch; the status is what is checked
+    out["capture_error"] = str(e)[:200]
+print("RESULT " + json.dumps(out))
+"""
+
+
+def test_uncached_capture_without_a_fitting_primitive_is_unsupported():
+    """Under capture, a first ftrainGemm call whose every Primitive needs a
+    workspace (the allow-list keeps split-k Primitives only) and gets none
+    returns UNSUPPORTED and names the ways out, instead of allocating."""
+    import json
+    import os
+    import subprocess
+    import sys
+
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, FTRAIN_ENABLED_PRIMITIVES="Fp32Mfma16Gemm_64x128_Dma_SplitK,Fp32Mfma16Gemm_64x64_Dma_SplitK")
+    proc = subprocess.run([sys.executable, "-c", CAPTURE_CHILD, os.path.join(repo, "flash-train_amd"), repo],
+                          env=env, capture_output=True, text=True, timeout=110)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    out = json.loads(next(x for x in proc.stdout.splitlines() if x.startswith("RESULT "))[len("RESULT "):])
+    assert out["status"] == 4, out  # UNSUPPORTED
+    assert "stream capture" in out["message"] and "ftrainGemmNoAlloc" in out["message"], out
