@@ -83,9 +83,11 @@ struct SharedPlan {
     std::atomic<int> owners{1};
 };
 
+// Never destroyed: HIP may run a graph's user-object destructor while the
+// process tears down its statics.
 std::mutex& releasedMutex() {
-    static std::mutex m;
-    return m;
+    static auto* m = new std::mutex();
+    return *m;
 }
 std::vector<FTrainPlan>& releasedPlans() {
     static auto* v = new std::vector<FTrainPlan>();
