@@ -593,7 +593,7 @@ def main() -> None:
             log(f"config {name}")
             configs.append(run_config(name, steps, all_primitives=name in PRIMITIVE_MATRIX))
         # Grouped GEMM (mixture-of-experts forward) and bf16 inputs on the BASELINE shapes.
-        for name, steps in (("square_8192", 20), ("mlp_fwd", 20)):
+        for name, steps in (("square_8192", 20), ("mlp_fwd", 20), ("skinny_64x4096x4096", 200)):
             log(f"config {name} bf16")
             configs.append(run_config(name, steps, dtype="bf16"))
         for experts in (8, 64):
