@@ -22,6 +22,11 @@ extern "C" {
  * rank-two device views (c may have null memory, which drops the beta term);
  * alpha and beta are host fp32 scalars.  Asynchronous on `stream`.  On
  * failure the thread's last message is the failing step's message.
+ * Under stream capture a problem not yet seen on this thread and stream runs
+ * the first Primitive that needs no more than `workspace_bytes` (nothing is
+ * allocated during the capture); FTRAIN_STATUS_UNSUPPORTED when none does.
+ * A graph that captured a call keeps its Plan alive until the graph and its
+ * executable graphs are destroyed.
  */
 FTRAIN_API FTrainStatus ftrainGemm(FTrainStorageView a, FTrainStorageView b, FTrainStorageView c, FTrainStorageView d,
                                    FTrainStorageView alpha, FTrainStorageView beta, FTrainNumericType compute_type,
