@@ -31,6 +31,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(os.path.dirname(HERE))
 FP32_PEAK = 157.3
 HALF_PEAK = 2500.0  # dense bf16 / fp16 MFMA, TFLOP/s
+PEAK_CLOCK_HZ = 2.4e9  # MI355X highest shader clock (the peaks above are quoted at it)
 
 
 def rows(path: str) -> list:
@@ -88,6 +89,11 @@ def main() -> None:
     fs, ws = 262144.0 / cf, 262144.0 / cw  # the calibration copy moves 256 MiB each way
     traffic = fetch * 1024 * fs + write * 1024 * ws
     busy = mc["SQ_VALU_MFMA_BUSY_CYCLES"] / (1024.0 * mc["GRBM_GUI_ACTIVE"] / 8.0)
+    # MFMA cycles per SIMD over the traced kernel time at the highest shader clock: a lower bound on
+    # the busy fraction whatever the clock was.  GRBM_GUI_ACTIVE spans the counter window, which
+    # adds several microseconds to a dispatch (a 4-5 us reduction kernel reads as a 6 GHz clock),
+    # so the ratio above understates short kernels.
+    busy_floor = mc["SQ_VALU_MFMA_BUSY_CYCLES"] / 1024.0 / (kernel_us * 1e-6 * PEAK_CLOCK_HZ)
     conflict = mc["SQ_LDS_BANK_CONFLICT"] / mc["SQ_LDS_IDX_ACTIVE"] if mc.get("SQ_LDS_IDX_ACTIVE") else 0.0
 
     b = "python3 bench.py --no-cpu --no-overhead --no-configs " + a.bench_args
@@ -122,13 +128,18 @@ def main() -> None:
         f"{alg / kernel_us / 1e3:.1f} GB/s ({100 * alg / kernel_us / 1e3 / 8000:.1f}% of 8 TB/s).",
         "",
         "## HBM traffic and counters per dispatch (PMC)", "",
-        "| FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes (scaled) | Algorithmic bytes | Ratio | MFMA busy | LDS bank conflicts / LDS active |",
-        "|---:|---:|---:|---:|---:|---:|---:|",
-        f"| {fetch:.1f} | {write:.1f} | {traffic:.4g} | {alg:.4g} | {traffic / alg:.2f} | {100 * busy:.1f}% | {conflict:.3f} |",
+        "| FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes (scaled) | Algorithmic bytes | Ratio | MFMA busy | MFMA busy, floor | LDS bank conflicts / LDS active |",
+        "|---:|---:|---:|---:|---:|---:|---:|---:|",
+        f"| {fetch:.1f} | {write:.1f} | {traffic:.4g} | {alg:.4g} | {traffic / alg:.2f} | {100 * busy:.1f}% | "
+        f"{100 * busy_floor:.1f}% | {conflict:.3f} |",
         "",
         f"Scales from the copy calibration (a 256 MiB device copy reads {cf:.1f} KiB and writes {cw:.1f} KiB "
         f"per dispatch): FETCH_SIZE × {fs:.4f}, WRITE_SIZE × {ws:.4f}.",
         "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs × GRBM_GUI_ACTIVE / 8 XCDs).",
+        f"MFMA busy, floor = SQ_VALU_MFMA_BUSY_CYCLES / 1024 SIMDs / (the traced kernel time × "
+        f"{PEAK_CLOCK_HZ / 1e9:.1f} GHz, the highest shader clock): the busy fraction is at least this at any clock. "
+        "GRBM_GUI_ACTIVE spans the counter window, which adds several µs to each dispatch, so the first ratio "
+        "understates kernels of a few tens of µs.",
     ]
     with open(a.out, "w") as f:
         f.write("\n".join(lines) + "\n")
@@ -136,6 +147,7 @@ def main() -> None:
     tj = json.load(open(tj_path)) if os.path.exists(tj_path) else {}
     tj[a.workload] = {"kernel": a.title, "hbm_bytes_per_launch": int(traffic), "algorithmic_bytes": int(alg),
                       "kernel_us_timed_mean": round(kernel_us, 2), "mfma_busy": round(busy, 4),
+                      "mfma_busy_floor": round(busy_floor, 4),
                       "profile": os.path.relpath(os.path.abspath(a.out), REPO)}
     with open(tj_path, "w") as f:
         json.dump(tj, f, indent=1)
