@@ -79,6 +79,11 @@ constexpr VariantInfo kInfo[] = {
     {"Bf16MfmaGemm_128x128_Dma_SplitK", 128, 128, 64, 256, 2, true, P, false, false, true, 0.55, BF16, 4096.0, 0.45},
     {"Fp16MfmaGemm_128x128_Dma", 128, 128, 64, 256, 2, true, N, false, false, true, 0.48, FP16, 4096.0, 0.45},
     {"Fp16MfmaGemm_128x128_Dma_SplitK", 128, 128, 64, 256, 2, true, P, false, false, true, 0.55, FP16, 4096.0, 0.45},
+    // Applicable to m of at most 64 only.  The low single-workgroup figure makes the model spread
+    // such a problem over 8 splits (one workgroup per CU), as measured (64x4096x4096: 4 splits
+    // leave half the CUs idle).
+    {"Bf16MfmaGemm_64x128_Dma_SplitK", 64, 128, 64, 256, 2, true, P, false, false, true, 0.52, BF16, 4096.0, 0.35},
+    {"Fp16MfmaGemm_64x128_Dma_SplitK", 64, 128, 64, 256, 2, true, P, false, false, true, 0.52, FP16, 4096.0, 0.35},
     {"Bf16Gemv", kGemvHalfRows, kGemvHalfCols, 1, 1024, 1, true, N, true, false, false, 0, BF16, 4096.0, 0},
     {"Fp16Gemv", kGemvHalfRows, kGemvHalfCols, 1, 1024, 1, true, N, true, false, false, 0, FP16, 4096.0, 0},
 };

@@ -15,7 +15,9 @@
 //            are available), plus a fixed cost per round of resident
 //            workgroups.
 //   memory : algorithmic bytes (a, b, d, optional c) at 80% of 8 TB/s, plus
-//            the partial tiles (written and read once) for split-k.
+//            the partial tiles (written and read once) for split-k; scaled
+//            by the share of CUs the launch's workgroups occupy when there
+//            are fewer workgroups than CUs.
 //   time   = max(compute, memory) + the reduction's pass over the partial
 //            tiles (split-k) + launch latency (one more for split-k).
 #include <algorithm>
@@ -51,6 +53,7 @@ constexpr double kFusedStoreMicros    = 2.0;  // per round: a split workgroup's 
 // Fixed cost per round of resident workgroups (operand prologue, epilogue
 // stores, the ramp of the first stages); fitted with the catalog efficiencies.
 constexpr double kRoundMicros     = 3.35;
+constexpr double kTieWeight       = 1e-3;
 constexpr uint64_t kMinSplitDepth = 256;  // reduction depth worth one split-k workgroup
 constexpr uint64_t kMinGemvDepth  = 64;
 
@@ -134,7 +137,14 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
     const double per_round = vi.split != SplitKind::kFused ? kRoundMicros
                              : kFusedRampMicros + (splits > 1 ? kFusedStoreMicros : 0.0);
     const double compute   = double(per_cu) * 2.0 * vi.bm * vi.bn * depth / cu_rate + rounds * per_round;
-    return std::max(compute, bytes / kHbmBytesPerMicro) + serial_us + launch;
+    // A launch with fewer workgroups than CUs streams memory through only that many of them (a CU
+    // moves a bounded number of bytes per clock): 64x4096x14336 bf16 on the 64x128 split tile took
+    // 36.3 us at 4 splits (128 workgroups) against 23.8 us at 8.
+    const double fill = std::min(1.0, double(wgs) / double(cus));
+    // When memory bounds several variants alike, the one with the least compute overlaps it best
+    // (64x14336x4096 bf16 at 4 splits: the 64x128 DMA split tile 25.9 us, the 128x128 one 27.6,
+    // the register-staged 128x128 30.2): a thousandth of the compute time breaks such ties.
+    return std::max(compute, bytes / (kHbmBytesPerMicro * fill)) + serial_us + launch + kTieWeight * compute;
 }
 
 }  // namespace

@@ -438,6 +438,8 @@ const void* kernelFor(Variant v, bool ta, bool tb) {
         return dma128KernelBf16(ta, tb, v == Variant::kBf16MfmaDma128x128S);
     if (v == Variant::kFp16MfmaDma128x128 || v == Variant::kFp16MfmaDma128x128S)
         return dma128KernelFp16(ta, tb, v == Variant::kFp16MfmaDma128x128S);
+    if (v == Variant::kBf16MfmaDma64x128S) return dma64x128KernelBf16(ta, tb);
+    if (v == Variant::kFp16MfmaDma64x128S) return dma64x128KernelFp16(ta, tb);
     if (ta || tb) {
         if (v == Variant::kSimt) return reinterpret_cast<const void*>(&simt_gemm);  // strides are runtime values
         if (v == Variant::kGemvS && !tb && ta) return reinterpret_cast<const void*>(&gemv_splitk<true, true>);

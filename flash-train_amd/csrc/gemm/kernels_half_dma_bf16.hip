@@ -9,6 +9,8 @@ const void* groupedDmaKernelBf16(bool ta, bool tb) { return ddev::groupedDmaKern
 
 const void* groupedDma128KernelBf16(bool ta, bool tb) { return ddev::groupedDmaKernel<true, 128>(ta, tb); }
 
+const void* dma64x128KernelBf16(bool ta, bool tb) { return ddev::dma64x128Kernel<true>(ta, tb); }
+
 const void* dma128KernelBf16(bool ta, bool tb, bool split) {
     return split ? ddev::dma128Kernel<true, true>(ta, tb) : ddev::dma128Kernel<true, false>(ta, tb);
 }

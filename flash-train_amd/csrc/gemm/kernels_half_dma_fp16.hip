@@ -9,6 +9,8 @@ const void* groupedDmaKernelFp16(bool ta, bool tb) { return ddev::groupedDmaKern
 
 const void* groupedDma128KernelFp16(bool ta, bool tb) { return ddev::groupedDmaKernel<false, 128>(ta, tb); }
 
+const void* dma64x128KernelFp16(bool ta, bool tb) { return ddev::dma64x128Kernel<false>(ta, tb); }
+
 const void* dma128KernelFp16(bool ta, bool tb, bool split) {
     return split ? ddev::dma128Kernel<false, true>(ta, tb) : ddev::dma128Kernel<false, false>(ta, tb);
 }

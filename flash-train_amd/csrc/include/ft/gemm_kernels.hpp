@@ -203,6 +203,9 @@ enum class Variant : int {
     kBf16MfmaDma128x128S,
     kFp16MfmaDma128x128,
     kFp16MfmaDma128x128S,
+    // bf16 / fp16 64x128 DMA-staged split-k tiles (m of at most 64; row-major a).
+    kBf16MfmaDma64x128S,
+    kFp16MfmaDma64x128S,
     // One-pass skinny-m kernels (m <= 8, row-major b) for bf16 / fp16 inputs.
     kBf16Gemv,
     kFp16Gemv,
@@ -292,6 +295,8 @@ const void* dmaKernelBf16(bool ta, bool tb);
 const void* dmaKernelFp16(bool ta, bool tb);
 const void* dma128KernelBf16(bool ta, bool tb, bool split);
 const void* dma128KernelFp16(bool ta, bool tb, bool split);
+const void* dma64x128KernelBf16(bool ta, bool tb);  // null for a column-major a
+const void* dma64x128KernelFp16(bool ta, bool tb);
 const void* groupedDmaKernelBf16(bool ta, bool tb);
 const void* groupedDmaKernelFp16(bool ta, bool tb);
 const void* groupedDma128KernelBf16(bool ta, bool tb);

@@ -644,13 +644,24 @@ def test_finder_choices_for_16_bit_tiles(tlib):
     # bf16, MI355X, every applicable Primitive timed (us): the Finder's pick was the fastest on each
     # of these.  Small and mid-size squares: the 128x128 DMA tile (2048^3 25.3 against 256x256 DMA
     # 39.1); large ones: the 256x256 DMA tile (8192^3 871 against 128x128 DMA 906); deep k: the
-    # 128x128 DMA split-k tile (64x4096x4096 15.1 against the register-staged split-k 20.1,
-    # 256x256x65536 21.2 against 29.3).
+    # 128x128 DMA split-k tile (256x256x65536 21.2 against the register-staged split-k 29.3).
     assert rank(tlib, 2048, 2048, 2048, ab_type=c.BF16)[0] == "Bf16MfmaGemm_128x128_Dma"
     assert rank(tlib, 8192, 8192, 8192, ab_type=c.BF16)[0] == "Bf16MfmaGemm_256x256_Dma"
     assert rank(tlib, 16384, 14336, 4096, ab_type=c.BF16)[0] == "Bf16MfmaGemm_256x256_Dma"
-    for shape in ((64, 4096, 4096), (256, 256, 65536), (384, 4096, 4096), (1536, 1536, 8192)):
+    for shape in ((256, 256, 65536), (384, 4096, 4096), (1536, 1536, 8192)):
         assert rank(tlib, *shape, ab_type=c.BF16)[0] == "Bf16MfmaGemm_128x128_Dma_SplitK", shape
+    # One tile row: the 64x128 DMA split tile, at the split count measured fastest (after a warm
+    # clock, forced split counts, us): 64x4096x4096 12.7 at 8 splits (128x128 split tile 13.5),
+    # 64x4096x14336 23.8 at 8 (25.4), 64x14336x4096 26.2 at 4 (26.8; the register-staged split
+    # tile 30.2); 4 splits of 64x4096x14336 (128 workgroups) took 36.3.
+    tile64 = "Bf16MfmaGemm_64x128_Dma_SplitK"
+    names = {tlib.ftrainTestingVariantName(i).decode(): i for i in range(tlib.ftrainTestingVariantCount())}
+    for shape, splits in (((64, 4096, 4096), 8), ((64, 4096, 14336), 8), ((64, 14336, 4096), 4)):
+        assert rank(tlib, *shape, ab_type=c.BF16)[0] == tile64, shape
+        assert tlib.ftrainTestingChooseSplits(names[tile64], *shape, 256) == splits, shape
+    # Taller problems keep the 128-row tiles: the 64-row one does not apply above m = 64.
+    assert tile64 not in rank(tlib, 65, 4096, 4096, ab_type=c.BF16)
+    assert "Fp16MfmaGemm_64x128_Dma_SplitK" == rank(tlib, 64, 4096, 4096, ab_type=c.FP16)[0]
 
 
 def test_finder_respects_alignment_and_row_limits(tlib):

@@ -123,6 +123,21 @@ def test_half_dma_tile(capi, ops, oracle, kind, cd, la, lb, m, n, k, pad, with_c
         assert f"{kind.capitalize()}MfmaGemm_128x128_Dma_SplitK" in names, names
 
 
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+@pytest.mark.parametrize("cd", ["fp32", "same"])
+@pytest.mark.parametrize("la,lb", list(itertools.product((False, True), (False, True))))
+@pytest.mark.parametrize("m,n,k,pad,with_c", [(64, 4096, 4096, 0, False), (40, 200, 1024, 8, True),
+                                              (1, 136, 576, 8, True), (64, 1024, 8192, 0, True)])
+def test_half_dma_64_row_split_tile(capi, ops, oracle, kind, cd, la, lb, m, n, k, pad, with_c):
+    # The 64x128 split-k DMA tile (m of at most 64, row-major a): a full-height tile, partial ones
+    # (rows clamped, stores dropped), an n edge, uneven splits (576 = 320 + 256) and deep k; every
+    # Primitive of each Plan.  A column-major a leaves it out of the Plan.
+    names = run_case(capi, ops, oracle, kind, kind if cd == "same" else "fp32", m, n, k, la, lb, pad=pad,
+                     with_c=with_c, seed=m + k + pad)
+    tile = f"{kind.capitalize()}MfmaGemm_64x128_Dma_SplitK"
+    assert (tile in names) == (not la), names
+
+
 @pytest.mark.parametrize("cd", ["fp32", "same"])
 def test_half_split_k_wide_reduction(capi, ops, oracle, cd):
     # 384x4096 outputs at k = 4096: the split-k tile's reduction runs one thread per output unit
