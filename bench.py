@@ -421,8 +421,9 @@ def reference_measure(fn, warmup: int = 10, target_ms: float = 200.0, lo: int = 
 
 
 def reference_suite() -> list:
-    """L1 (flash_train.torch.gemm), L3 (cached Plan, Primitive 0) and the torch.matmul baseline per
-    reference shape, with a, b ~ N(0, 1) drawn as the reference harness draws them (seed 2026)."""
+    """L1 (flash_train.torch.gemm), L2 (ftrainGemm, through ctypes), L3 (cached Plan, Primitive 0; the
+    reference's L4 for Primitive 0 is the same call) and the torch.matmul baseline per reference shape,
+    with a, b ~ N(0, 1) drawn as the reference harness draws them (seed 2026)."""
     import torch
 
     import flash_train.capi as capi
@@ -437,11 +438,18 @@ def reference_suite() -> list:
         plan = capi.plan_for(a, b, None, d, 1.0, 0.0)
         h = torch.cuda.current_stream().cuda_stream
         l3 = reference_measure(lambda: plan.execute(0, h))
+        al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+        va, vb, vc, vd = capi.matrix(a), capi.matrix(b), capi.View(None, [m, n]), capi.matrix(d)
+        l2_call = lambda: capi.gemm_status(va, vb, vc, vd, al.view, be.view, stream=h)
+        if l2_call() != capi.SUCCESS:
+            raise RuntimeError(f"ftrainGemm {m}x{k}x{n}: {capi.last_message()}")
+        l2 = reference_measure(l2_call)
         l1 = reference_measure(lambda: ftt.gemm(a, b))
         base = reference_measure(lambda: torch.matmul(a, b))
         flops = 2.0 * m * n * k
         out.append({"shape_mkn": [m, k, n], "primitive": plan.name(0), "l3_plan_ms": round(l3, 5),
-                    "l1_torch_gemm_ms": round(l1, 5), "torch_matmul_ms": round(base, 5),
+                    "l2_ftrain_gemm_ms": round(l2, 5), "l1_torch_gemm_ms": round(l1, 5),
+                    "torch_matmul_ms": round(base, 5),
                     "l3_tflops": round(flops / (l3 * 1e-3) / 1e12, 3)})
         del a, b, d, plan
     torch.cuda.empty_cache()
