@@ -90,8 +90,23 @@ def run(cmd: list[str]) -> None:
         raise SystemExit(f"build step failed: {cmd[-1]}")
 
 
+# Host-code sanitizer for a checking build (None for the product build); device code is unchanged.
+SANITIZER = None
+
+
+def out_dir() -> str:
+    return os.path.join(BUILD, SANITIZER) if SANITIZER else BUILD
+
+
+def sanitizer_flags() -> list[str]:
+    flags = [f"-fsanitize={SANITIZER}", "-fno-omit-frame-pointer", "-g"]
+    if SANITIZER == "undefined":
+        flags.append("-fno-sanitize-recover=undefined")
+    return flags
+
+
 def obj_path(src: str) -> str:
-    return os.path.join(BUILD, src.replace("/", "_") + ".o")
+    return os.path.join(out_dir(), src.replace("/", "_") + ".o")
 
 
 def up_to_date(out: str) -> bool:
@@ -116,6 +131,10 @@ def compile_one(src: str) -> str:
     cmd = [HIPCC, *COMMON, "-MD", "-MF", out + ".d"]
     if src.endswith(".hip"):
         cmd += ["-x", "hip", *DEVICE]
+        if SANITIZER:
+            cmd += [x for f in sanitizer_flags() for x in ("-Xarch_host", f)]
+    elif SANITIZER:
+        cmd += ["-O1", *sanitizer_flags()]
     cmd += ["-c", os.path.join(HERE, src), "-o", out]
     run(cmd)
     return out
@@ -127,8 +146,10 @@ def link_shared(objs: list[str], out: str, soname: str) -> None:
     script = os.path.join(BUILD, "exports.map")
     with open(script, "w") as f:
         f.write("{ global: ftrain*; local: *; };\n")
-    run([HIPCC, f"-Wl,--version-script={script}", "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", out,
-         f"-Wl,-soname,{soname}", f"-L{ROCM}/lib", "-lroctx64", f"-Wl,-rpath,{ROCM}/lib", "-Wl,--no-undefined"])
+    san = [f"-fsanitize={SANITIZER}", "-shared-libsan"] if SANITIZER else []
+    run([HIPCC, f"-Wl,--version-script={script}", "-shared", "-fPIC", f"--offload-arch={ARCH}", *san, *objs, "-o", out,
+         f"-Wl,-soname,{soname}", f"-L{ROCM}/lib", "-lroctx64", f"-Wl,-rpath,{ROCM}/lib",
+         *([] if SANITIZER else ["-Wl,--no-undefined"])])
 
 
 def torch_flags() -> tuple[list[str], list[str]]:
@@ -170,15 +191,24 @@ def main(argv: list[str] | None = None) -> None:
     ap.add_argument("--no-torch", action="store_true")
     ap.add_argument("--incremental", action="store_true",
                     help="skip sources whose object is newer than every file it includes")
+    ap.add_argument("--host-sanitizer", choices=("address", "undefined"),
+                    help="a checking build: both libraries with their host code under this sanitizer (device "
+                         "code unchanged), into _build/<sanitizer>/, for the CPU suite: FTRAIN_LIBRARY_DIR="
+                         "flash-train_amd/_build/<sanitizer> LD_PRELOAD=<clang's asan or ubsan_standalone runtime> "
+                         "python -m pytest tests -m 'not gpu'")
     args = ap.parse_args(argv)
-    global INCREMENTAL
+    global INCREMENTAL, SANITIZER
     INCREMENTAL = args.incremental
-    os.makedirs(BUILD, exist_ok=True)
+    SANITIZER = args.host_sanitizer
+    os.makedirs(out_dir(), exist_ok=True)
     with concurrent.futures.ThreadPoolExecutor(args.jobs) as pool:
         lib_objs = list(pool.map(compile_one, LIB_SOURCES))
         test_objs = list(pool.map(compile_one, TESTING_SOURCES))
-    link_shared(lib_objs, os.path.join(PKG, "libflash_train.so"), "libflash_train.so")
-    link_shared(lib_objs + test_objs, os.path.join(PKG, "libflash_train_testing.so"), "libflash_train_testing.so")
+    lib_dir = out_dir() if SANITIZER else PKG
+    link_shared(lib_objs, os.path.join(lib_dir, "libflash_train.so"), "libflash_train.so")
+    link_shared(lib_objs + test_objs, os.path.join(lib_dir, "libflash_train_testing.so"), "libflash_train_testing.so")
+    if SANITIZER:
+        return
     build_plan_overhead()
     if not args.no_torch:
         build_torch_binding()

@@ -20,8 +20,11 @@ from typing import Optional, Sequence
 import torch  # noqa: F401  (HIP runtime must be loaded by torch first)
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
-LIBRARY_PATH = os.path.join(_PKG, "libflash_train.so")
-TESTING_LIBRARY_PATH = os.path.join(_PKG, "libflash_train_testing.so")
+# FTRAIN_LIBRARY_DIR points the loader at another build of the two libraries (the checking builds
+# of build.py --host-sanitizer); by default they sit next to this file.
+_LIB_DIR = os.environ.get("FTRAIN_LIBRARY_DIR") or _PKG
+LIBRARY_PATH = os.path.join(_LIB_DIR, "libflash_train.so")
+TESTING_LIBRARY_PATH = os.path.join(_LIB_DIR, "libflash_train_testing.so")
 
 # ---- enums (common.h) ----
 SUCCESS, INVALID_ARGUMENT, OUT_OF_MEMORY, OVERFLOW, UNSUPPORTED, INTERNAL_ERROR = 0, 1, 2, 3, 4, 50
