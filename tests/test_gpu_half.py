@@ -276,3 +276,31 @@ def test_half_large_sampled(capi, ops, oracle, kind):
     ref = oracle.gemm_f64(a.float().numpy()[rows], w.float().numpy().T, None, 1.0, 0.0)
     rep = oracle.tolerance_check(d.cpu().numpy()[rows], ref, k)
     assert rep["ok"], rep
+
+
+@pytest.mark.parametrize("name", ["square_8192", "mlp_fwd", "skinny_64x4096x4096"])
+def test_half_bench_configs_at_full_size(capi, ops, oracle, name):
+    """The bf16 configurations the bench reports, at their full size (fp32 d): 64 sampled rows of the
+    Finder's pick against fp64 of the decoded bf16 inputs, far inside the bar, and over every row the
+    size-independent identity d @ 1 = alpha * a @ (b @ 1) + beta * c @ 1."""
+    import math
+
+    a_h, b_h, c_h, cfg = oracle.seeded_inputs(name)
+    a_h, b_h = a_h.to(torch.bfloat16), b_h.to(torch.bfloat16)
+    m, n, k, alpha, beta = cfg["m"], cfg["n"], cfg["k"], cfg["alpha"], cfg["beta"]
+    d = torch.full((m, n), float("nan"), device="cuda")
+    plan = capi.plan_for(a_h.cuda(), b_h.cuda(), c_h.cuda() if c_h is not None else None, d, alpha, beta, ops)
+    print(name, plan.names()[:3])
+    plan.execute(0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(7).choice(m, size=min(m, 64), replace=False))
+    ref = oracle.sampled_rows_f64(a_h.float(), b_h.float(), c_h, alpha, beta, rows)
+    rep = oracle.tolerance_check(d[torch.as_tensor(rows).cuda()].cpu().numpy(), ref, k)
+    assert rep["ok"] and rep["max_abs_err"] <= 1e-2 * rep["bound"], (name, plan.name(0), rep)
+    row_sums = d.double().sum(dim=1).cpu()
+    want = alpha * (a_h.double() @ b_h.double().sum(dim=1))
+    if c_h is not None:
+        want += beta * c_h.double().sum(dim=1)
+    err = (row_sums - want).abs().max().item()
+    scale = want.abs().max().item() + math.sqrt(n * k)
+    assert err <= 1e-4 * math.sqrt(k) * scale, (name, err, scale)
