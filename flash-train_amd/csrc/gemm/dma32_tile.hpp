@@ -82,14 +82,14 @@ __device__ __forceinline__ void store_b128(floatx4 v, __amdgpu_buffer_rsrc_t res
 }
 
 // Output tile of workgroup `bid`: the 8 XCDs take contiguous runs of tile
-// ids (hardware ids are dealt to XCDs in turn), walked in bands of 4 tile
-// rows.
-__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+// ids (hardware ids are dealt to XCDs in turn), walked in bands of
+// `rows_per_band` tile rows.
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn, int rows_per_band = 4) {
     const int tiles = tiles_m * tiles_n;
     const int per   = tiles >> 3;
     int t           = bid;
     if (bid < (per << 3)) t = (bid & 7) * per + (bid >> 3);
-    constexpr int kBand = 4;
+    const int kBand = rows_per_band;
     const int band_span = kBand * tiles_n;
     const int band      = t / band_span;
     const int first_m   = band * kBand;
@@ -115,7 +115,7 @@ __device__ __forceinline__ int a_swz(int row) {
 constexpr int kPartialPolicy = 2;
 
 template <int BM, int BN, int WM, int WN, bool SPLIT, bool TB = false, bool TA = false>
-__device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid, int z) {
+__device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid, int z, int band = 4) {
     static_assert(WM * WN == 4, "4 waves");
     constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 16, TN = WTN / 16, NC = TN / 4;
     static_assert(TN % 4 == 0 && TM >= 1, "column runs of four blocks");
@@ -141,7 +141,7 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wrow = (wave / WN) * WTM, wcol = (wave % WN) * WTN;
     int tm, tn;
-    tile_of(bid, p.tiles_m, p.tiles_n, tm, tn);
+    tile_of(bid, p.tiles_m, p.tiles_n, tm, tn, band);
     const int m0 = tm * BM, n0 = tn * BN;
     const int M = p.m, N = p.n;
     const int kbeg = SPLIT ? z * p.k_chunk : 0;
@@ -472,7 +472,9 @@ __global__ __launch_bounds__(256, MINB) void grouped_fp32_gemm_dma(GroupedGemmAr
     const GemmParams p = g.params[lo];
     const int local    = bid - g.tile_start[lo];
     if (local >= p.tiles_m * p.tiles_n) return;
-    fp32_gemm_dma_tile<BM, BN, WM, WN, false, TB, TA>(p, local, 0);
+    // One band per group of at most 16 tile rows: each group has a b of its own, which bands of 4
+    // rows fetched once per band.
+    fp32_gemm_dma_tile<BM, BN, WM, WN, false, TB, TA>(p, local, 0, p.tiles_m <= 16 ? p.tiles_m : 4);
 }
 
 }  // namespace ftrain::gemm::d32
