@@ -80,7 +80,9 @@ def main() -> None:
     flops = 2.0 * m * n * k
     half = bj.get("dtype") in ("bf16", "fp16")
     peak = HALF_PEAK if half else FP32_PEAK
-    alg = (2.0 if half else 4.0) * (m * k + k * n) + 4.0 * m * n * (2 if cfg.get("c") else 1)
+    # A grouped launch (bench.py --grouped E) reads one k x n weight per expert.
+    experts = cfg.get("experts", 1)
+    alg = (2.0 if half else 4.0) * (m * k + experts * k * n) + 4.0 * m * n * (2 if cfg.get("c") else 1)
     fetch = counters(os.path.join(a.dir, "F", "run_counter_collection.csv"), a.kernel)["FETCH_SIZE"]
     write = counters(os.path.join(a.dir, "W", "run_counter_collection.csv"), a.kernel)["WRITE_SIZE"]
     mc = counters(os.path.join(a.dir, "M", "run_counter_collection.csv"), a.kernel)
