@@ -184,7 +184,9 @@ struct Operand {
 // SPLIT: the workgroup reduces k range [z k_chunk, (z + 1) k_chunk) and stores its raw fp32 sums
 // to slice z of p.d (dense m x n); the reduction kernel forms d.
 // BM: tile rows (T by default; 64 with T = 128 for m of at most 64, row-major a only).
-template <bool BF16, bool TA, bool TB, int T = 256, bool SPLIT = false, int BM = T>
+// PF: stages of b to prefetch into L2 ahead of the stage being staged (0: none), for a b larger
+// than the MALL, whose stages otherwise arrive from HBM later than the DMA lead covers.
+template <bool BF16, bool TA, bool TB, int T = 256, bool SPLIT = false, int BM = T, int PF = 0>
 // band: tile rows per band of the tile order (tile_of).
 __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int bid, int z = 0, int band = 8) {
     constexpr bool A_TR = TA, B_TR = !TB;
@@ -214,6 +216,32 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
     Operand<B_TR, T> opb;
     opa.init(pa, p.lda, m0, M, wave, lane);
     opb.init(pb, p.ldb, n0, N, wave, lane);
+    // L2 prefetch of b: one DMA per wave per stage, each lane touching one 128-byte line of the
+    // stage's b tile (256 lines at T = 256), into a 1 KiB sink per wave that nothing reads.  Lines
+    // past the matrix are clamped onto its last column (row-major b) or column (column-major b).
+    __shared__ __attribute__((aligned(1024))) u16 pf_sink[PF ? 4 * 512 : 8];
+    const unsigned lsink = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)pf_sink + wave * 1024;
+    unsigned pf_voff    = 0;
+    const char* pf_base = nullptr;
+    if constexpr (PF > 0) {
+        static_assert(T == 256, "prefetch lines cover a 256-column stage");
+        const int L = wave * 64 + lane;
+        if constexpr (B_TR) {  // row-major b: 64 k rows x T columns, T / 64 lines per row
+            constexpr int LPR = T / 64;
+            const int krow = L / LPR, line = L % LPR;
+            pf_voff = static_cast<unsigned>((krow * p.ldb + (min(n0 + 64 * line, N - 8) - n0)) * 2);
+            pf_base = reinterpret_cast<const char*>(pb + n0);
+        } else {  // column-major b: T columns of 64 k, one line each
+            pf_voff = static_cast<unsigned>((min(n0 + L, N - 1) - n0) * p.ldb * 2);
+            pf_base = reinterpret_cast<const char*>(pb + (size_t)n0 * p.ldb);
+        }
+    }
+    auto prefetch = [&](int st) {
+        if constexpr (PF > 0) {
+            const size_t step = B_TR ? (size_t)kStageK * p.ldb * 2 : (size_t)kStageK * 2;
+            dma_1k(pf_voff, pf_base + (size_t)st * step, lsink);
+        }
+    };
     const unsigned la0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)As0;
     const unsigned lb0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)Bs0;
     const unsigned la1 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)As1;
@@ -302,6 +330,8 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
 #pragma unroll
                 for (int d = 0; d < ND; ++d)
                     if (((2 * d + 1) * NM) / (2 * ND) == t) dma_one(dma_st, d, la, lb);
+                // After the stage's last DMA: the prefetch is always the latest memory instruction.
+                if (PF > 0 && t == NM - 1) prefetch(min(dma_st + PF, nst - 1));
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -317,13 +347,15 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
     const int st1 = min(1, nst - 1);
 #pragma unroll
     for (int d = 0; d < ND; ++d) dma_one(st1, d, la1, lb1);
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(ND) : "memory");
+    // With prefetch, each wait below leaves exactly one instruction pending, the latest prefetch.
+    prefetch(min(1 + PF, nst - 1));
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(ND + (PF > 0 ? 1 : 0)) : "memory");
     read_half(fa0, fb0, As0, Bs0, 0);
 
     // Stages past the last reload the last one (harmless: nothing reads them).
 #define FT_DMA_PHASE(XA, XB, YA, YB, LXA, LXB, ST)                               \
     run_half(fa0, fb0, fa1, fb1, XA, XB, 1, std::false_type{}, 0, 0u, 0u);                          \
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory"); \
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(PF > 0 ? 1 : 0) : "memory"); \
     run_half(fa1, fb1, fa0, fb0, YA, YB, 0, std::true_type{}, min((ST) + 2, nst - 1), LXA, LXB);
     int st = 0;
     for (; st + 1 < nst; st += 2) {
@@ -421,9 +453,9 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
     }
 }
 
-template <bool BF16, bool TA, bool TB>
+template <bool BF16, bool TA, bool TB, int PF = 0>
 __global__ __launch_bounds__(256, 1) void half_gemm_dma(HalfGemmParams p) {
-    half_gemm_dma_tile<BF16, TA, TB>(p, blockIdx.x);
+    half_gemm_dma_tile<BF16, TA, TB, 256, false, 256, PF>(p, blockIdx.x);
 }
 
 // 128x128 tiles, two workgroups per CU, whole-k or split-k.  Split-k workgroups are renumbered so
@@ -466,7 +498,7 @@ __global__ __launch_bounds__(256, 2) void half_gemm_dma64x128(HalfGemmParams p) 
 // are multiples of 8, so the group-local id keeps the hardware id's XCD;
 // ids past the group's tiles are padding and exit at once (before any
 // barrier, the whole workgroup).
-template <bool BF16, bool TA, bool TB, int T = 256>
+template <bool BF16, bool TA, bool TB, int T = 256, int PF = 0>
 __global__ __launch_bounds__(256, 256 / T) void grouped_half_gemm_dma(GroupedHalfArgs g) {
     const int bid = blockIdx.x;
     int lo = 0, hi = g.groups - 1;
@@ -483,17 +515,17 @@ __global__ __launch_bounds__(256, 256 / T) void grouped_half_gemm_dma(GroupedHal
     // One band per group when the group has at most kGroupBand tile rows: each group has a b of its
     // own, which bands of 8 rows fetched once per band (8 MoE experts of 4 to 13 tile rows: 1.5x
     // the b bytes of one band per expert).
-    half_gemm_dma_tile<BF16, TA, TB, T>(p, local, 0, p.tiles_m <= kGroupBand ? p.tiles_m : 8);
+    half_gemm_dma_tile<BF16, TA, TB, T, false, T, PF>(p, local, 0, p.tiles_m <= kGroupBand ? p.tiles_m : 8);
 }
 
 // Kernel for one input type, tile size and operand orientation (ta: column-major a, tb:
 // column-major b).
-template <bool BF16, int T = 256>
+template <bool BF16, int T = 256, int PF = 0>
 const void* groupedDmaKernel(bool ta, bool tb) {
-    if (ta) return tb ? reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, true, true, T>)
-                      : reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, true, false, T>);
-    return tb ? reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, false, true, T>)
-              : reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, false, false, T>);
+    if (ta) return tb ? reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, true, true, T, PF>)
+                      : reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, true, false, T, PF>);
+    return tb ? reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, false, true, T, PF>)
+              : reinterpret_cast<const void*>(&grouped_half_gemm_dma<BF16, false, false, T, PF>);
 }
 template <bool BF16, bool SPLIT>
 const void* dma128Kernel(bool ta, bool tb) {
@@ -508,12 +540,19 @@ const void* dma64x128Kernel(bool ta, bool tb) {
     return tb ? reinterpret_cast<const void*>(&half_gemm_dma64x128<BF16, true>)
               : reinterpret_cast<const void*>(&half_gemm_dma64x128<BF16, false>);
 }
+// Stages of b a large-b launch prefetches ahead (measured: 2048x114688x4096 bf16 1508-1512 us at 4,
+// 1517-1530 at 2, 1620-1633 without).
+constexpr int kLargeBPrefetch = 4;
+template <bool BF16, int PF = 0>
+const void* dmaKernelFor(bool ta, bool tb) {
+    if (ta) return tb ? reinterpret_cast<const void*>(&half_gemm_dma<BF16, true, true, PF>)
+                      : reinterpret_cast<const void*>(&half_gemm_dma<BF16, true, false, PF>);
+    return tb ? reinterpret_cast<const void*>(&half_gemm_dma<BF16, false, true, PF>)
+              : reinterpret_cast<const void*>(&half_gemm_dma<BF16, false, false, PF>);
+}
 template <bool BF16>
-const void* dmaKernel(bool ta, bool tb) {
-    if (ta) return tb ? reinterpret_cast<const void*>(&half_gemm_dma<BF16, true, true>)
-                      : reinterpret_cast<const void*>(&half_gemm_dma<BF16, true, false>);
-    return tb ? reinterpret_cast<const void*>(&half_gemm_dma<BF16, false, true>)
-              : reinterpret_cast<const void*>(&half_gemm_dma<BF16, false, false>);
+const void* dmaKernel(bool ta, bool tb, bool large_b) {
+    return large_b ? dmaKernelFor<BF16, kLargeBPrefetch>(ta, tb) : dmaKernelFor<BF16>(ta, tb);
 }
 
 }  // namespace ftrain::gemm::ddev

@@ -400,13 +400,16 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
         const bool half    = v_->input != FTRAIN_NUMERIC_TYPE_FP32;
         const bool cd_half = p.d().type != FTRAIN_NUMERIC_TYPE_FP32;
         for (Bucket& bk : buckets_) bk = Bucket{};
+        uint64_t b_bytes[4] = {0, 0, 0, 0};  // every group's b, per bucket: the launch streams them all
         for (uint32_t g = 0; g < p.groups(); ++g) {
             if (p.emptyOutput(g)) continue;
             GemmLaunch l;
             if (const char* why = p.launch(g, l)) raise(FTRAIN_STATUS_UNSUPPORTED, "%s", why);
             // Groups are launched per operand orientation (one kernel
             // instantiation each); a degenerate matrix may read as either.
-            Bucket& bk       = buckets_[(l.ta ? 1 : 0) + (l.tb ? 2 : 0)];
+            const int o      = (l.ta ? 1 : 0) + (l.tb ? 2 : 0);
+            Bucket& bk       = buckets_[o];
+            b_bytes[o] += l.shape.k * l.shape.n * (half ? 2 : 4);
             const gemm::VariantInfo& vi = gemm::info(v_->tile);
             const int32_t tm = int32_t(ceilDiv(l.shape.m, vi.bm)), tn = int32_t(ceilDiv(l.shape.n, vi.bn));
             bk.tile_start.push_back(bk.tiles);
@@ -422,7 +425,8 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
         }
         for (int o = 0; o < 4; ++o)
             if (buckets_[o].tiles > 0) {
-                buckets_[o].kernel  = gemm::groupedKernelFor(v_->input, v_->which, o & 1, o & 2);
+                buckets_[o].kernel  = gemm::groupedKernelFor(v_->input, v_->which, o & 1, o & 2,
+                                                              b_bytes[o] > gemm::kLargeBBytes);
                 buckets_[o].threads = gemm::info(v_->tile).threads;
             }
         table_.reset();

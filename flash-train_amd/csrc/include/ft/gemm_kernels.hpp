@@ -256,7 +256,10 @@ const VariantInfo& info(Variant v);
 // kernelFor: the variant's kernel for a column-major (ta) or row-major a and
 // a column-major (tb) or row-major b; null when that layout is not
 // instantiated for the variant (see VariantInfo::layouts).
-const void* kernelFor(Variant v, bool ta = false, bool tb = false);
+// large_b: b (k x n, every group's together for a grouped launch) takes more than kLargeBBytes;
+// the 256x256 16-bit DMA tiles then prefetch it into L2.
+constexpr uint64_t kLargeBBytes = 256ull << 20;  // the MI355X MALL
+const void* kernelFor(Variant v, bool ta = false, bool tb = false, bool large_b = false);
 // The one-pass skinny kernels (Variant::kGemv, kBf16Gemv, kFp16Gemv) for m
 // rows of a (up to the variant's row limit) and a row-major (ta false) or,
 // fp32 only, column-major a; null otherwise.  `threads` receives the
@@ -291,14 +294,15 @@ const void* groupedDma32Kernel128(bool ta, bool tb);  // grouped 128x128 DMA til
 const void* groupedDma32Kernel64x128(bool tb);        // grouped 64x128 DMA tile, row-major a
 const void* dma32KernelTB(Variant v);  // column-major b
 const void* dma32KernelTA(Variant v, bool tb);  // column-major a
-const void* dmaKernelBf16(bool ta, bool tb);
-const void* dmaKernelFp16(bool ta, bool tb);
+// large_b: the form that prefetches b into L2 ahead of its DMA (for a b larger than the MALL).
+const void* dmaKernelBf16(bool ta, bool tb, bool large_b);
+const void* dmaKernelFp16(bool ta, bool tb, bool large_b);
 const void* dma128KernelBf16(bool ta, bool tb, bool split);
 const void* dma128KernelFp16(bool ta, bool tb, bool split);
 const void* dma64x128KernelBf16(bool ta, bool tb);  // null for a column-major a
 const void* dma64x128KernelFp16(bool ta, bool tb);
-const void* groupedDmaKernelBf16(bool ta, bool tb);
-const void* groupedDmaKernelFp16(bool ta, bool tb);
+const void* groupedDmaKernelBf16(bool ta, bool tb, bool large_b);
+const void* groupedDmaKernelFp16(bool ta, bool tb, bool large_b);
 const void* groupedDma128KernelBf16(bool ta, bool tb);
 const void* groupedDma128KernelFp16(bool ta, bool tb);
 // Grouped kernels: element type (FTRAIN_NUMERIC_TYPE_FP32 / BF16 / FP16),
@@ -306,7 +310,7 @@ const void* groupedDma128KernelFp16(bool ta, bool tb);
 // family's large tile: fp32 16x16x4 256x128, bf16/fp16 256x256; 3 = fp32
 // 16x16x4 128x256) and operand
 // orientation.
-const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool tb);
+const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool tb, bool large_b = false);
 const void* groupedKernelNN(int which);
 const void* groupedKernelTN(int which);
 const void* groupedKernelNT(int which);

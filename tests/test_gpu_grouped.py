@@ -289,3 +289,39 @@ def test_abcd_column_major_weights(capi, oracle):
 
     names = run_all(capi, args, check)
     assert "GroupedFp32Mfma16Gemm_128x128_Dma" in names, names
+
+
+def test_abcd_bf16_large_total_b_exact(capi):
+    """Eight experts whose weights total 302 MB (each 4096 x 4608 bf16):
+    the grouped 256x256 DMA tile then prefetches b into L2.  Integer inputs in [-2, 2] make every
+    fp32 result exact, so each group must equal its fp64 product bit for bit, ragged rows included."""
+    m_list, k, n = [300, 0, 512, 129, 256, 64, 700, 256], 4096, 4608
+    G, M = len(m_list), sum(m_list)
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    a = torch.randint(-2, 3, (M, k), device="cuda", generator=gen).to(torch.bfloat16)
+    b = torch.randint(-2, 3, (G, k, n), device="cuda", generator=gen).to(torch.bfloat16)
+    d = torch.full((M, n), float("nan"), device="cuda")
+    ops = capi.GroupedOps("abcd")
+    al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+    dims = [(m, n) for m in m_list]
+    args = ops.args(a=capi.GroupedSpec(capi.matrix(a), G, dims=[(m, k) for m in m_list]),
+                    b=capi.GroupedSpec(capi.matrix(b.view(G * k, n)), G, dims=[(k, n)] * G),
+                    c=capi.GroupedSpec(capi.View(None, [M, n], numeric_type=capi.TORCH_NUMERIC_TYPES[torch.float32]), G,
+                                       dims=dims),
+                    d=capi.GroupedSpec(capi.matrix(d), G, dims=dims), alpha=al.view, beta=be.view)
+    plan = args.plan()
+    args.close()
+    names = plan.names()
+    i = names.index("GroupedBf16MfmaGemm_256x256_Dma")
+    want, row = [], 0
+    for g, m in enumerate(m_list):
+        want.append((a[row:row + m].double() @ b[g].double()).float())
+        row += m
+    for _ in range(2):
+        d.fill_(float("nan"))
+        plan.execute(i, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        row = 0
+        for g, m in enumerate(m_list):
+            assert torch.equal(d[row:row + m], want[g]), (g, m)
+            row += m

@@ -170,6 +170,37 @@ def test_half_dma_tile_exact_and_repeatable(capi, ops, kind):
 
 
 @pytest.mark.parametrize("kind", ["bf16", "fp16"])
+@pytest.mark.parametrize("lb", [False, True])
+def test_half_dma_tile_prefetching_a_large_b(capi, ops, kind, lb):
+    # A b of more than 256 MiB (4096 x 32776, 268 MB) selects the 256x256 DMA tile's form that
+    # prefetches b into L2 four stages ahead.  Integer inputs in [-2, 2] make the fp32 result exact:
+    # it must equal the fp64 product bit for bit, with an edge tile in m and a last column tile of 8
+    # (the prefetched lines clamped onto the matrix), and b row- or column-major with a padded ld.
+    m, n, k = 384, 32776, 4096
+    gen = torch.Generator(device="cuda").manual_seed(17)
+    a = torch.randint(-2, 3, (m, k), device="cuda", generator=gen).to(DT[kind])
+    b_int = torch.randint(-2, 3, (k, n), device="cuda", generator=gen)
+    if lb:
+        store = torch.full((n, k + 8), float("nan"), dtype=DT[kind], device="cuda")
+        store[:, :k] = b_int.t().to(DT[kind])
+        b = store[:, :k].t()
+    else:
+        store = torch.full((k, n + 8), float("nan"), dtype=DT[kind], device="cuda")
+        store[:, :n] = b_int.to(DT[kind])
+        b = store[:, :n]
+    exact = (a.double() @ b_int.double()).float()
+    del b_int
+    d = torch.empty(m, n, device="cuda")
+    plan = capi.plan_for(a, b, None, d, 1.0, 0.0, ops)
+    i = plan.names().index(f"{kind.capitalize()}MfmaGemm_256x256_Dma")
+    for _ in range(2):
+        d.fill_(float("nan"))
+        plan.execute(i, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert torch.equal(d, exact), (kind, lb, (d - exact).abs().max().item())
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
 @pytest.mark.parametrize("cd", ["fp32", "same"])
 @pytest.mark.parametrize("m,n,k,pad", [(1, 8192, 8192, 0), (2, 200, 1000, 8), (1, 64, 8, 0), (2, 4096, 2056, 0),
                                        (3, 64, 64, 0), (4, 128, 1024, 8), (5, 64, 64, 0)])
