@@ -341,15 +341,19 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
         for (int r = 0; r < NR; ++r) read_one(ga, gb, As, Bs, hf, r);
     };
 
-    // Prologue: stages 0 and 1 in flight (ND DMAs per wave each); wait for stage 0.
+    // Prologue: stages 0 and 1 in flight (ND DMAs per wave each), with prefetch stages 2 .. PF + 1
+    // too; wait for stage 0.  Each wait below then leaves exactly one instruction pending, the
+    // latest prefetch (memory instructions complete in issue order for the counter).
 #pragma unroll
     for (int d = 0; d < ND; ++d) dma_one(0, d, la0, lb0);
+#pragma unroll
+    for (int i = 2; i <= PF; ++i) prefetch(min(i, nst - 1));
     const int st1 = min(1, nst - 1);
 #pragma unroll
     for (int d = 0; d < ND; ++d) dma_one(st1, d, la1, lb1);
-    // With prefetch, each wait below leaves exactly one instruction pending, the latest prefetch.
     prefetch(min(1 + PF, nst - 1));
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(ND + (PF > 0 ? 1 : 0)) : "memory");
+    static_assert(ND + PF <= 63, "the wait count field holds 63");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(ND + PF) : "memory");
     read_half(fa0, fb0, As0, Bs0, 0);
 
     // Stages past the last reload the last one (harmless: nothing reads them).
