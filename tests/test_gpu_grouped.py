@@ -291,15 +291,16 @@ def test_abcd_column_major_weights(capi, oracle):
     assert "GroupedFp32Mfma16Gemm_128x128_Dma" in names, names
 
 
-def test_abcd_bf16_large_total_b_exact(capi):
-    """Eight experts whose weights total 302 MB (each 4096 x 4608 bf16):
+@pytest.mark.parametrize("dtype,dname", [(torch.bfloat16, "Bf16"), (torch.float16, "Fp16")])
+def test_abcd_half_large_total_b_exact(capi, dtype, dname):
+    """Eight experts whose weights total 302 MB (each 4096 x 4608, 16-bit):
     the grouped 256x256 DMA tile then prefetches b into L2.  Integer inputs in [-2, 2] make every
     fp32 result exact, so each group must equal its fp64 product bit for bit, ragged rows included."""
     m_list, k, n = [300, 0, 512, 129, 256, 64, 700, 256], 4096, 4608
     G, M = len(m_list), sum(m_list)
     gen = torch.Generator(device="cuda").manual_seed(31)
-    a = torch.randint(-2, 3, (M, k), device="cuda", generator=gen).to(torch.bfloat16)
-    b = torch.randint(-2, 3, (G, k, n), device="cuda", generator=gen).to(torch.bfloat16)
+    a = torch.randint(-2, 3, (M, k), device="cuda", generator=gen).to(dtype)
+    b = torch.randint(-2, 3, (G, k, n), device="cuda", generator=gen).to(dtype)
     d = torch.full((M, n), float("nan"), device="cuda")
     ops = capi.GroupedOps("abcd")
     al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
@@ -312,7 +313,7 @@ def test_abcd_bf16_large_total_b_exact(capi):
     plan = args.plan()
     args.close()
     names = plan.names()
-    i = names.index("GroupedBf16MfmaGemm_256x256_Dma")
+    i = names.index(f"Grouped{dname}MfmaGemm_256x256_Dma")
     want, row = [], 0
     for g, m in enumerate(m_list):
         want.append((a[row:row + m].double() @ b[g].double()).float())
