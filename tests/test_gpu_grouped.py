@@ -292,11 +292,14 @@ def test_abcd_column_major_weights(capi, oracle):
 
 
 @pytest.mark.parametrize("dtype,dname", [(torch.bfloat16, "Bf16"), (torch.float16, "Fp16")])
-def test_abcd_half_large_total_b_exact(capi, dtype, dname):
-    """Eight experts whose weights total 302 MB (each 4096 x 4608, 16-bit):
-    the grouped 256x256 DMA tile then prefetches b into L2.  Integer inputs in [-2, 2] make every
-    fp32 result exact, so each group must equal its fp64 product bit for bit, ragged rows included."""
-    m_list, k, n = [300, 0, 512, 129, 256, 64, 700, 256], 4096, 4608
+@pytest.mark.parametrize("b_col_major", [False, True])
+def test_abcd_half_large_total_b_exact(capi, dtype, dname, b_col_major):
+    """Eight experts whose weights total 302 MB (each 4096 x 4616, 16-bit, row-major or stored as
+    nn.Linear keeps them): the grouped 256x256 DMA tile then prefetches b into L2.  n = 18 * 256 + 8
+    leaves a last column tile of 8 (prefetched lines clamped onto the matrix).  Integer inputs in
+    [-2, 2] make every fp32 result exact, so each group must equal its fp64 product bit for bit,
+    ragged rows included."""
+    m_list, k, n = [300, 0, 512, 129, 256, 64, 700, 256], 4096, 4616
     G, M = len(m_list), sum(m_list)
     gen = torch.Generator(device="cuda").manual_seed(31)
     a = torch.randint(-2, 3, (M, k), device="cuda", generator=gen).to(dtype)
@@ -305,8 +308,13 @@ def test_abcd_half_large_total_b_exact(capi, dtype, dname):
     ops = capi.GroupedOps("abcd")
     al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
     dims = [(m, n) for m in m_list]
-    args = ops.args(a=capi.GroupedSpec(capi.matrix(a), G, dims=[(m, k) for m in m_list]),
-                    b=capi.GroupedSpec(capi.matrix(b.view(G * k, n)), G, dims=[(k, n)] * G),
+    if b_col_major:
+        w = b.transpose(1, 2).contiguous()  # storage of b_g^T, n x k per group
+        bspec = capi.GroupedSpec(capi.matrix(w.view(G * n, k)), G, dims=[(k, n)] * G, strides=[(1, k)] * G,
+                                 offsets=[g * n * k for g in range(G)])
+    else:
+        bspec = capi.GroupedSpec(capi.matrix(b.view(G * k, n)), G, dims=[(k, n)] * G)
+    args = ops.args(a=capi.GroupedSpec(capi.matrix(a), G, dims=[(m, k) for m in m_list]), b=bspec,
                     c=capi.GroupedSpec(capi.View(None, [M, n], numeric_type=capi.TORCH_NUMERIC_TYPES[torch.float32]), G,
                                        dims=dims),
                     d=capi.GroupedSpec(capi.matrix(d), G, dims=dims), alpha=al.view, beta=be.view)
@@ -318,6 +326,8 @@ def test_abcd_half_large_total_b_exact(capi, dtype, dname):
     for g, m in enumerate(m_list):
         want.append((a[row:row + m].double() @ b[g].double()).float())
         row += m
+    if b_col_major:
+        del b
     for _ in range(2):
         d.fill_(float("nan"))
         plan.execute(i, torch.cuda.current_stream().cuda_stream)
