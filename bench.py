@@ -607,7 +607,7 @@ def main() -> None:
             log(f"config {name}")
             configs.append(run_config(name, steps, all_primitives=name in PRIMITIVE_MATRIX))
         # Grouped GEMM (mixture-of-experts forward) and bf16 inputs on the BASELINE shapes.
-        for name, steps in (("square_8192", 20), ("mlp_fwd", 20), ("skinny_64x4096x4096", 200)):
+        for name, steps in (("square_8192", 50), ("mlp_fwd", 50), ("skinny_64x4096x4096", 200)):
             log(f"config {name} bf16")
             configs.append(run_config(name, steps, dtype="bf16", all_primitives=True))
         for experts in (8, 64):
