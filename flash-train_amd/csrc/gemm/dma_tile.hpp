@@ -558,8 +558,8 @@ const void* dmaKernelFor(bool ta, bool tb) {
               : reinterpret_cast<const void*>(&half_gemm_dma<BF16, false, false, PF>);
 }
 template <bool BF16>
-const void* dmaKernel(bool ta, bool tb, bool large_b) {
-    return large_b ? dmaKernelFor<BF16, kLargeBPrefetch>(ta, tb) : dmaKernelFor<BF16>(ta, tb);
+const void* dmaKernel(bool ta, bool tb, bool prefetch_b) {
+    return prefetch_b ? dmaKernelFor<BF16, kLargeBPrefetch>(ta, tb) : dmaKernelFor<BF16>(ta, tb);
 }
 
 }  // namespace ftrain::gemm::ddev

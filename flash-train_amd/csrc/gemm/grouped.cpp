@@ -400,7 +400,9 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
         const bool half    = v_->input != FTRAIN_NUMERIC_TYPE_FP32;
         const bool cd_half = p.d().type != FTRAIN_NUMERIC_TYPE_FP32;
         for (Bucket& bk : buckets_) bk = Bucket{};
-        uint64_t b_bytes[4] = {0, 0, 0, 0};  // every group's b, per bucket: the launch streams them all
+        // Per bucket: every group's b (the launch streams them all), the deepest k, the tile rows and
+        // the groups, for the L2 prefetch of b (gemm::prefetchB).
+        uint64_t b_bytes[4] = {0, 0, 0, 0}, max_k[4] = {0, 0, 0, 0}, tile_rows[4] = {0, 0, 0, 0}, groups[4] = {0, 0, 0, 0};
         for (uint32_t g = 0; g < p.groups(); ++g) {
             if (p.emptyOutput(g)) continue;
             GemmLaunch l;
@@ -410,8 +412,11 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
             const int o      = (l.ta ? 1 : 0) + (l.tb ? 2 : 0);
             Bucket& bk       = buckets_[o];
             b_bytes[o] += l.shape.k * l.shape.n * (half ? 2 : 4);
+            max_k[o] = std::max<uint64_t>(max_k[o], l.shape.k);
             const gemm::VariantInfo& vi = gemm::info(v_->tile);
             const int32_t tm = int32_t(ceilDiv(l.shape.m, vi.bm)), tn = int32_t(ceilDiv(l.shape.n, vi.bn));
+            tile_rows[o] += uint64_t(tm);
+            groups[o] += 1;
             bk.tile_start.push_back(bk.tiles);
             bk.tiles += int32_t(groupSlots(uint64_t(tm) * uint64_t(tn)));
             const int32_t m = int32_t(l.shape.m), n = int32_t(l.shape.n), k = int32_t(l.shape.k);
@@ -426,7 +431,8 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
         for (int o = 0; o < 4; ++o)
             if (buckets_[o].tiles > 0) {
                 buckets_[o].kernel  = gemm::groupedKernelFor(v_->input, v_->which, o & 1, o & 2,
-                                                              b_bytes[o] > gemm::kLargeBBytes);
+                                                              gemm::prefetchB(b_bytes[o], max_k[o],
+                                                                              double(tile_rows[o]) / double(groups[o])));
                 buckets_[o].threads = gemm::info(v_->tile).threads;
             }
         table_.reset();

@@ -411,7 +411,7 @@ const void* gemvKernel(Variant v, int m, bool ta, int& threads) {
     return ta ? reinterpret_cast<const void*>(&gemv_pass<8, 2, 8, true>) : reinterpret_cast<const void*>(&gemv_pass<8, 2, 8, false>);
 }
 
-const void* kernelFor(Variant v, bool ta, bool tb, bool large_b) {
+const void* kernelFor(Variant v, bool ta, bool tb, bool prefetch_b) {
     if (info(v).gemv && info(v).split == SplitKind::kNone) {
         if (tb) return nullptr;
         int threads = 0;
@@ -432,8 +432,8 @@ const void* kernelFor(Variant v, bool ta, bool tb, bool large_b) {
         return table[i / kHalfTiles][(ta ? 1 : 0) + (tb ? 2 : 0)](tile);
     }
     if (v >= Variant::kMfma16Dma256x256 && v <= Variant::kMfma16Dma128x64) return ta ? dma32KernelTA(v, tb) : tb ? dma32KernelTB(v) : dma32Kernel(v);
-    if (v == Variant::kBf16MfmaDma256x256) return dmaKernelBf16(ta, tb, large_b);
-    if (v == Variant::kFp16MfmaDma256x256) return dmaKernelFp16(ta, tb, large_b);
+    if (v == Variant::kBf16MfmaDma256x256) return dmaKernelBf16(ta, tb, prefetch_b);
+    if (v == Variant::kFp16MfmaDma256x256) return dmaKernelFp16(ta, tb, prefetch_b);
     if (v == Variant::kBf16MfmaDma128x128 || v == Variant::kBf16MfmaDma128x128S)
         return dma128KernelBf16(ta, tb, v == Variant::kBf16MfmaDma128x128S);
     if (v == Variant::kFp16MfmaDma128x128 || v == Variant::kFp16MfmaDma128x128S)
@@ -465,7 +465,7 @@ const void* kernelFor(Variant v, bool ta, bool tb, bool large_b) {
 
 const void* groupedKernelNN(int which) { return groupedLayoutKernel<false, false>(which); }
 
-const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool tb, bool large_b) {
+const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool tb, bool prefetch_b) {
     using Fn                        = const void* (*)(int);
     static constexpr Fn table[3][4] = {
         {groupedKernelNN, groupedKernelTN, groupedKernelNT, groupedKernelTT},
@@ -474,7 +474,7 @@ const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool t
     const int t = input == FTRAIN_NUMERIC_TYPE_FP32 ? 0 : input == FTRAIN_NUMERIC_TYPE_BF16 ? 1 : 2;
     const int o = (ta ? 1 : 0) + (tb ? 2 : 0);
     if (t != 0 && which == 3)
-        return t == 1 ? groupedDmaKernelBf16(ta, tb, large_b) : groupedDmaKernelFp16(ta, tb, large_b);
+        return t == 1 ? groupedDmaKernelBf16(ta, tb, prefetch_b) : groupedDmaKernelFp16(ta, tb, prefetch_b);
     if (t != 0 && which == 4) return t == 1 ? groupedDma128KernelBf16(ta, tb) : groupedDma128KernelFp16(ta, tb);
     if (t == 0 && which == 4) return ta || tb ? nullptr : groupedDma32Kernel();
     if (t == 0 && which == 5) return groupedDma32Kernel128(ta, tb);

@@ -3,10 +3,10 @@
 
 namespace ftrain::gemm {
 
-const void* dmaKernelBf16(bool ta, bool tb, bool large_b) { return ddev::dmaKernel<true>(ta, tb, large_b); }
+const void* dmaKernelBf16(bool ta, bool tb, bool prefetch_b) { return ddev::dmaKernel<true>(ta, tb, prefetch_b); }
 
-const void* groupedDmaKernelBf16(bool ta, bool tb, bool large_b) {
-    return large_b ? ddev::groupedDmaKernel<true, 256, ddev::kLargeBPrefetch>(ta, tb) : ddev::groupedDmaKernel<true>(ta, tb);
+const void* groupedDmaKernelBf16(bool ta, bool tb, bool prefetch_b) {
+    return prefetch_b ? ddev::groupedDmaKernel<true, 256, ddev::kLargeBPrefetch>(ta, tb) : ddev::groupedDmaKernel<true>(ta, tb);
 }
 
 const void* groupedDma128KernelBf16(bool ta, bool tb) { return ddev::groupedDmaKernel<true, 128>(ta, tb); }

@@ -3,10 +3,10 @@
 
 namespace ftrain::gemm {
 
-const void* dmaKernelFp16(bool ta, bool tb, bool large_b) { return ddev::dmaKernel<false>(ta, tb, large_b); }
+const void* dmaKernelFp16(bool ta, bool tb, bool prefetch_b) { return ddev::dmaKernel<false>(ta, tb, prefetch_b); }
 
-const void* groupedDmaKernelFp16(bool ta, bool tb, bool large_b) {
-    return large_b ? ddev::groupedDmaKernel<false, 256, ddev::kLargeBPrefetch>(ta, tb) : ddev::groupedDmaKernel<false>(ta, tb);
+const void* groupedDmaKernelFp16(bool ta, bool tb, bool prefetch_b) {
+    return prefetch_b ? ddev::groupedDmaKernel<false, 256, ddev::kLargeBPrefetch>(ta, tb) : ddev::groupedDmaKernel<false>(ta, tb);
 }
 
 const void* groupedDma128KernelFp16(bool ta, bool tb) { return ddev::groupedDmaKernel<false, 128>(ta, tb); }

@@ -212,9 +212,9 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
         wide_ = WideParams{a, b, c, d, alpha, beta, s.m, s.n, s.k, a_rs, a_cs, b_rs, b_cs, g.ldc, g.ldd};
 
         int threads = info_->threads;
-        const bool large_b = s.k * s.n * (half_ ? 2 : 4) > gemm::kLargeBBytes;
+        const bool prefetch_b = gemm::prefetchB(s.k * s.n * (half_ ? 2 : 4), s.k);
         kernel_     = info_->gemv && info_->split == SplitKind::kNone ? gemm::gemvKernel(v_, int(s.m), g.ta, threads)
-                                                                  : gemm::kernelFor(v_, g.ta, g.tb, large_b);
+                                                                  : gemm::kernelFor(v_, g.ta, g.tb, prefetch_b);
         checkBlockSize(kernel_, threads, info_->name);
         block_  = dim3(threads);
         if (info_->simt) {

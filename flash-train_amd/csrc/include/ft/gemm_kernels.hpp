@@ -256,10 +256,9 @@ const VariantInfo& info(Variant v);
 // kernelFor: the variant's kernel for a column-major (ta) or row-major a and
 // a column-major (tb) or row-major b; null when that layout is not
 // instantiated for the variant (see VariantInfo::layouts).
-// large_b: b (k x n, every group's together for a grouped launch) takes more than kLargeBBytes;
-// the 256x256 16-bit DMA tiles then prefetch it into L2.
-constexpr uint64_t kLargeBBytes = 256ull << 20;  // the MI355X MALL
-const void* kernelFor(Variant v, bool ta = false, bool tb = false, bool large_b = false);
+// prefetch_b: the 256x256 16-bit DMA tiles take their form that prefetches b into L2 ahead of its
+// DMA (prefetchB decides).
+const void* kernelFor(Variant v, bool ta = false, bool tb = false, bool prefetch_b = false);
 // The one-pass skinny kernels (Variant::kGemv, kBf16Gemv, kFp16Gemv) for m
 // rows of a (up to the variant's row limit) and a row-major (ta false) or,
 // fp32 only, column-major a; null otherwise.  `threads` receives the
@@ -294,15 +293,15 @@ const void* groupedDma32Kernel128(bool ta, bool tb);  // grouped 128x128 DMA til
 const void* groupedDma32Kernel64x128(bool tb);        // grouped 64x128 DMA tile, row-major a
 const void* dma32KernelTB(Variant v);  // column-major b
 const void* dma32KernelTA(Variant v, bool tb);  // column-major a
-// large_b: the form that prefetches b into L2 ahead of its DMA (for a b larger than the MALL).
-const void* dmaKernelBf16(bool ta, bool tb, bool large_b);
-const void* dmaKernelFp16(bool ta, bool tb, bool large_b);
+// prefetch_b: the form that prefetches b into L2 ahead of its DMA.
+const void* dmaKernelBf16(bool ta, bool tb, bool prefetch_b);
+const void* dmaKernelFp16(bool ta, bool tb, bool prefetch_b);
 const void* dma128KernelBf16(bool ta, bool tb, bool split);
 const void* dma128KernelFp16(bool ta, bool tb, bool split);
 const void* dma64x128KernelBf16(bool ta, bool tb);  // null for a column-major a
 const void* dma64x128KernelFp16(bool ta, bool tb);
-const void* groupedDmaKernelBf16(bool ta, bool tb, bool large_b);
-const void* groupedDmaKernelFp16(bool ta, bool tb, bool large_b);
+const void* groupedDmaKernelBf16(bool ta, bool tb, bool prefetch_b);
+const void* groupedDmaKernelFp16(bool ta, bool tb, bool prefetch_b);
 const void* groupedDma128KernelBf16(bool ta, bool tb);
 const void* groupedDma128KernelFp16(bool ta, bool tb);
 // Grouped kernels: element type (FTRAIN_NUMERIC_TYPE_FP32 / BF16 / FP16),
@@ -310,7 +309,20 @@ const void* groupedDma128KernelFp16(bool ta, bool tb);
 // family's large tile: fp32 16x16x4 256x128, bf16/fp16 256x256; 3 = fp32
 // 16x16x4 128x256) and operand
 // orientation.
-const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool tb, bool large_b = false);
+const void* groupedKernelFor(FTrainNumericType input, int which, bool ta, bool tb, bool prefetch_b = false);
+
+// When the 256x256 16-bit DMA tiles prefetch b into L2 (bf16, MI355X, against the same tile
+// without it): b (every group's together for a grouped launch) larger than the 256 MB MALL, and k
+// at most kPrefetchMaxK; a grouped launch also needs at least a band of 8 tile rows per group on
+// average.  Measured: plain 2048x114688x4096 -8%, 4096x65536x4096 -7.5%, 1024x131072x4096 -9.5%,
+// 8192x32768x4096, 16384x16384x8192 and 8192x65536x2048 within 1%, but 4096x4096x65536 +4%;
+// grouped 8 experts of 2048 rows (k 4096) -1 to -2.5%, 16 or more experts (4 tile rows or fewer
+// each) +2 to +35%, 8 experts of 4096 rows at k 14336 +5%.
+constexpr uint64_t kLargeBBytes  = 256ull << 20;
+constexpr uint64_t kPrefetchMaxK = 8192;
+inline bool prefetchB(uint64_t b_bytes, uint64_t max_k, double tile_rows_per_group = 8.0) {
+    return b_bytes > kLargeBBytes && max_k <= kPrefetchMaxK && tile_rows_per_group >= 8.0;
+}
 const void* groupedKernelNN(int which);
 const void* groupedKernelTN(int which);
 const void* groupedKernelNT(int which);

@@ -295,11 +295,11 @@ def test_abcd_column_major_weights(capi, oracle):
 @pytest.mark.parametrize("b_col_major", [False, True])
 def test_abcd_half_large_total_b_exact(capi, dtype, dname, b_col_major):
     """Eight experts whose weights total 302 MB (each 4096 x 4616, 16-bit, row-major or stored as
-    nn.Linear keeps them): the grouped 256x256 DMA tile then prefetches b into L2.  n = 18 * 256 + 8
-    leaves a last column tile of 8 (prefetched lines clamped onto the matrix).  Integer inputs in
-    [-2, 2] make every fp32 result exact, so each group must equal its fp64 product bit for bit,
-    ragged rows included."""
-    m_list, k, n = [300, 0, 512, 129, 256, 64, 700, 256], 4096, 4616
+    nn.Linear keeps them) and at least 8 tile rows each: the grouped 256x256 DMA tile then prefetches
+    b into L2.  n = 18 * 256 + 8 leaves a last column tile of 8 (prefetched lines clamped onto the
+    matrix).  Integer inputs in [-2, 2] make every fp32 result exact, so each group must equal its
+    fp64 product bit for bit, ragged rows and an empty group included."""
+    m_list, k, n = [2085, 0, 2100, 1999, 2300, 2048, 2200, 1900, 2171], 4096, 4616
     G, M = len(m_list), sum(m_list)
     gen = torch.Generator(device="cuda").manual_seed(31)
     a = torch.randint(-2, 3, (M, k), device="cuda", generator=gen).to(dtype)
