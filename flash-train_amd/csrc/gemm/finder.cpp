@@ -54,6 +54,7 @@ constexpr double kFusedStoreMicros    = 2.0;  // per round: a split workgroup's 
 // stores, the ramp of the first stages); fitted with the catalog efficiencies.
 constexpr double kRoundMicros     = 3.35;
 constexpr double kTieWeight       = 1e-3;
+constexpr double kCuBytesPerMicro = 6.4e4;  // one CU's sustained load rate (about 27 bytes per clock)
 constexpr uint64_t kMinSplitDepth = 256;  // reduction depth worth one split-k workgroup
 constexpr uint64_t kMinGemvDepth  = 64;
 
@@ -113,10 +114,13 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
         // Too few waves cannot reach the HBM peak; about four per CU do
         // (measured with the one-pass kernel: 1024 waves over 256 CUs stream
         // 5.4-6.3 TB/s, 256 waves lose to split-k).
+        // A CU also loads at a bounded rate, so a launch of few workgroups is bound by the bytes each
+        // one reads (bf16 1x4096x4096, 64 workgroups of 512 KiB: 9.0 us).
         const int threads = vi.split == SplitKind::kNone ? gemvPassThreads(int(std::max<uint64_t>(s.m, 1))) : vi.threads;
         const double wgs  = double(ceilDiv(std::max<uint64_t>(s.n, 1), uint64_t(vi.bn)) * splits);
         const double fill = std::min(1.0, wgs * (threads / 64) / (double(cus) * 4.0));
-        return bytes / (kHbmBytesPerMicro * fill) + serial_us + launch;
+        const double per_cu = std::ceil(wgs / double(cus)) * bytes / wgs;
+        return std::max(bytes / (kHbmBytesPerMicro * fill), per_cu / kCuBytesPerMicro) + serial_us + launch;
     }
     // Work per workgroup includes the tile padding at the m/n edges.  The
     // dispatcher refills a CU as soon as one of its workgroups retires, so a

@@ -118,9 +118,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_pass_half(HalfGemmParams p) {
 
 template <bool BF16>
 const void* pick(int m) {
+    static_assert(kGemvHalfRows == 2, "one kernel per row count");
     if (m <= 1) return reinterpret_cast<const void*>(&gemv_pass_half<BF16, 8, 2, 1>);
-    if (m <= 2) return reinterpret_cast<const void*>(&gemv_pass_half<BF16, 16, 2, 2>);
-    return reinterpret_cast<const void*>(&gemv_pass_half<BF16, 16, 2, 4>);
+    return reinterpret_cast<const void*>(&gemv_pass_half<BF16, 16, 2, 2>);
 }
 
 }  // namespace

@@ -115,10 +115,11 @@ constexpr int kGemvCols = 256;
 // row): fp32 and 16-bit inputs.
 constexpr int kGemvPassCols = 32;
 constexpr int kGemvHalfCols = 64;
-// Rows of a the 16-bit one-pass kernel takes (measured at 8192^2 against the
-// split-k 128x128 tile: one, two and four rows 23.5 / 25.0 / 31.0 us against
-// 34.3-34.7; eight rows 38.3 against 35.7).
-constexpr int kGemvHalfRows = 4;
+// Rows of a the 16-bit one-pass kernel takes.  Measured on MI355X, bf16, us, against the
+// 64x128 DMA split-k tile: one row 9.0 / 4.6 / 23.9 against 9.1 / 7.3 / 25.4 (4096^2, 2048^2,
+// 8192^2), two rows 10.7 / 5.8 / 26.2 against 9.1 / 7.2 / 25.8, four rows 17.9 / 10.1 / 31.0
+// against 9.2 / 7.5 / 26.5.
+constexpr int kGemvHalfRows = 2;
 
 enum class Variant : int {
     // v_mfma_f32_16x16x4_f32 256x256 tiles, 4 waves of 128x128 (one per

@@ -630,14 +630,20 @@ def test_finder_choices_for_the_baseline_configs(tlib):
 
 
 def test_finder_choices_for_16_bit_skinny_m(tlib):
-    # bf16, MI355X (us): 1x8192x8192 Bf16Gemv 23.5 against the split-k 128x128 tile 34.3; 2 and 4 rows
-    # 25.0 / 31.0 against 34.1-34.7; at 8 rows it ties (38.3 against 35.7) and is limited to 4 rows.
+    # bf16, MI355X (us): the one-pass kernel against the 64x128 DMA split-k tile: one row 23.9 / 4.6 /
+    # 3.9 against 25.4 / 7.3 / 7.3 (8192^2, 2048^2, 1x4096x1024), two rows 26.2 / 5.8 against 25.8 /
+    # 7.2; four rows 31.0 / 17.9 against 26.5 / 9.2 (8192^2, 4096^2), so it takes at most two rows.
+    # 64 workgroups (4096 columns) are bound by what each CU loads: 1x4096x4096 ties (9.0 against 9.1).
     for t in (c.BF16, c.FP16):
         name = "Bf16Gemv" if t == c.BF16 else "Fp16Gemv"
+        tile = "Bf16MfmaGemm_64x128_Dma_SplitK" if t == c.BF16 else "Fp16MfmaGemm_64x128_Dma_SplitK"
         assert rank(tlib, 1, 8192, 8192, ab_type=t)[0] == name
-        assert rank(tlib, 2, 8192, 8192, ab_type=t)[0] == name
-        assert rank(tlib, 4, 8192, 8192, ab_type=t)[0] == name
-        assert name not in rank(tlib, 5, 8192, 8192, ab_type=t)
+        assert rank(tlib, 1, 2048, 2048, ab_type=t)[0] == name
+        assert rank(tlib, 2, 2048, 2048, ab_type=t)[0] == name
+        assert rank(tlib, 1, 4096, 1024, ab_type=t)[0] == name
+        assert rank(tlib, 1, 4096, 4096, ab_type=t)[0] in (name, tile)
+        assert name not in rank(tlib, 3, 8192, 8192, ab_type=t)
+        assert rank(tlib, 4, 4096, 4096, ab_type=t)[0] == tile
 
 
 def test_finder_choices_for_16_bit_tiles(tlib):
