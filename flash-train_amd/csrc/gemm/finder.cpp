@@ -120,7 +120,13 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
         const double wgs  = double(ceilDiv(std::max<uint64_t>(s.n, 1), uint64_t(vi.bn)) * splits);
         const double fill = std::min(1.0, wgs * (threads / 64) / (double(cus) * 4.0));
         const double per_cu = std::ceil(wgs / double(cus)) * bytes / wgs;
-        return std::max(bytes / (kHbmBytesPerMicro * fill), per_cu / kCuBytesPerMicro) + serial_us + launch;
+        const double t      = std::max(bytes / (kHbmBytesPerMicro * fill), per_cu / kCuBytesPerMicro) + serial_us + launch;
+        // The split-k skinny kernel keeps few loads in flight per wave and runs well below the
+        // streaming model, more so with more rows of a (measured on MI355X, us, model in brackets:
+        // 1x1024x4096 11.9 [8.7], 4x1024x4096 16.5 [8.9], 8x1024x8192 40.1 [12.0], 1x4096x4096 28.4
+        // [16.5], 8x4096x4096 68.3 [17.2]); it lost to the one-pass kernel or a DMA split-k tile on
+        // every shape measured (1x1024x4096 one-pass 6.7, 8x1024x8192 64x128 DMA split-k 13.4).
+        return vi.split == SplitKind::kPartial ? t * (1.5 + double(std::min<uint64_t>(s.m, 8)) / 4.0) : t;
     }
     // Work per workgroup includes the tile padding at the m/n edges.  The
     // dispatcher refills a CU as soon as one of its workgroups retires, so a

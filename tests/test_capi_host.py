@@ -611,10 +611,15 @@ def test_finder_choices_for_the_baseline_configs(tlib):
     # GEMV: the one-pass kernel (37.8 us) against split-k plus its reduction (47.6 us).
     assert rank(tlib, 1, 8192, 8192)[0] == "Fp32Gemv"
     # It also wins with 128 (1x4096x8192: 24.8 against 39.2 us) and 64 workgroups of 16 waves
-    # (2x2048x4096: 10.7 against 14.7); with 32 workgroups of 8 waves split-k wins (14.3 against 16.5).
+    # (2x2048x4096: 11.0 against 13.1 for the 64x128 DMA split-k tile), and with fewer workgroups
+    # over a short k (1x1024x4096: 6.7 against 9.5 for the 64x64 DMA split-k tile).  The split-k
+    # skinny kernel lost everywhere it was measured: 1x1024x8192 19.1 against 13.1 for the 64x128
+    # DMA split-k tile, 8x1024x8192 40.1 against 13.4.
     assert rank(tlib, 1, 4096, 8192)[0] == "Fp32Gemv"
     assert rank(tlib, 2, 2048, 4096)[0] == "Fp32Gemv"
-    assert rank(tlib, 1, 1024, 8192)[0] == "Fp32Gemv_SplitK"
+    assert rank(tlib, 1, 1024, 4096)[0] == "Fp32Gemv"
+    assert rank(tlib, 1, 1024, 8192)[0].endswith("_Dma_SplitK")
+    assert rank(tlib, 8, 1024, 8192)[0].endswith("_Dma_SplitK")
     # Skinny and deep k (model-chosen split counts): 64x4096x4096: DMA 64x64 split-k 26.7, 64x128
     # 27.0, 64x256 28.6, deep-k 29.0; 4096x64x4096: DMA 64x64 split-k 25.6, 128x64 26.7, 256x64
     # 29.2; 256x256x65536: DMA 128x64 split-k 66.2, 64x128 66.4, 64x64 68.1, 256x64 75.2;
