@@ -613,8 +613,9 @@ def main() -> None:
         for experts in (8, 64):
             log(f"config grouped mlp_fwd over {experts} experts")
             configs.append(grouped_core("mlp_fwd", experts, "fp32", steps=10, warmup=2))
-        log("config grouped mlp_fwd over 8 experts bf16")
-        configs.append(grouped_core("mlp_fwd", 8, "bf16", steps=20, warmup=2))
+        for experts in (8, 64):
+            log(f"config grouped mlp_fwd over {experts} experts bf16")
+            configs.append(grouped_core("mlp_fwd", experts, "bf16", steps=20, warmup=2))
         result["configs"] = configs
         log("reference benchmark shapes")
         result["reference_suite"] = reference_suite()
