@@ -170,7 +170,8 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    auto main_loop = [&](auto checked_tag) {
+    // Stages [k_lo, k_lo + n_st * BK), the last one cut at kend.
+    auto main_loop = [&](auto checked_tag, const int k_lo, const int n_st) {
         constexpr bool CHECKED = decltype(checked_tag)::value;
         // m / n index of a load.  The unchecked loop clamps it into the matrix
         // (a vector of `run` elements stays inside): an edge tile then reads
@@ -298,14 +299,14 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
         constexpr int FIRST = TA ? NM / 2 : NM * 7 / 8;
         floatx4 av[2][TM][KS / 4];
         float bv[2][KS][TN];
-        auto clamp_k0 = [&](int stage) { return kbeg + min(stage, nst - 1) * BK; };
-        if (nst > 0) {
-            load_stage(kbeg);
+        auto clamp_k0 = [&](int stage) { return k_lo + min(stage, n_st - 1) * BK; };
+        if (n_st > 0) {
+            load_stage(k_lo);
             store_stage(0);
             load_stage(clamp_k0(1));
         }
         __syncthreads();
-        if (nst > 0) {
+        if (n_st > 0) {
             read_a(0, av[0]);
             read_b(0, bv[0]);
         }
@@ -332,7 +333,7 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
             __builtin_amdgcn_sched_barrier(0);
         };
         if constexpr (SIMPLE) {
-            for (int st = 0; st < nst; ++st) {
+            for (int st = 0; st < n_st; ++st) {
                 read_a(st & 1, av[0]);
                 read_b(st & 1, bv[0]);
                 mfmas(av[0], bv[0], 0, NM);
@@ -341,7 +342,7 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
                 __syncthreads();
             }
         } else {
-            for (int st = 0; st < nst; ++st) {
+            for (int st = 0; st < n_st; ++st) {
                 iteration(st, av[0], bv[0], av[1], bv[1]);
                 // Rotate the register sets by copying (the allocator coalesces
                 // the copies; swapping references across an unrolled pair made
@@ -358,10 +359,21 @@ __device__ __forceinline__ void mfma16_gemm_tile(const GemmParams& p, int bid, i
         }
     };
 
-    if ((kend - kbeg) % BK == 0)
-        main_loop(std::false_type{});
-    else
-        main_loop(std::true_type{});
+    // A k tail: the whole stages run the unchecked loop and the last, partial one a checked pass of
+    // its own (zeros past kend) instead of checking every stage.  The split-k tiles keep one
+    // checked loop (a second loop copy made the 256x256 one spill registers).
+    const int full = (kend - kbeg) / BK;
+    if (full == nst) {
+        main_loop(std::false_type{}, kbeg, nst);
+    } else if constexpr (SPLIT != kWhole) {
+        main_loop(std::true_type{}, kbeg, nst);
+    } else {
+        if (full > 0) {
+            main_loop(std::false_type{}, kbeg, full);
+            __syncthreads();  // the checked pass rewrites the LDS buffers the last stage read
+        }
+        main_loop(std::true_type{}, kbeg + full * BK, 1);
+    }
 
     // Epilogue: block (bi, bj) register r is D[row 4g + r][col (bj/4)*64 +
     // 4*j16 + bj%4]: run q of the lane is bj = 4q .. 4q+3.
