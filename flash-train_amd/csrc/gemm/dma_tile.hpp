@@ -177,7 +177,28 @@ struct Operand {
             dma_1k(row * ld2 + chunk16, base + (size_t)st * kStageK * 2, lds + (wave + 4 * j) * 1024);
         }
     }
+    // What DMA j of stage st would write to the stage buffer `stage`, by an ordinary load and LDS
+    // store, with zeros for the lanes whose k (within the stage) is k_left or more: the partial last
+    // stage of a k tail.  Those lanes load nothing (their address may lie past the matrix).
+    __device__ __forceinline__ void fill(int st, int j, u16* stage, int wave, int lane, int k_left) const {
+        const char* src;
+        bool ok;
+        if constexpr (TR) {
+            ok  = kRpd * (wave + 4 * j) + lane / kCpr < k_left;
+            src = base + ((size_t)st * kStageK + 4 * kRpd * j) * ld * 2 + voff;
+        } else {
+            ok  = int(chunk16 / 2) < k_left;  // the chunk's first k; k is a multiple of 8
+            src = base + (size_t)st * kStageK * 2 + min(r8 + 32u * j, last) * ld2 + chunk16;
+        }
+        u32x4 v = u32x4{0u, 0u, 0u, 0u};
+        if (ok) v = *reinterpret_cast<const u32x4*>(src);
+        *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(stage) + (wave + 4 * j) * 1024 + 16 * lane) = v;
+    }
 };
+
+// What the DMA pipeline reads when k holds no whole stage (its data is discarded): operands
+// initialised on it with a leading dimension of 0 keep every lane's offset within 512 bytes.
+static __device__ __attribute__((aligned(256))) u16 dma_dummy[512];
 
 // Output tile `bid` of p (tile_of order), k split z when SPLIT; the whole workgroup calls it.
 // T: tile size (256: waves of 128x128, one workgroup per CU; 128: waves of 64x64, two per CU).
@@ -206,7 +227,10 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
     const int m0 = tm * BM, n0 = tn * T;
     const int M = p.m, N = p.n;
     const int kbeg = SPLIT ? z * p.k_chunk : 0;
-    const int nst  = ((SPLIT ? min(p.k, kbeg + p.k_chunk) : p.k) - kbeg) / kStageK;
+    const int kend = SPLIT ? min(p.k, kbeg + p.k_chunk) : p.k;
+    // Whole stages go through the DMA pipeline; a partial last one (k_tail) is staged afterwards.
+    const int nst    = (kend - kbeg) / kStageK;
+    const int k_tail = (kend - kbeg) - nst * kStageK;
 
     // A split's operands start at k = kbeg: a k-contiguous operand's rows advance by kbeg
     // elements, a transposed one's by kbeg rows.
@@ -216,6 +240,12 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
     Operand<B_TR, T> opb;
     opa.init(pa, p.lda, m0, M, wave, lane);
     opb.init(pb, p.ldb, n0, N, wave, lane);
+    // Last stage index the DMAs clamp to; with no whole stage the pipeline runs on the dummy.
+    const int last_st = nst > 0 ? nst - 1 : 0;
+    if (nst == 0) {
+        opa.init(dma_dummy, 0, 0, BM, wave, lane);
+        opb.init(dma_dummy, 0, 0, T, wave, lane);
+    }
     // L2 prefetch of b: one DMA per wave per stage, each lane touching one 128-byte line of the
     // stage's b tile (256 lines at T = 256), into a 1 KiB sink per wave that nothing reads.  Lines
     // past the matrix are clamped onto its last column (row-major b) or column (column-major b).
@@ -234,6 +264,10 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
         } else {  // column-major b: T columns of 64 k, one line each
             pf_voff = static_cast<unsigned>((min(n0 + L, N - 1) - n0) * p.ldb * 2);
             pf_base = reinterpret_cast<const char*>(pb + (size_t)n0 * p.ldb);
+        }
+        if (nst == 0) {  // every prefetch then reads stage 0 of the dummy
+            pf_voff = 0;
+            pf_base = reinterpret_cast<const char*>(dma_dummy);
         }
     }
     auto prefetch = [&](int st) {
@@ -331,7 +365,7 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
                 for (int d = 0; d < ND; ++d)
                     if (((2 * d + 1) * NM) / (2 * ND) == t) dma_one(dma_st, d, la, lb);
                 // After the stage's last DMA: the prefetch is always the latest memory instruction.
-                if (PF > 0 && t == NM - 1) prefetch(min(dma_st + PF, nst - 1));
+                if (PF > 0 && t == NM - 1) prefetch(min(dma_st + PF, last_st));
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -343,15 +377,16 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
 
     // Prologue: stages 0 and 1 in flight (ND DMAs per wave each), with prefetch stages 2 .. PF + 1
     // too; wait for stage 0.  Each wait below then leaves exactly one instruction pending, the
-    // latest prefetch (memory instructions complete in issue order for the counter).
+    // latest prefetch (memory instructions complete in issue order for the counter).  With no whole
+    // stage it reads the dummy.
 #pragma unroll
     for (int d = 0; d < ND; ++d) dma_one(0, d, la0, lb0);
 #pragma unroll
-    for (int i = 2; i <= PF; ++i) prefetch(min(i, nst - 1));
-    const int st1 = min(1, nst - 1);
+    for (int i = 2; i <= PF; ++i) prefetch(min(i, last_st));
+    const int st1 = min(1, last_st);
 #pragma unroll
     for (int d = 0; d < ND; ++d) dma_one(st1, d, la1, lb1);
-    prefetch(min(1 + PF, nst - 1));
+    prefetch(min(1 + PF, last_st));
     static_assert(ND + PF <= 63, "the wait count field holds 63");
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(ND + PF) : "memory");
     read_half(fa0, fb0, As0, Bs0, 0);
@@ -360,7 +395,7 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
 #define FT_DMA_PHASE(XA, XB, YA, YB, LXA, LXB, ST)                               \
     run_half(fa0, fb0, fa1, fb1, XA, XB, 1, std::false_type{}, 0, 0u, 0u);                          \
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(PF > 0 ? 1 : 0) : "memory"); \
-    run_half(fa1, fb1, fa0, fb0, YA, YB, 0, std::true_type{}, min((ST) + 2, nst - 1), LXA, LXB);
+    run_half(fa1, fb1, fa0, fb0, YA, YB, 0, std::true_type{}, min((ST) + 2, last_st), LXA, LXB);
     int st = 0;
     for (; st + 1 < nst; st += 2) {
         FT_DMA_PHASE(As0, Bs0, As1, Bs1, la0, lb0, st)
@@ -374,6 +409,22 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
 #undef FT_DMA_PHASE
     // The workgroup's LDS must not be released with a DMA still writing it.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // k tail: the partial last stage is staged into buffer 0 by ordinary loads (zeros past kend),
+    // once every wave has finished reading the buffers, then multiplied like a whole stage.
+    if (k_tail > 0) {
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        opa.init(pa, p.lda, m0, M, wave, lane);
+        opb.init(pb, p.ldb, n0, N, wave, lane);
+#pragma unroll
+        for (int j = 0; j < NDA; ++j) opa.fill(nst, j, As0, wave, lane, k_tail);
+#pragma unroll
+        for (int j = 0; j < NDB; ++j) opb.fill(nst, j, Bs0, wave, lane, k_tail);
+        __syncthreads();
+        read_half(fa0, fb0, As0, Bs0, 0);
+        run_half(fa0, fb0, fa1, fb1, As0, Bs0, 1, std::false_type{}, 0, 0u, 0u);
+        run_half(fa1, fb1, fa0, fb0, As0, Bs0, 0, std::false_type{}, 0, 0u, 0u);
+    }
 
     // Epilogue through buffer loads and stores relative to the tile's corner.  The byte offset of
     // an element splits into a per-lane part (4 h rows and lane column li) in the VGPR offset and

@@ -23,6 +23,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <cstring>
 #include <limits>
 #include <numeric>
 
@@ -55,10 +56,21 @@ constexpr double kFusedStoreMicros    = 2.0;  // per round: a split workgroup's 
 constexpr double kRoundMicros     = 3.35;
 constexpr double kTieWeight       = 1e-3;
 constexpr double kCuBytesPerMicro = 6.4e4;  // one CU's sustained load rate (about 27 bytes per clock)
+// A 16-bit DMA tile stages a partial last stage (k not a multiple of 64) by ordinary loads once its
+// pipeline has drained: per tile, the drain, the loads' latency and a barrier.  Fitted to the bf16
+// grouped weight gradient (16384 ragged tokens, 4096x14336 weights, ms, DMA against register-staged
+// 256x256 tile): 8 experts 1.80 / 2.01, 16 2.25 / 2.42, 32 3.28 / 3.23, 64 5.28 / 4.86, 128 9.15 /
+// 8.22; the DMA tile is ranked first at 8 experts only (7% lost at 16).
+constexpr double kDmaTailMicros = 3.0;
 constexpr uint64_t kMinSplitDepth = 256;  // reduction depth worth one split-k workgroup
 constexpr uint64_t kMinGemvDepth  = 64;
 
 uint64_t ceilDiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+// Whether variant vi runs a k tail through the separate pass of the 16-bit DMA tiles.
+bool dmaTail(const VariantInfo& vi, uint64_t k) {
+    return vi.input != FTRAIN_NUMERIC_TYPE_FP32 && std::strstr(vi.name, "_Dma") != nullptr && k % 64 != 0;
+}
 }  // namespace
 
 int computeUnits(FTrainDeviceId device) {
@@ -146,7 +158,11 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
     // and, when split, its workgroups' partial-tile stores and arrival.
     const double per_round = vi.split != SplitKind::kFused ? kRoundMicros
                              : kFusedRampMicros + (splits > 1 ? kFusedStoreMicros : 0.0);
-    const double compute   = double(per_cu) * 2.0 * vi.bm * vi.bn * depth / cu_rate + rounds * per_round;
+    // The tail pass: every tile's when whole-k, the last split's tiles when split.
+    const double tails     = !dmaTail(vi, s.k) ? 0.0 : used == 1 ? rounds
+                                                   : double(ceilDiv(ceilDiv(tiles, cus), uint64_t(vi.occupancy)));
+    const double compute   = double(per_cu) * 2.0 * vi.bm * vi.bn * depth / cu_rate + rounds * per_round +
+                           tails * kDmaTailMicros;
     // A launch with fewer workgroups than CUs streams memory through only that many of them (a CU
     // moves a bounded number of bytes per clock): 64x4096x14336 bf16 on the 64x128 split tile took
     // 36.3 us at 4 splits (128 workgroups) against 23.8 us at 8.
@@ -228,10 +244,11 @@ double groupedMicros(Variant v, const std::vector<GemmShape>& shapes, bool has_c
     const VariantInfo& vi = info(v);
     const double eb = vi.input == FTRAIN_NUMERIC_TYPE_FP32 ? 4.0 : 2.0;
     double flops = 0.0, bytes = 0.0;
-    uint64_t tiles = 0;
+    uint64_t tiles = 0, tail_tiles = 0;
     for (const GemmShape& s : shapes) {
         const uint64_t t = ceilDiv(s.m, vi.bm) * ceilDiv(s.n, vi.bn);
         tiles += t;
+        if (dmaTail(vi, s.k)) tail_tiles += t;
         flops += double(t) * 2.0 * vi.bm * vi.bn * double(std::max<uint64_t>(s.k, vi.bk));
         bytes += eb * (double(s.m) * s.k + double(s.k) * s.n + double(s.m) * s.n * (has_c ? 2.0 : 1.0));
     }
@@ -239,7 +256,9 @@ double groupedMicros(Variant v, const std::vector<GemmShape>& shapes, bool has_c
     const uint64_t per_cu = ceilDiv(tiles, cus);
     const double cu_rate  = vi.flop_per_clk * kClockPerMicro * residentEfficiency(vi, per_cu);
     const double rounds   = double(ceilDiv(per_cu, uint64_t(vi.occupancy)));
-    const double compute  = double(per_cu) * (flops / double(tiles)) / cu_rate + rounds * kRoundMicros;
+    const double tails    = double(ceilDiv(ceilDiv(tail_tiles, cus), uint64_t(vi.occupancy)));
+    const double compute  = double(per_cu) * (flops / double(tiles)) / cu_rate + rounds * kRoundMicros +
+                           tails * kDmaTailMicros;
     return std::max(compute, bytes / kHbmBytesPerMicro) + kLaunchMicros;
 }
 

@@ -383,10 +383,10 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
                               "32-bit offsets (fp32 DMA tiles)");
             if ((v_->tile == gemm::Variant::kBf16MfmaDma256x256 || v_->tile == gemm::Variant::kFp16MfmaDma256x256 ||
                  v_->tile == gemm::Variant::kBf16MfmaDma128x128 || v_->tile == gemm::Variant::kFp16MfmaDma128x128) &&
-                (l.shape.k == 0 || l.shape.k % 64 != 0 || l.lda >= (int64_t(1) << 23) || l.ldb >= (int64_t(1) << 23) ||
-                 l.ldc >= (int64_t(1) << 21) || l.ldd >= (int64_t(1) << 21)))
+                (l.lda >= (int64_t(1) << 23) || l.ldb >= (int64_t(1) << 23) || l.ldc >= (int64_t(1) << 21) ||
+                 l.ldd >= (int64_t(1) << 21)))
                 return Result(FTRAIN_STATUS_UNSUPPORTED,
-                              "a group's k is not a positive multiple of 64 or a leading dimension is too large for 32-bit offsets (DMA tiles)");
+                              "a group's leading dimension is too large for 32-bit offsets (DMA tiles)");
             const gemm::VariantInfo& vi = gemm::info(v_->tile);
             tiles += groupSlots(ceilDiv(l.shape.m, vi.bm) * ceilDiv(l.shape.n, vi.bn));
             if (tiles > kMax) return Result(FTRAIN_STATUS_UNSUPPORTED, "the tile count exceeds the grid limit");

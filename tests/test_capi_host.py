@@ -670,6 +670,12 @@ def test_finder_choices_for_16_bit_tiles(tlib):
     for shape, splits in (((64, 4096, 4096), 8), ((64, 4096, 14336), 8), ((64, 14336, 4096), 4)):
         assert rank(tlib, *shape, ab_type=c.BF16)[0] == tile64, shape
         assert tlib.ftrainTestingChooseSplits(names[tile64], *shape, 256) == splits, shape
+    # k not a multiple of 64: the DMA tiles stage the partial last stage and still lead (bf16, us:
+    # 8192x8192x8200 819 against 944 for the register-staged 256x256 tile, 16384x14336x4104 1491
+    # against 1764); a k that is not a multiple of 8 (row-major a) leaves only the per-element tile.
+    assert rank(tlib, 8192, 8192, 8200, ab_type=c.BF16)[0] == "Bf16MfmaGemm_256x256_Dma"
+    assert rank(tlib, 16384, 14336, 4104, ab_type=c.BF16)[0] == "Bf16MfmaGemm_256x256_Dma"
+    assert rank(tlib, 4096, 4096, 4100, ab_type=c.BF16) == ["Bf16MfmaGemm_64x64_Unaligned"]
     # Taller problems keep the 128-row tiles: the 64-row one does not apply above m = 64.
     assert tile64 not in rank(tlib, 65, 4096, 4096, ab_type=c.BF16)
     assert "Fp16MfmaGemm_64x128_Dma_SplitK" == rank(tlib, 64, 4096, 4096, ab_type=c.FP16)[0]

@@ -336,3 +336,38 @@ def test_abcd_half_large_total_b_exact(capi, dtype, dname, b_col_major):
         for g, m in enumerate(m_list):
             assert torch.equal(d[row:row + m], want[g]), (g, m)
             row += m
+
+
+@pytest.mark.parametrize("dtype,dname", [(torch.bfloat16, "Bf16"), (torch.float16, "Fp16")])
+def test_ab_weight_gradient_ragged_tokens_exact_on_dma_tiles(capi, dtype, dname):
+    """dW_g = X_g^T @ dY_g with token counts that are not multiples of 64 (one below a stage, one of
+    zero): every Primitive of the Plan, the DMA tiles included (their partial last stage staged by
+    ordinary loads, zeros past each expert's tokens).  Integer inputs in [-2, 2] make the fp32
+    result exact, so each group must equal its fp64 product bit for bit."""
+    tokens, M, N = [1000, 0, 37, 300, 129, 2100], 512, 768
+    G, T = len(tokens), sum(tokens)
+    gen = torch.Generator(device="cuda").manual_seed(41)
+    X = torch.randint(-2, 3, (T, M), device="cuda", generator=gen).to(dtype)
+    dY = torch.randint(-2, 3, (T, N), device="cuda", generator=gen).to(dtype)
+    d_list = [torch.full((M, N), float("nan"), device="cuda") for _ in range(G)]
+    offs = [sum(tokens[:g]) for g in range(G)]
+    ops = capi.GroupedOps("ab")
+    al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+    args = ops.args(
+        a=capi.GroupedSpec(capi.matrix(X), G, dims=[(M, t) for t in tokens], strides=[(1, M)] * G,
+                           offsets=[o * M for o in offs]),
+        b=capi.GroupedSpec(capi.matrix(dY), G, dims=[(t, N) for t in tokens]),
+        c=[capi.View(None, [M, N], numeric_type=capi.TORCH_NUMERIC_TYPES[torch.float32]) for _ in range(G)],
+        d=[capi.matrix(t) for t in d_list], alpha=al.view, beta=be.view)
+    plan = args.plan()
+    args.close()
+    names = plan.names()
+    assert f"Grouped{dname}MfmaGemm_256x256_Dma" in names and f"Grouped{dname}MfmaGemm_128x128_Dma" in names, names
+    want = [(X[o:o + t].double().t() @ dY[o:o + t].double()).float() for o, t in zip(offs, tokens)]
+    for i, name in enumerate(names):
+        for t in d_list:
+            t.fill_(float("nan"))
+        plan.execute(i, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        for g in range(G):
+            assert torch.equal(d_list[g], want[g]), (name, g, tokens[g])

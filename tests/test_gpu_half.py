@@ -126,6 +126,22 @@ def test_half_dma_tile(capi, ops, oracle, kind, cd, la, lb, m, n, k, pad, with_c
 @pytest.mark.parametrize("kind", ["bf16", "fp16"])
 @pytest.mark.parametrize("cd", ["fp32", "same"])
 @pytest.mark.parametrize("la,lb", list(itertools.product((False, True), (False, True))))
+@pytest.mark.parametrize("m,n,k,pad,with_c", [(256, 256, 72, 8, True), (296, 520, 40, 0, True),
+                                              (384, 256, 1000, 8, False), (64, 1024, 8200, 0, True),
+                                              (384, 4096, 4104, 0, False)])
+def test_half_dma_tiles_with_a_k_tail(capi, ops, oracle, kind, cd, la, lb, m, n, k, pad, with_c):
+    # k not a multiple of 64: the DMA tiles run the whole stages through their pipeline and stage the
+    # partial last one by ordinary loads, zeros past k (one stage and 8 more k; less than one stage;
+    # 15 stages and 40 more; deep k on the split tiles, whose last split holds the tail).  Every
+    # Primitive of each Plan, every operand orientation, NaN past each leading dimension.
+    names = run_case(capi, ops, oracle, kind, kind if cd == "same" else "fp32", m, n, k, la, lb, pad=pad,
+                     with_c=with_c, seed=k + m)
+    assert any("_Dma" in nm for nm in names), names
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+@pytest.mark.parametrize("cd", ["fp32", "same"])
+@pytest.mark.parametrize("la,lb", list(itertools.product((False, True), (False, True))))
 @pytest.mark.parametrize("m,n,k,pad,with_c", [(64, 4096, 4096, 0, False), (40, 200, 1024, 8, True),
                                               (1, 136, 576, 8, True), (64, 1024, 8192, 0, True)])
 def test_half_dma_64_row_split_tile(capi, ops, oracle, kind, cd, la, lb, m, n, k, pad, with_c):

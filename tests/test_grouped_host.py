@@ -117,10 +117,15 @@ def test_half_types_select_their_variants(tlib):
     st, msg, plan = moe_abcd(tlib, [64, 32], a_type=c.FP16, d_type=c.FP16)
     assert st == c.SUCCESS, msg
     assert all(n.startswith("GroupedFp16") for n in plan.names()) and len(plan) == 5
-    # k not a multiple of 64: the DMA tiles (whole 64-k stages) step aside.
+    # k not a multiple of 64: the DMA tiles stage the partial last stage themselves and stay.
     st, msg, plan = moe_abcd(tlib, [64, 32], k=72, a_type=c.BF16)
     assert st == c.SUCCESS, msg
-    assert not any(n.endswith("_Dma") for n in plan.names()) and len(plan) == 3
+    assert "GroupedBf16MfmaGemm_256x256_Dma" in plan.names() and len(plan) == 5
+    # k not a multiple of 8 with a k-contiguous operand: 16-byte loads do not fit, only the
+    # per-element tile remains.
+    st, msg, plan = moe_abcd(tlib, [64, 32], k=70, a_type=c.BF16)
+    assert st == c.SUCCESS, msg
+    assert plan.names() == ["GroupedBf16MfmaGemm_64x64_Unaligned"]
 
 
 def test_group_shape_mismatch_is_invalid(tlib):
