@@ -210,6 +210,76 @@ def grouped_core(workload: str, E: int, dtype: str, steps: int, warmup: int, war
                        "ok": bool(ok)}}
 
 
+def grouped_wgrad_core(E: int, dtype: str, steps: int, warmup: int, tokens_total: int = 16384, m: int = 4096,
+                       n: int = 14336) -> dict:
+    """Mixture-of-experts weight gradient, one GroupedABGemm Plan (Primitive 0): dW_e = X_e^T @ dY_e over
+    each expert's tokens (the reduction depth, uneven and not a multiple of any tile: expert_rows), X the
+    packed m-wide activations, dY the packed n-wide output gradients, fp32 dW.  Timed with HIP events on
+    the launch stream; 4 sampled rows of every expert's dW checked against fp64."""
+    import numpy as np
+    import torch
+
+    import flash_train.capi as capi
+    from oracle import oracle
+
+    tokens = expert_rows(tokens_total, E)
+    dt = {"fp32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[dtype]
+    g = torch.Generator().manual_seed(2026)
+    X_h = torch.randn(tokens_total, m, generator=g).to(dt)
+    dY_h = torch.randn(tokens_total, n, generator=g).to(dt)
+    X, dY = X_h.cuda(), dY_h.cuda()
+    d_all = torch.empty(E, m, n, device="cuda")
+    offs = [sum(tokens[:e]) for e in range(E)]
+    ops = capi.GroupedOps("ab")
+    al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+    gargs = ops.args(
+        a=capi.GroupedSpec(capi.matrix(X), E, dims=[(m, t) for t in tokens], strides=[(1, m)] * E,
+                           offsets=[o * m for o in offs]),
+        b=capi.GroupedSpec(capi.matrix(dY), E, dims=[(t, n) for t in tokens]),
+        c=[capi.View(None, [m, n], numeric_type=capi.TORCH_NUMERIC_TYPES[torch.float32]) for _ in range(E)],
+        d=[capi.matrix(d_all[e]) for e in range(E)], alpha=al.view, beta=be.view)
+    plan = gargs.plan()
+    gargs.close()
+    name = plan.name(0)
+    log(f"grouped weight gradient {m}x{n} over {E} experts, tokens {tokens}; primitive 0 = {name}")
+    stream = torch.cuda.Stream()
+    h = stream.cuda_stream
+    with torch.cuda.stream(stream):
+        warm_up(lambda: plan.execute(0, h), stream, warmup, 25.0)
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            plan.execute(0, h)
+        stop.record(stream)
+        torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+
+    rng = np.random.default_rng(3)
+    ok, worst = True, 0.0
+    for e, t in enumerate(tokens):
+        rows = np.sort(rng.choice(m, size=4, replace=False))
+        o = offs[e]
+        ref = (X_h[o:o + t, rows].double().t() @ dY_h[o:o + t].double()).numpy()
+        rep = oracle.tolerance_check(d_all[e][torch.as_tensor(rows).cuda()].cpu().numpy(), ref, max(t, 1))
+        ok, worst = ok and rep["ok"], max(worst, rep["max_abs_err"] / max(rep["bound"], 1e-30))
+    del X, dY, d_all, plan
+    torch.cuda.empty_cache()
+
+    half = dtype != "fp32"
+    flops = 2.0 * tokens_total * m * n
+    tflops = flops / (ms * 1e-3) / 1e12
+    peak = HALF_MATRIX_PEAK_TFLOPS if half else FP32_MATRIX_PEAK_TFLOPS
+    eb = 2.0 if half else 4.0
+    alg_bytes = eb * tokens_total * (m + n) + 4.0 * E * m * n
+    return {"workload": f"grouped_wgrad_e{E}" + ("" if not half else f"_{dtype}"), "m": m, "n": n,
+            "k": tokens_total, "experts": E, "tokens": tokens, "dtype": dtype, "primitive": name, "steps": steps,
+            "ms": round(ms, 5), "tflops": round(tflops, 3),
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": peak, "unit": "TFLOP/s",
+                         "frac": round(tflops / peak, 4), "traffic": None,
+                         "algorithmic_bytes": alg_bytes, "algorithmic_flops": flops},
+            "parity": {"rows_checked": 4 * E, "worst_err_over_bound": worst, "ok": bool(ok)}}
+
+
 def run_grouped(args) -> None:
     """--grouped E: one step = one GroupedABCDGemm launch sequence over all experts; prints one JSON line."""
     g = grouped_core(args.workload, args.grouped, args.dtype, args.steps, args.warmup, args.warm_ms)
@@ -616,6 +686,8 @@ def main() -> None:
         for experts in (8, 64):
             log(f"config grouped mlp_fwd over {experts} experts bf16")
             configs.append(grouped_core("mlp_fwd", experts, "bf16", steps=20, warmup=2))
+        log("config grouped weight gradient over 8 experts bf16")
+        configs.append(grouped_wgrad_core(8, "bf16", steps=20, warmup=2))
         result["configs"] = configs
         log("reference benchmark shapes")
         result["reference_suite"] = reference_suite()
