@@ -686,8 +686,9 @@ def main() -> None:
         for experts in (8, 64):
             log(f"config grouped mlp_fwd over {experts} experts bf16")
             configs.append(grouped_core("mlp_fwd", experts, "bf16", steps=20, warmup=2))
-        log("config grouped weight gradient over 8 experts bf16")
-        configs.append(grouped_wgrad_core(8, "bf16", steps=20, warmup=2))
+        for dtype, steps in (("fp32", 10), ("bf16", 20)):
+            log(f"config grouped weight gradient over 8 experts {dtype}")
+            configs.append(grouped_wgrad_core(8, dtype, steps=steps, warmup=2))
         result["configs"] = configs
         log("reference benchmark shapes")
         result["reference_suite"] = reference_suite()

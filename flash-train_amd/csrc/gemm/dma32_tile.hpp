@@ -114,6 +114,10 @@ __device__ __forceinline__ int a_swz(int row) {
 // after this launch; measured on MI355X, 64x4096x4096 on the 64x128 tile: about 0.5 us less per call).
 constexpr int kPartialPolicy = 2;
 
+// What the DMA pipeline reads when k holds no whole stage (its data is discarded): with the
+// leading dimensions taken as 0, every lane's offset stays within 1 KiB of it.
+static __device__ __attribute__((aligned(256))) float dma32_dummy[512];
+
 template <int BM, int BN, int WM, int WN, bool SPLIT, bool TB = false, bool TA = false>
 __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid, int z, int band = 4) {
     static_assert(WM * WN == 4, "4 waves");
@@ -146,8 +150,15 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
     const int M = p.m, N = p.n;
     const int kbeg = SPLIT ? z * p.k_chunk : 0;
     const int kend = SPLIT ? min(p.k, kbeg + p.k_chunk) : p.k;
-    const int nst  = (kend - kbeg) / kStageK;
-    const int64_t lda = p.lda, ldb = p.ldb;
+    // Whole stages go through the DMA pipeline; a partial last one (k_tail) is staged afterwards.
+    // With no whole stage the pipeline runs on the dummy (none).
+    const int nst     = (kend - kbeg) / kStageK;
+    const int k_tail  = (kend - kbeg) - nst * kStageK;
+    const int last_st = nst > 0 ? nst - 1 : 0;
+    const bool none   = nst == 0;
+    const int64_t lda_r = p.lda, ldb_r = p.ldb;
+    const int64_t lda = none ? 0 : lda_r, ldb = none ? 0 : ldb_r;
+    const char* const dummy = reinterpret_cast<const char*>(dma32_dummy);
 
     // DMA sources.  A block q = wave + 4 j: rows 8q .. 8q + 7 (lane: row 8q + lane / 8), slot
     // lane % 8 holds chunk (lane % 8) ^ h(row); h does not depend on j (32 j leaves bits 1-3).
@@ -157,25 +168,28 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
     const unsigned achunk = 16 * ((lane & 7) ^ a_swz(ar));
     const unsigned alast  = static_cast<unsigned>(min(M - 1 - m0, BM - 1));
     const unsigned lda4   = static_cast<unsigned>(4 * lda);
-    const char* abase     = reinterpret_cast<const char*>(p.a + (size_t)m0 * lda + kbeg);
+    const char* abase_r   = reinterpret_cast<const char*>(p.a + (size_t)m0 * lda_r + kbeg);
+    const char* abase     = none ? dummy : abase_r;
     // B block q = wave + 4 j: k rows RB q .. RB q + RB - 1 (lane: row RB q + lane / CPR), slot
     // lane % CPR holds chunk (lane % CPR) ^ swizzle; a chunk past n is clamped onto the last whole
     // one (n % 4 == 0).  x = the swizzle bit of the block's k rows.
-    const char* bbase = reinterpret_cast<const char*>(p.b + (size_t)kbeg * ldb + n0);
-    auto boff = [&](int x) {
+    const char* bbase_r = reinterpret_cast<const char*>(p.b + (size_t)kbeg * ldb_r + n0);
+    const char* bbase   = none ? dummy : bbase_r;
+    auto boff = [&](int x, int64_t ld) {
         const int kr = lane / CPR, chunk = (lane % CPR) ^ (x ? 16 : 0);
-        return static_cast<unsigned>((kr * ldb + (min(n0 + 4 * chunk, N - 4) - n0)) * 4);
+        return static_cast<unsigned>((kr * ld + (min(n0 + 4 * chunk, N - 4) - n0)) * 4);
     };
-    const unsigned boff0 = boff(0), boff1 = BSWZ ? boff(1) : boff0;
+    const unsigned boff0 = boff(0, ldb), boff1 = BSWZ ? boff(1, ldb) : boff0;
     // Column-major a: block q = wave + 4 j holds k rows RA q .. RA q + RA - 1 of the stage (lane: k
     // row RA q + lane / CPA, slot lane % CPA holds chunk (lane % CPA) ^ swizzle, four rows of a);
     // a chunk past m is clamped onto the last whole one (m % 4 == 0).
-    const char* atbase = reinterpret_cast<const char*>(p.a + (size_t)kbeg * lda + m0);
-    auto aoff = [&](int x) {
+    const char* atbase_r = reinterpret_cast<const char*>(p.a + (size_t)kbeg * lda_r + m0);
+    const char* atbase   = none ? dummy : atbase_r;
+    auto aoff = [&](int x, int64_t ld) {
         const int kr = lane / CPA, chunk = (lane % CPA) ^ (x ? 16 : 0);
-        return static_cast<unsigned>((kr * lda + (min(m0 + 4 * chunk, M - 4) - m0)) * 4);
+        return static_cast<unsigned>((kr * ld + (min(m0 + 4 * chunk, M - 4) - m0)) * 4);
     };
-    const unsigned aoff0 = TA ? aoff(0) : 0u, aoff1 = TA && ASWZ ? aoff(1) : aoff0;
+    const unsigned aoff0 = TA ? aoff(0, lda) : 0u, aoff1 = TA && ASWZ ? aoff(1, lda) : aoff0;
     auto dma_a = [&](int st, int j, unsigned lds) {
         if constexpr (TA) {
             const int q = wave + 4 * j, kr0 = RA * q;
@@ -193,7 +207,8 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
     // 2g + hf of two adjacent g: those 32 sit in 32 distinct 16-byte slots modulo 512 bytes, the
     // width of the LDS banks (no bank conflict).  Columns past n are clamped onto the last one;
     // 255 columns of ldb < 2^22 keep the lane offset below 2^32.
-    const char* btbase = reinterpret_cast<const char*>(p.b + (size_t)n0 * ldb + kbeg);
+    const char* btbase_r = reinterpret_cast<const char*>(p.b + (size_t)n0 * ldb_r + kbeg);
+    const char* btbase   = none ? dummy : btbase_r;
     const unsigned blast = static_cast<unsigned>(min(N - 1 - n0, BN - 1));
     auto dma_bt = [&](int st, int j, unsigned lds) {
         const int q = wave + 4 * j, t = (lane & 7) ^ (q & 7);
@@ -317,11 +332,11 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
         for (int r = 0; r < NR; ++r) read_one(ga, gb, As, Bs, hf, r);
     };
 
-    // Every launch has at least one stage (k > 0; a split's chunk is a whole number of stages).
+    // The pipeline always runs (on the dummy when k holds no whole stage).
     {
 #pragma unroll
         for (int d = 0; d < ND; ++d) dma_one(0, d, la0, lb0);
-        const int st1 = min(1, nst - 1);
+        const int st1 = min(1, last_st);
 #pragma unroll
         for (int d = 0; d < ND; ++d) dma_one(st1, d, la1, lb1);
         asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(ND) : "memory");
@@ -342,7 +357,7 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
     run_half(fa0, fb0, fa1, fb1, XA, XB, 1, std::false_type{}, 0, 0u, 0u);                        \
     rotate();                                                                                     \
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");         \
-    run_half(fa0, fb0, fa1, fb1, YA, YB, 0, std::true_type{}, min((ST) + 2, nst - 1), LXA, LXB);  \
+    run_half(fa0, fb0, fa1, fb1, YA, YB, 0, std::true_type{}, min((ST) + 2, last_st), LXA, LXB);  \
     rotate();
         int st = 0;
         for (; st + 1 < nst; st += 2) {
@@ -355,6 +370,53 @@ __device__ __forceinline__ void fp32_gemm_dma_tile(const GemmParams& p, int bid,
 #undef FT_DMA32_PHASE
         // The workgroup's LDS must not be released with a DMA still writing it.
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+        // k tail: the partial last stage is staged into buffer 0 by ordinary loads at the addresses
+        // the DMAs would use (the real operands), lanes whose k lies past kend storing zeros and
+        // loading nothing, once every wave has finished reading the buffers; then it is multiplied
+        // like a whole stage.
+        if (k_tail > 0) {
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            auto put = [&](float* stage, int q, bool ok, const char* src) {
+                floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
+                if (ok) v = *reinterpret_cast<const floatx4*>(src);
+                *reinterpret_cast<floatx4*>(reinterpret_cast<char*>(stage) + q * 1024 + 16 * lane) = v;
+            };
+            const size_t st_k = (size_t)nst * kStageK;
+#pragma unroll
+            for (int j = 0; j < DA; ++j) {
+                const int q = wave + 4 * j;
+                if constexpr (TA) {
+                    const int kr0 = RA * q;
+                    const unsigned off = aoff(ASWZ && ((kr0 >> 3) & 1), lda_r);
+                    put(As0, q, kr0 + lane / CPA < k_tail, atbase_r + (st_k + kr0) * lda_r * 4 + off);
+                } else {
+                    const unsigned row = min(ar + 32u * j, alast);
+                    put(As0, q, int(achunk / 4) < k_tail,
+                        abase_r + st_k * 4 + (size_t)row * lda_r * 4 + achunk);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < DB; ++j) {
+                const int q = wave + 4 * j;
+                if constexpr (TB) {
+                    const int t = (lane & 7) ^ (q & 7);
+                    const int cb = 4 * ((lane >> 3) & 1) + 2 * (lane >> 5) + (t & 1);
+                    const int ch = 4 * (t >> 2) + 2 * ((lane >> 4) & 1) + ((t >> 1) & 1);
+                    const unsigned col = min(static_cast<unsigned>(8 * q + cb), blast);
+                    put(Bs0, q, 4 * ch < k_tail, btbase_r + st_k * 4 + (size_t)col * ldb_r * 4 + 16 * ch);
+                } else {
+                    const int kr0 = RB * q;
+                    const unsigned off = boff(BSWZ && ((kr0 >> 3) & 1), ldb_r);
+                    put(Bs0, q, kr0 + lane / CPR < k_tail, bbase_r + (st_k + kr0) * ldb_r * 4 + off);
+                }
+            }
+            __syncthreads();
+            read_half(fa0, fb0, As0, Bs0, 0);
+            run_half(fa0, fb0, fa1, fb1, As0, Bs0, 1, std::false_type{}, 0, 0u, 0u);
+            rotate();
+            run_half(fa0, fb0, fa1, fb1, As0, Bs0, 0, std::false_type{}, 0, 0u, 0u);
+        }
     }
 
     // Epilogue, one row block at a time: block (bi, bj) register r is D[row 16 bi + 4 g + r][col

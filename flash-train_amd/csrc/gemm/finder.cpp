@@ -56,7 +56,7 @@ constexpr double kFusedStoreMicros    = 2.0;  // per round: a split workgroup's 
 constexpr double kRoundMicros     = 3.35;
 constexpr double kTieWeight       = 1e-3;
 constexpr double kCuBytesPerMicro = 6.4e4;  // one CU's sustained load rate (about 27 bytes per clock)
-// A 16-bit DMA tile stages a partial last stage (k not a multiple of 64) by ordinary loads once its
+// A DMA tile stages a partial last stage (k not a multiple of its stage) by ordinary loads once its
 // pipeline has drained: per tile, the drain, the loads' latency and a barrier.  Fitted to the bf16
 // grouped weight gradient (16384 ragged tokens, 4096x14336 weights, ms, DMA against register-staged
 // 256x256 tile): 8 experts 1.80 / 2.01, 16 2.25 / 2.42, 32 3.28 / 3.23, 64 5.28 / 4.86, 128 9.15 /
@@ -67,9 +67,10 @@ constexpr uint64_t kMinGemvDepth  = 64;
 
 uint64_t ceilDiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
-// Whether variant vi runs a k tail through the separate pass of the 16-bit DMA tiles.
+// Whether variant vi runs a k tail through the separate pass of the DMA tiles (stages of 32 k for
+// fp32, 64 for 16-bit inputs).
 bool dmaTail(const VariantInfo& vi, uint64_t k) {
-    return vi.input != FTRAIN_NUMERIC_TYPE_FP32 && std::strstr(vi.name, "_Dma") != nullptr && k % 64 != 0;
+    return std::strstr(vi.name, "_Dma") != nullptr && k % (vi.input == FTRAIN_NUMERIC_TYPE_FP32 ? 32 : 64) != 0;
 }
 }  // namespace
 

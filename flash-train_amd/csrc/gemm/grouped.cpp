@@ -368,19 +368,18 @@ class GroupedGemmPrimitive final : public Primitive<GroupedGemmProblem> {
                     return Result(FTRAIN_STATUS_UNSUPPORTED, "a group's c or d does not fit 128-bit stores");
             }
             if (v_->tile == gemm::Variant::kMfma16Dma256x256 &&
-                (l.ta || l.tb || l.shape.k == 0 || l.shape.k % 32 != 0 || l.lda >= (int64_t(1) << 22) ||
-                 l.ldb >= (int64_t(1) << 22) || l.ldc >= (int64_t(1) << 21) || l.ldd >= (int64_t(1) << 21)))
+                (l.ta || l.tb || l.lda >= (int64_t(1) << 22) || l.ldb >= (int64_t(1) << 22) ||
+                 l.ldc >= (int64_t(1) << 21) || l.ldd >= (int64_t(1) << 21)))
                 return Result(FTRAIN_STATUS_UNSUPPORTED,
-                              "a group is not row-major a and b with k a positive multiple of 32 and leading dimensions "
-                              "that fit 32-bit offsets (fp32 DMA tiles)");
+                              "a group is not row-major a and b with leading dimensions that fit 32-bit offsets (fp32 "
+                              "DMA tiles)");
             if (v_->tile == gemm::Variant::kMfma16Dma64x128 && l.ta)
                 return Result(FTRAIN_STATUS_UNSUPPORTED, "a group's a is column-major (the 64x128 DMA tile takes row-major a)");
             if ((v_->tile == gemm::Variant::kMfma16Dma128x128 || v_->tile == gemm::Variant::kMfma16Dma64x128) &&
-                (l.shape.k == 0 || l.shape.k % 32 != 0 || l.lda >= (int64_t(1) << 22) || l.ldb >= (int64_t(1) << 22) ||
-                 l.ldc >= (int64_t(1) << 21) || l.ldd >= (int64_t(1) << 21)))
+                (l.lda >= (int64_t(1) << 22) || l.ldb >= (int64_t(1) << 22) || l.ldc >= (int64_t(1) << 21) ||
+                 l.ldd >= (int64_t(1) << 21)))
                 return Result(FTRAIN_STATUS_UNSUPPORTED,
-                              "a group's k is not a positive multiple of 32 or a leading dimension is too large for "
-                              "32-bit offsets (fp32 DMA tiles)");
+                              "a group's leading dimension is too large for 32-bit offsets (fp32 DMA tiles)");
             if ((v_->tile == gemm::Variant::kBf16MfmaDma256x256 || v_->tile == gemm::Variant::kFp16MfmaDma256x256 ||
                  v_->tile == gemm::Variant::kBf16MfmaDma128x128 || v_->tile == gemm::Variant::kFp16MfmaDma128x128) &&
                 (l.lda >= (int64_t(1) << 23) || l.ldb >= (int64_t(1) << 23) || l.ldc >= (int64_t(1) << 21) ||

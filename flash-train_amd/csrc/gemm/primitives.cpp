@@ -166,11 +166,11 @@ class GemmPrimitive final : public Primitive<GemmProblem> {
                     return Result(FTRAIN_STATUS_UNSUPPORTED, "a matrix address is not 16-byte aligned");
         }
         if (v_ >= Variant::kMfma16Dma256x256 && v_ <= Variant::kMfma16Dma128x64 &&
-            (s.k == 0 || s.k % 32 != 0 || g.lda >= (int64_t(1) << 22) || g.ldb >= (int64_t(1) << 22) ||
-             g.ldc >= (int64_t(1) << 21) || g.ldd >= (int64_t(1) << 21)))
+            (s.k == 0 || g.lda >= (int64_t(1) << 22) || g.ldb >= (int64_t(1) << 22) || g.ldc >= (int64_t(1) << 21) ||
+             g.ldd >= (int64_t(1) << 21)))
             return Result(FTRAIN_STATUS_UNSUPPORTED,
-                          "needs k a positive multiple of 32, leading dimensions of a and b below 2^22 and of c and d "
-                          "below 2^21 (DMA stages, 32-bit offsets)");
+                          "needs k positive, leading dimensions of a and b below 2^22 and of c and d below 2^21 "
+                          "(DMA stages, 32-bit offsets)");
         if (v_ >= Variant::kBf16MfmaDma256x256 && v_ <= Variant::kFp16MfmaDma64x128S &&
             (s.k == 0 || g.lda >= (int64_t(1) << 23) || g.ldb >= (int64_t(1) << 23) || g.ldc >= (int64_t(1) << 21) ||
              g.ldd >= (int64_t(1) << 21)))

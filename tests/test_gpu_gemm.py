@@ -551,15 +551,15 @@ def test_fp32_dma_tile(capi, ops, oracle, m, n, k, with_c, pad):
     assert torch.equal(outs[0], outs[1])
 
 
-def test_fp32_dma_tile_skips_other_layouts_and_k_tails(capi, ops):
+def test_fp32_dma_tile_layouts_and_k_tails(capi, ops):
     a = torch.zeros(256, 64, device="cuda")
     b = torch.zeros(64, 256, device="cuda")
     d = torch.empty(256, 256, device="cuda")
     assert "Fp32Mfma16Gemm_256x256_Dma" in capi.plan_for(a, b, None, d, 1.0, 0.0, ops).names()
-    # column-major b and a k tail (k % 32 != 0): the row-major, whole-stage kernel does not apply
+    # column-major b: the row-major kernel does not apply; a k tail (k % 32 != 0) it stages itself
     assert "Fp32Mfma16Gemm_256x256_Dma" not in capi.plan_for(a, b.t().contiguous().t(), None, d, 1.0, 0.0, ops).names()
     a3 = torch.zeros(256, 48, device="cuda")
-    assert "Fp32Mfma16Gemm_256x256_Dma" not in capi.plan_for(a3, b[:48], None, d, 1.0, 0.0, ops).names()
+    assert "Fp32Mfma16Gemm_256x256_Dma" in capi.plan_for(a3, b[:48], None, d, 1.0, 0.0, ops).names()
     # the 128x128 tile takes a column-major b, a column-major a, or both; the 64x128 split tile
     # (wave rows of 32) takes no column-major a
     a, b = torch.zeros(256, 1024, device="cuda"), torch.zeros(1024, 256, device="cuda")  # deep enough to split

@@ -371,3 +371,34 @@ def test_ab_weight_gradient_ragged_tokens_exact_on_dma_tiles(capi, dtype, dname)
         torch.cuda.synchronize()
         for g in range(G):
             assert torch.equal(d_list[g], want[g]), (name, g, tokens[g])
+
+
+def test_ab_weight_gradient_ragged_tokens_fp32_dma_tile(capi, oracle):
+    """fp32 dW_g = X_g^T @ dY_g with token counts that are not multiples of 32 (one of zero, one below a
+    stage): every Primitive, the 128x128 DMA tile included (partial last stage staged by ordinary
+    loads), against fp64."""
+    tokens, M, N = [500, 0, 19, 300, 129], 256, 384
+    G, T = len(tokens), sum(tokens)
+    X = rnd((T, M), 51).cuda()
+    dY = rnd((T, N), 52).cuda()
+    d_list = [torch.full((M, N), float("nan"), device="cuda") for _ in range(G)]
+    offs = [sum(tokens[:g]) for g in range(G)]
+    ops = capi.GroupedOps("ab")
+    al, be = capi.HostScalar(1.0), capi.HostScalar(0.0)
+    args = ops.args(
+        a=capi.GroupedSpec(capi.matrix(X), G, dims=[(M, t) for t in tokens], strides=[(1, M)] * G,
+                           offsets=[o * M for o in offs]),
+        b=capi.GroupedSpec(capi.matrix(dY), G, dims=[(t, N) for t in tokens]),
+        c=[capi.View(None, [M, N]) for _ in range(G)], d=[capi.matrix(t) for t in d_list], alpha=al.view,
+        beta=be.view)
+    X_h, dY_h = X.cpu().numpy(), dY.cpu().numpy()
+
+    def check(name):
+        for g, t in enumerate(tokens):
+            o = offs[g]
+            ref = oracle.gemm_f64(np.ascontiguousarray(X_h[o:o + t].T), dY_h[o:o + t], None, 1.0, 0.0)
+            close(oracle, d_list[g].cpu().numpy(), ref, max(t, 1), what=(name, g))
+            d_list[g].fill_(float("nan"))
+
+    names = run_all(capi, args, check)
+    assert "GroupedFp32Mfma16Gemm_128x128_Dma" in names, names

@@ -95,6 +95,18 @@ def run_every_primitive(capi, ops, oracle, m, n, k, la, lb, lcd, pad, with_c, al
 LAYOUTS = list(itertools.product((False, True), (False, True), (False, True)))
 
 
+@pytest.mark.parametrize("la,lb", list(itertools.product((False, True), (False, True))))
+@pytest.mark.parametrize("m,n,k,pad", [(256, 256, 20, 4), (256, 256, 44, 0), (384, 256, 1000, 4), (512, 512, 4100, 0),
+                                       (64, 4096, 4100, 0), (4096, 64, 4100, 0), (256, 256, 65540, 0)])
+def test_fp32_dma_tiles_with_a_k_tail(capi, ops, oracle, la, lb, m, n, k, pad):
+    # k not a multiple of 32: the fp32 DMA tiles run the whole stages through their pipeline and stage
+    # the partial last one by ordinary loads, zeros past k (less than one stage; one stage and 12 more;
+    # 31 stages and 8 more; deep k and skinny shapes on the split tiles, whose last split holds the
+    # tail).  Every Primitive of each Plan, every operand orientation, NaN past each leading dimension.
+    names = run_every_primitive(capi, ops, oracle, m, n, k, la, lb, False, pad, with_c=True, seed=k)
+    assert any("_Dma" in nm for nm in names), names
+
+
 @pytest.mark.parametrize("la,lb,lcd", LAYOUTS)
 @pytest.mark.parametrize("m,n,k,pad", [(256, 192, 160, 4), (256, 192, 150, 4), (129, 67, 37, 3), (64, 64, 1024, 0)])
 def test_layouts_every_primitive(capi, ops, oracle, la, lb, lcd, m, n, k, pad):

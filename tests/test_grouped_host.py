@@ -194,7 +194,9 @@ def test_ab_with_c_and_d_lists_and_a_column_major(tlib):
     cl = [D([M, N]) for _ in tokens]
     st, msg, plan = ops.args(a=a, b=b, c=cl, d=cl, alpha=al.view, beta=be.view).plan_status_on_device(0)
     assert st == c.SUCCESS, msg
-    assert sorted(plan.names()) == sorted(FP32_GROUPED[3:])  # k of 40 and 24: no fp32 DMA tile
+    # k of 40, 0 and 24 (partial stages): the 128x128 DMA tile takes any orientation; the 256x256
+    # and 64x128 ones need a row-major a.
+    assert sorted(plan.names()) == sorted(["GroupedFp32Mfma16Gemm_128x128_Dma"] + FP32_GROUPED[3:])
 
 
 def test_descriptor_values_that_overflow_addresses_are_rejected(tlib):
