@@ -140,6 +140,16 @@ def test_half_dma_tiles_with_a_k_tail(capi, ops, oracle, kind, cd, la, lb, m, n,
 
 
 @pytest.mark.parametrize("kind", ["bf16", "fp16"])
+@pytest.mark.parametrize("k", [2, 7, 9, 63, 65, 101, 127, 129, 1001])
+def test_half_dma_tiles_any_k_with_column_major_a(capi, ops, oracle, kind, k):
+    # A column-major a and a row-major b are both read along k rows, so k need not be a multiple of
+    # the 8-element load: the DMA tiles' partial last stage is staged row by row, zeros past k, and
+    # a k below one stage runs the pipeline on a dummy buffer.  Every Primitive of the Plan.
+    names = run_case(capi, ops, oracle, kind, "fp32", 136, 264, k, True, False, pad=8, with_c=True, seed=k)
+    assert any("_Dma" in nm for nm in names), names
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
 @pytest.mark.parametrize("cd", ["fp32", "same"])
 @pytest.mark.parametrize("la,lb", list(itertools.product((False, True), (False, True))))
 @pytest.mark.parametrize("m,n,k,pad,with_c", [(64, 4096, 4096, 0, False), (40, 200, 1024, 8, True),

@@ -107,6 +107,14 @@ def test_fp32_dma_tiles_with_a_k_tail(capi, ops, oracle, la, lb, m, n, k, pad):
     assert any("_Dma" in nm for nm in names), names
 
 
+@pytest.mark.parametrize("k", [2, 3, 5, 31, 33, 63, 97, 1001])
+def test_fp32_dma_tiles_any_k_with_column_major_a(capi, ops, oracle, k):
+    # A column-major a and a row-major b are both read along k rows, so k need not be a multiple of
+    # the 4-element load: the fp32 DMA tiles' partial last stage is staged row by row, zeros past k.
+    names = run_every_primitive(capi, ops, oracle, 132, 260, k, True, False, False, 4, with_c=True, seed=k)
+    assert any("_Dma" in nm for nm in names), names
+
+
 @pytest.mark.parametrize("la,lb,lcd", LAYOUTS)
 @pytest.mark.parametrize("m,n,k,pad", [(256, 192, 160, 4), (256, 192, 150, 4), (129, 67, 37, 3), (64, 64, 1024, 0)])
 def test_layouts_every_primitive(capi, ops, oracle, la, lb, lcd, m, n, k, pad):
