@@ -207,7 +207,8 @@ static __device__ __attribute__((aligned(256))) u16 dma_dummy[512];
 // BM: tile rows (T by default; 64 with T = 128 for m of at most 64, row-major a only).
 // PF: stages of b to prefetch into L2 ahead of the stage being staged (0: none), for a b larger
 // than the MALL, whose stages otherwise arrive from HBM later than the DMA lead covers.
-template <bool BF16, bool TA, bool TB, int T = 256, bool SPLIT = false, int BM = T, int PF = 0>
+// NB: stage buffers (2, or 3 for a ring in which each stage's DMAs run two stages ahead of its use).
+template <bool BF16, bool TA, bool TB, int T = 256, bool SPLIT = false, int BM = T, int PF = 0, int NB = 2>
 // band: tile rows per band of the tile order (tile_of).
 __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int bid, int z = 0, int band = 8) {
     constexpr bool A_TR = TA, B_TR = !TB;
@@ -219,6 +220,9 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
     __shared__ __attribute__((aligned(1024))) u16 Bs0[kStageB];
     __shared__ __attribute__((aligned(1024))) u16 As1[kStageA];
     __shared__ __attribute__((aligned(1024))) u16 Bs1[kStageB];
+    static_assert(NB == 2 || (NB == 3 && PF == 0), "a three-buffer ring takes no prefetch");
+    __shared__ __attribute__((aligned(1024))) u16 As2[NB > 2 ? kStageA : 8];
+    __shared__ __attribute__((aligned(1024))) u16 Bs2[NB > 2 ? kStageB : 8];
     const int tid = threadIdx.x, lane = tid & 63, li = lane & 31, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wrow = (wave >> 1) * (BM / 2), wcol = (wave & 1) * (T / 2);
@@ -280,6 +284,8 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
     const unsigned lb0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)Bs0;
     const unsigned la1 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)As1;
     const unsigned lb1 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)Bs1;
+    const unsigned la2 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)As2;
+    const unsigned lb2 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) u16*)Bs2;
 
     // Operand of k-step ks (0..3 in the stage) for rows (or columns) x .. x + 31.
     const int tr_k = (lane & 15) >> 2, tr_x = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
@@ -387,8 +393,13 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
 #pragma unroll
     for (int d = 0; d < ND; ++d) dma_one(st1, d, la1, lb1);
     prefetch(min(1 + PF, last_st));
-    static_assert(ND + PF <= 63, "the wait count field holds 63");
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(ND + PF) : "memory");
+    if constexpr (NB == 3) {
+        const int st2 = min(2, last_st);
+#pragma unroll
+        for (int d = 0; d < ND; ++d) dma_one(st2, d, la2, lb2);
+    }
+    static_assert((NB - 1) * ND + PF <= 63, "the wait count field holds 63");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NB - 1) * ND + PF) : "memory");
     read_half(fa0, fb0, As0, Bs0, 0);
 
     // Stages past the last reload the last one (harmless: nothing reads them).
@@ -396,16 +407,37 @@ __device__ __forceinline__ void half_gemm_dma_tile(const HalfGemmParams& p, int 
     run_half(fa0, fb0, fa1, fb1, XA, XB, 1, std::false_type{}, 0, 0u, 0u);                          \
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(PF > 0 ? 1 : 0) : "memory"); \
     run_half(fa1, fb1, fa0, fb0, YA, YB, 0, std::true_type{}, min((ST) + 2, last_st), LXA, LXB);
+    // Ring: the wait for the next stage leaves the one after it in flight, and the freed buffer
+    // takes the stage three ahead.
+#define FT_RING_PHASE(XA, XB, YA, YB, LXA, LXB, ST)                                                  \
+    run_half(fa0, fb0, fa1, fb1, XA, XB, 1, std::false_type{}, 0, 0u, 0u);                          \
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(ND) : "memory");   \
+    run_half(fa1, fb1, fa0, fb0, YA, YB, 0, std::true_type{}, min((ST) + 3, last_st), LXA, LXB);
     int st = 0;
-    for (; st + 1 < nst; st += 2) {
-        FT_DMA_PHASE(As0, Bs0, As1, Bs1, la0, lb0, st)
-        FT_DMA_PHASE(As1, Bs1, As0, Bs0, la1, lb1, st + 1)
+    if constexpr (NB == 2) {
+        for (; st + 1 < nst; st += 2) {
+            FT_DMA_PHASE(As0, Bs0, As1, Bs1, la0, lb0, st)
+            FT_DMA_PHASE(As1, Bs1, As0, Bs0, la1, lb1, st + 1)
+        }
+        // An odd stage count ends with one more stage in buffer 0 (a separate copy: leaving the
+        // loop between its two phases costs the register allocator the fragment double buffer).
+        if (st < nst) {
+            FT_DMA_PHASE(As0, Bs0, As1, Bs1, la0, lb0, st)
+        }
+    } else {
+        for (; st + 2 < nst; st += 3) {
+            FT_RING_PHASE(As0, Bs0, As1, Bs1, la0, lb0, st)
+            FT_RING_PHASE(As1, Bs1, As2, Bs2, la1, lb1, st + 1)
+            FT_RING_PHASE(As2, Bs2, As0, Bs0, la2, lb2, st + 2)
+        }
+        if (st < nst) {
+            FT_RING_PHASE(As0, Bs0, As1, Bs1, la0, lb0, st)
+        }
+        if (st + 1 < nst) {
+            FT_RING_PHASE(As1, Bs1, As2, Bs2, la1, lb1, st + 1)
+        }
     }
-    // An odd stage count ends with one more stage in buffer 0 (a separate copy: leaving the
-    // loop between its two phases costs the register allocator the fragment double buffer).
-    if (st < nst) {
-        FT_DMA_PHASE(As0, Bs0, As1, Bs1, la0, lb0, st)
-    }
+#undef FT_RING_PHASE
 #undef FT_DMA_PHASE
     // The workgroup's LDS must not be released with a DMA still writing it.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -533,7 +565,9 @@ __global__ __launch_bounds__(256, 2) void half_gemm_dma128(HalfGemmParams p) {
 
 // 64x128 split-k tiles for m of at most 64 (a 128-row tile would stage and multiply 64 rows of
 // clamped copies): waves of 32x64, row-major a.  Measured on MI355X, 64x4096x4096 bf16 at 8
-// splits: 6.7 us for the GEMM kernel against 8.0 us on the 128x128 split tile.
+// splits: 6.7 us for the GEMM kernel against 8.0 us on the 128x128 split tile.  Three stage
+// buffers (72 KiB, still two workgroups per CU), each stage's DMAs issued two stages ahead:
+// 12.2 / 11.6 us per step with row- / column-major b against 12.8 / 12.3 with two.
 template <bool BF16, bool TB>
 __global__ __launch_bounds__(256, 2) void half_gemm_dma64x128(HalfGemmParams p) {
     int bid = blockIdx.x, z = blockIdx.z;
@@ -545,7 +579,7 @@ __global__ __launch_bounds__(256, 2) void half_gemm_dma64x128(HalfGemmParams p) 
         const int t   = w - z * tiles, per = tiles >> 3;
         bid           = t < (per << 3) ? ((t % per) << 3) + t / per : t;
     }
-    half_gemm_dma_tile<BF16, false, TB, 128, true, 64>(p, bid, z);
+    half_gemm_dma_tile<BF16, false, TB, 128, true, 64, 0, 3>(p, bid, z);
 }
 
 // Grouped GEMM over a device table of per-group parameters: the workgroup's

@@ -204,14 +204,18 @@ def matrix(t: Optional[torch.Tensor], shape: Optional[Sequence[int]] = None, **k
     """Device matrix view over a tensor (or a null-memory view of `shape`).
 
     A contiguous tensor gets FTRAIN_INDEX_TYPE_CONTINUOUS; a non-contiguous
-    one (a transpose, a column slice) its explicit element strides.  The
-    numeric type follows the tensor's dtype unless given."""
+    one (a transpose, a column slice) its explicit element strides, also when
+    `shape` repeats its shape.  The numeric type follows the tensor's dtype
+    unless given."""
     if t is None:
         return View(None, list(shape), **kw)
     if "numeric_type" not in kw:
         kw["numeric_type"] = TORCH_NUMERIC_TYPES.get(t.dtype, FP32)
-    if not t.is_contiguous() and shape is None and "index_type" not in kw and "strides" not in kw:
+    same_shape = shape is None or list(shape) == list(t.shape)
+    if not t.is_contiguous() and same_shape and "index_type" not in kw and "strides" not in kw:
         return View(t.data_ptr(), list(t.shape), index_type=INDEX_INVALID, strides=list(t.stride()), **kw)
+    if not t.is_contiguous() and not same_shape:
+        raise ValueError(f"a non-contiguous tensor of shape {list(t.shape)} viewed as {list(shape)}")
     return View(t.data_ptr(), list(shape) if shape is not None else list(t.shape), **kw)
 
 

@@ -164,6 +164,50 @@ def test_half_dma_64_row_split_tile(capi, ops, oracle, kind, cd, la, lb, m, n, k
     assert (tile in names) == (not la), names
 
 
+@pytest.mark.parametrize("kind", ["bf16", "fp16"])
+@pytest.mark.parametrize("tb", [False, True], ids=["b_row", "b_col"])
+@pytest.mark.parametrize("k,splits", [(256, 4), (512, 4), (768, 4), (1024, 4), (1280, 4), (1800, 4), (264, 4),
+                                      (200, 2), (4096, 8)])
+def test_half_64_row_split_tile_at_forced_split_counts(capi, oracle, kind, tb, k, splits):
+    """The 64x128 split tile runs a ring of three stage buffers.  Split counts forced through the test
+    hook give split ranges of 1, 2, 3, 4, 5 and 8 whole stages (every way out of the ring's
+    three-stage loop) and, with a k tail, a last split of 4 stages + 8 k, 1 stage + 8 k or only 8 k
+    (264 = 128 + 128 + 8).  Against fp64, d inside a 7.0-filled store, bit-identical over repeats."""
+    t = capi.testing_lib()
+    ops = capi.GemmOps(l=t)
+    m, n = 64, 392
+    g = np.random.default_rng(k * 3 + splits)
+    a = rounded(g.standard_normal((m, k)).astype(np.float32), kind)
+    b = rounded(g.standard_normal((k, n)).astype(np.float32), kind)
+    c = g.standard_normal((m, n)).astype(np.float32)
+    ref = oracle.gemm_f64(a, b, c, 0.5, -1.25)
+    av, _ = placed(a, DT[kind], False, 8)
+    bv, _ = placed(b, DT[kind], tb, 8)
+    cv, _ = placed(c, torch.float32, False, 4)
+    dv, dstore = placed(np.zeros((m, n), np.float32), torch.float32, False, 4, fill=7.0)
+    keep = torch.ones_like(dstore, dtype=torch.bool)
+    keep[:, :n] = False
+    name = f"{kind.capitalize()}MfmaGemm_64x128_Dma_SplitK"
+    try:
+        t.ftrainTestingForceSplits(splits)
+        plan = capi.plan_for(av, bv, cv, dv, 0.5, -1.25, ops)
+        assert name in plan.names(), plan.names()
+        i = plan.names().index(name)
+        outs = []
+        for _ in range(3):
+            dv.fill_(float("nan"))
+            plan.execute(i, torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            outs.append(dv.clone())
+            assert torch.all(dstore[keep] == 7.0), "wrote outside d"
+        rep = oracle.tolerance_check(outs[0].cpu().numpy(), ref, k)
+        assert rep["ok"], (kind, tb, k, splits, rep)
+        assert all(torch.equal(outs[0], o) for o in outs[1:])
+        plan.close()
+    finally:
+        t.ftrainTestingForceSplits(0)
+
+
 @pytest.mark.parametrize("cd", ["fp32", "same"])
 def test_half_split_k_wide_reduction(capi, ops, oracle, cd):
     # 384x4096 outputs at k = 4096: the split-k tile's reduction runs one thread per output unit
