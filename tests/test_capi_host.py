@@ -863,3 +863,19 @@ def test_concurrent_plan_creation_agrees(tlib, tops):
     for t in threads:
         t.join()
     assert len(set(results)) == 1 and results[0][0] == c.SUCCESS
+
+
+def test_matrix_view_keeps_the_strides_of_a_padded_tensor():
+    # A non-contiguous tensor keeps its element strides also when the caller repeats its shape (the
+    # c argument of plan_for); a different shape for such a tensor is refused rather than read as
+    # contiguous.
+    torch = pytest.importorskip("torch")
+    padded = torch.zeros(4, 10)[:, :6]
+    for v in (c.matrix(padded), c.matrix(padded, [4, 6])):
+        assert v.sv.index_type == c.INDEX_INVALID
+        assert [v.sv.strides[i] for i in range(2)] == [10, 1]
+        assert [v.sv.dims[i] for i in range(2)] == [4, 6]
+    with pytest.raises(ValueError):
+        c.matrix(padded, [6, 4])
+    dense = c.matrix(torch.zeros(4, 6), [4, 6])
+    assert dense.sv.index_type == c.INDEX_CONTINUOUS and not dense.sv.strides
