@@ -166,8 +166,13 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
                            tails * kDmaTailMicros;
     // A launch with fewer workgroups than CUs streams memory through only that many of them (a CU
     // moves a bounded number of bytes per clock): 64x4096x14336 bf16 on the 64x128 split tile took
-    // 36.3 us at 4 splits (128 workgroups) against 23.8 us at 8.
-    const double fill = std::min(1.0, double(wgs) / double(cus));
+    // 36.3 us at 4 splits (128 workgroups) against 23.8 us at 8.  On the 16-bit 64x128 split tile
+    // (m of at most 64) 85% of the CUs already stream at the full rate: 32x14336x4096 22.5 us at 2
+    // splits (224 workgroups) against 24.1 at 4, and 5-10% the same way at 4 to 64 rows of n 13824
+    // and 14336; the 128x128 split tile at such counts lost 4-15%, so it keeps the plain fraction.
+    const bool half_64x128 = vi.input != FTRAIN_NUMERIC_TYPE_FP32 && vi.bm == 64 && vi.bn == 128 &&
+                             vi.split == SplitKind::kPartial;
+    const double fill = std::min(1.0, double(wgs) / (double(cus) * (half_64x128 ? 0.85 : 1.0)));
     // When memory bounds several variants alike, the one with the least compute overlaps it best
     // (64x14336x4096 bf16 at 4 splits: the 64x128 DMA split tile 25.9 us, the 128x128 one 27.6,
     // the register-staged 128x128 30.2): a thousandth of the compute time breaks such ties.

@@ -663,11 +663,13 @@ def test_finder_choices_for_16_bit_tiles(tlib):
         assert rank(tlib, *shape, ab_type=c.BF16)[0] == "Bf16MfmaGemm_128x128_Dma_SplitK", shape
     # One tile row: the 64x128 DMA split tile, at the split count measured fastest (after a warm
     # clock, forced split counts, us): 64x4096x4096 12.7 at 8 splits (128x128 split tile 13.5),
-    # 64x4096x14336 23.8 at 8 (25.4), 64x14336x4096 26.2 at 4 (26.8; the register-staged split
-    # tile 30.2); 4 splits of 64x4096x14336 (128 workgroups) took 36.3.
+    # 64x4096x14336 23.8 at 8 (25.4), 64x14336x4096 23.7 at 2 (26.3 at 4; 224 workgroups, 85% of the
+    # CUs, already stream at the full rate), 32x14336x4096 22.8 at 2 (24.3 at 4); 4 splits of
+    # 64x4096x14336 (128 workgroups) took 36.3.
     tile64 = "Bf16MfmaGemm_64x128_Dma_SplitK"
     names = {tlib.ftrainTestingVariantName(i).decode(): i for i in range(tlib.ftrainTestingVariantCount())}
-    for shape, splits in (((64, 4096, 4096), 8), ((64, 4096, 14336), 8), ((64, 14336, 4096), 4)):
+    for shape, splits in (((64, 4096, 4096), 8), ((64, 4096, 14336), 8), ((64, 14336, 4096), 2),
+                          ((32, 14336, 4096), 2)):
         assert rank(tlib, *shape, ab_type=c.BF16)[0] == tile64, shape
         assert tlib.ftrainTestingChooseSplits(names[tile64], *shape, 256) == splits, shape
     # k not a multiple of 64: the DMA tiles stage the partial last stage and still lead (bf16, us:
