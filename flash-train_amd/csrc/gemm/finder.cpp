@@ -173,10 +173,20 @@ double modelMicros(const VariantInfo& vi, const GemmShape& s, bool has_c, int cu
     const bool half_64x128 = vi.input != FTRAIN_NUMERIC_TYPE_FP32 && vi.bm == 64 && vi.bn == 128 &&
                              vi.split == SplitKind::kPartial;
     const double fill = std::min(1.0, double(wgs) / (double(cus) * (half_64x128 ? 0.85 : 1.0)));
+    double memory     = bytes / (kHbmBytesPerMicro * fill);
+    // A whole-k launch of at most half as many workgroups as CUs is bound by what each workgroup
+    // loads at one CU's rate, not by a fraction of HBM: bf16 128x4096x1024 on the 128x128 DMA
+    // tile (32 workgroups of 0.5 MiB) 9.3 us against 13.2 for the split tile the fraction picked,
+    // 128x256x512 6.5 against 10.7 for the 64x64 unaligned tile.  At 224 workgroups (4x28672x4096)
+    // the fraction still ranks right.
+    if (vi.split == SplitKind::kNone && !vi.simt && 2 * wgs <= uint64_t(cus)) {
+        const double wg_bytes = eb * double(vi.bm + vi.bn) * double(s.k) + 4.0 * vi.bm * vi.bn;
+        memory = std::max(bytes / kHbmBytesPerMicro, wg_bytes / kCuBytesPerMicro);
+    }
     // When memory bounds several variants alike, the one with the least compute overlaps it best
     // (64x14336x4096 bf16 at 4 splits: the 64x128 DMA split tile 25.9 us, the 128x128 one 27.6,
     // the register-staged 128x128 30.2): a thousandth of the compute time breaks such ties.
-    return std::max(compute, bytes / (kHbmBytesPerMicro * fill)) + serial_us + launch + kTieWeight * compute;
+    return std::max(compute, memory) + serial_us + launch + kTieWeight * compute;
 }
 
 }  // namespace

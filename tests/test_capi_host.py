@@ -657,6 +657,11 @@ def test_finder_choices_for_16_bit_tiles(tlib):
     # 39.1); large ones: the 256x256 DMA tile (8192^3 871 against 128x128 DMA 906); deep k: the
     # 128x128 DMA split-k tile (256x256x65536 21.2 against the register-staged split-k 29.3).
     assert rank(tlib, 2048, 2048, 2048, ab_type=c.BF16)[0] == "Bf16MfmaGemm_128x128_Dma"
+    # Few whole-k workgroups, each bound by its own CU's load rate: 128x4096x1024 9.3 us against 13.2
+    # for the split tile, 4096x128x1024 9.5 against 13.4, 128x256x512 6.5 against 10.7 for the 64x64
+    # unaligned tile.
+    for shape in ((128, 4096, 1024), (4096, 128, 1024), (128, 256, 512)):
+        assert rank(tlib, *shape, ab_type=c.BF16)[0] == "Bf16MfmaGemm_128x128_Dma", shape
     assert rank(tlib, 8192, 8192, 8192, ab_type=c.BF16)[0] == "Bf16MfmaGemm_256x256_Dma"
     assert rank(tlib, 16384, 14336, 4096, ab_type=c.BF16)[0] == "Bf16MfmaGemm_256x256_Dma"
     for shape in ((256, 256, 65536), (384, 4096, 4096), (1536, 1536, 8192)):
